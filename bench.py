@@ -1,0 +1,279 @@
+#!/usr/bin/env python3
+"""Benchmark of the SparseWave hot path on one MI355X.
+
+Headline: CSR SpMV fp32/i32 on the 1,048,576-row lognormal matrix
+(configuration 2), reported as achieved HBM GB/s of algorithmic bytes
+(4(n+1) + 8 nnz + 4 m + 4 n per SpMV) and GFLOP/s (2 nnz), for the fastest
+mapping.  Every mapping, CSR SpMM (K = 4, 64), BSR SpMM (fp32, bf16) and the
+sparse-attention chain are measured on the same run and reported under
+"workloads".  A step is one call of the C ABI over one resident batch.
+
+Timing: W untimed warmup steps, then K timed steps between HIP events on
+the stream the kernels run on, with a device synchronize on both sides.
+The CPU baseline is the oracle's scalar restatement of the reference's
+host SpMV loop, timed on this host's cores on a bounded sample.
+
+Prints one JSON line.  --gpus N > 1 exits: this build measures one GPU.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+FP32_MFMA_PEAK_TFLOPS = 157.3
+BF16_MFMA_PEAK_TFLOPS = 2500.0
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--only-headline", action="store_true",
+                    help="measure the headline SpMV mappings only")
+    ap.add_argument("--no-cpu", action="store_true",
+                    help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    return ap.parse_args()
+
+
+def time_steps(fn, steps, warmup):
+    """Mean ms per step of `fn` over `steps` calls, HIP events on the
+    current stream (the stream the C ABI launches on)."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record(st)
+    for _ in range(steps):
+        fn()
+    b.record(st)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / steps
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU; every GPU "
+                          "box has one MI355X, so --gpus must be 1"}))
+        sys.exit(2)
+    import torch
+    import sparsewavecomp_amd as sw
+    from sparsewavecomp_amd import workloads as W
+
+    sw.load_library()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    def T(a, dtype=None):
+        x = torch.from_numpy(np.ascontiguousarray(a))
+        if dtype is not None:
+            x = x.to(dtype)
+        return x.to(dev)
+
+    K, Wm = args.steps, args.warmup
+    workloads = {}
+
+    # ---- configuration 2: CSR SpMV -----------------------------------------
+    log("generating configuration 2 (1,048,576 rows, lognormal)")
+    t0 = time.time()
+    csr, x = W.config2(seed=0)
+    log(f"  nnz={csr.nnz} in {time.time() - t0:.1f}s")
+    n, m, nnz = csr.rows, csr.cols, csr.nnz
+    ro, col, val, xv = (T(csr.row_offsets), T(csr.column_indices),
+                        T(csr.values), T(x))
+    y = torch.empty(n, device=dev)
+    spmv_bytes = W.algorithmic_bytes_spmv(n, m, nnz)
+    spmv_flops = 2 * nnz
+    mappings = [
+        "spmv-mapping=wave-per-position spmv-positions-per-lane=8",
+        "spmv-mapping=wave-per-position spmv-positions-per-lane=4",
+        "spmv-mapping=wave-per-position spmv-positions-per-lane=16",
+        "spmv-mapping=wave-per-row spmv-lanes-per-row=8",
+        "spmv-mapping=wave-per-row spmv-lanes-per-row=16",
+        "spmv-mapping=wave-per-row",
+        "spmv-mapping=thread-per-row",
+        "spmv-mapping=block-per-row spmv-block-size=128",
+        "spmv-mapping=wave-per-position",
+    ]
+    if args.only_headline:
+        mappings = mappings[:4]
+    spmv_results = {}
+    for opts in mappings:
+        o = sw.Options.parse(opts)
+        log(f"SpMV {opts}")
+        ms = time_steps(lambda: sw.spmv(ro, col, val, xv, y, options=o), K, Wm)
+        spmv_results[opts] = {
+            "ms": ms, "GB/s": spmv_bytes / ms / 1e6,
+            "GFLOP/s": spmv_flops / ms / 1e6,
+            "hbm_frac": spmv_bytes / ms / 1e6 / HBM_PEAK_GBS}
+        log(f"  {ms * 1e3:.1f} us  {spmv_bytes / ms / 1e6:.0f} GB/s")
+    best = min(spmv_results, key=lambda k: spmv_results[k]["ms"])
+    workloads["spmv_config2"] = {"bytes": spmv_bytes, "flops": spmv_flops,
+                                 "best": best, "mappings": spmv_results}
+
+    if not args.only_headline:
+        # ---- configuration 1: the reference's CPU-runnable case ------------
+        c1, x1 = W.config1(seed=0)
+        r1 = (T(c1.row_offsets), T(c1.column_indices), T(c1.values), T(x1))
+        y1 = torch.empty(c1.rows, device=dev)
+        res1 = {}
+        for opts in ["spmv-mapping=thread-per-row",
+                     "spmv-mapping=wave-per-row spmv-lanes-per-row=16"]:
+            o = sw.Options.parse(opts)
+            ms = time_steps(lambda: sw.spmv(*r1, y1, options=o), K, Wm)
+            res1[opts] = {"us": ms * 1e3}
+        workloads["spmv_config1"] = res1
+
+        # ---- configuration 3: CSR SpMM K = 4 and 64 -------------------------
+        for k, opts in [(4, "spmm-mapping=wave-per-row-tile spmm-tile-size=4 "
+                            "spmm-lanes-per-row=16"),
+                        (4, "spmm-mapping=wave-per-row-tile spmm-tile-size=4"),
+                        (64, "spmm-mapping=wave-per-row-tile "
+                             "spmm-tile-size=32 spmm-lanes-per-row=16"),
+                        (64, "spmm-mapping=wave-per-row-tile "
+                             "spmm-tile-size=32 spmm-lanes-per-row=64")]:
+            rhs = T(W.config3_rhs(m, k, seed=0))
+            out = torch.empty((n, k), device=dev)
+            o = sw.Options.parse(opts)
+            log(f"SpMM K={k} {opts}")
+            ms = time_steps(lambda: sw.spmm(ro, col, val, rhs, out, options=o),
+                            max(K // 2, 1), Wm)
+            b = W.algorithmic_bytes_spmm(n, m, nnz, k)
+            workloads.setdefault(f"spmm_config3_k{k}", {})[opts] = {
+                "ms": ms, "GB/s": b / ms / 1e6,
+                "GFLOP/s": 2 * nnz * k / ms / 1e6,
+                "hbm_frac": b / ms / 1e6 / HBM_PEAK_GBS}
+            log(f"  {ms * 1e3:.1f} us  {b / ms / 1e6:.0f} GB/s")
+            del rhs, out
+        del ro, col, val, xv, y
+        torch.cuda.empty_cache()
+
+        # ---- configuration 4: BSR SpMM fp32 and bf16 ------------------------
+        log("generating configuration 4 (BSR 262,144, b=16)")
+        bsr, rhs4 = W.config4(seed=0)
+        flops4 = 2 * bsr.nnzb * 16 * 16 * 128
+        for bf16 in (False, True):
+            dt = torch.bfloat16 if bf16 else None
+            args4 = (T(bsr.block_row_offsets), T(bsr.block_column_indices),
+                     T(bsr.block_values, dt), T(rhs4, dt))
+            out4 = torch.empty((bsr.rows, 128), device=dev)
+            o = sw.Options(bsr_use_mfma=1)
+            log(f"BSR SpMM {'bf16' if bf16 else 'fp32'}")
+            ms = time_steps(lambda: sw.bsr_spmm(*args4, out4, 16, options=o),
+                            K, Wm)
+            b = W.algorithmic_bytes_bsr(bsr.rows, bsr.cols, bsr.nnzb, 16, 128,
+                                        2 if bf16 else 4)
+            peak = BF16_MFMA_PEAK_TFLOPS if bf16 else FP32_MFMA_PEAK_TFLOPS
+            tf = flops4 / ms / 1e9
+            # ceiling = min(MFMA peak, HBM peak x arithmetic intensity)
+            ceiling = min(peak, HBM_PEAK_GBS / 1e3 * flops4 / b)
+            workloads[f"bsr_config4_{'bf16' if bf16 else 'fp32'}"] = {
+                "ms": ms, "TFLOP/s": tf, "mfma_frac": tf / peak,
+                "GB/s": b / ms / 1e6, "hbm_frac": b / ms / 1e6 / HBM_PEAK_GBS,
+                "roofline_ceiling_TFLOP/s": ceiling,
+                "roofline_frac": tf / ceiling}
+            log(f"  {ms * 1e3:.1f} us  {tf:.1f} TFLOP/s")
+            del args4, out4
+        del bsr, rhs4
+
+        # ---- configuration 5: sparse attention ------------------------------
+        mask, q, kt, v, alpha = W.config5(seed=0)
+        att = (T(mask.row_offsets), T(mask.column_indices), T(mask.values),
+               T(q), T(kt), T(v))
+        scores = torch.empty(mask.nnz, device=dev)
+        rmax = torch.empty(mask.rows, device=dev)
+        rsum = torch.empty(mask.rows, device=dev)
+        outa = torch.empty((mask.rows, 64), device=dev)
+        for opts in ["", "sddmm-lanes-per-row=64 spmm-mapping="
+                         "wave-per-row-tile spmm-tile-size=32 "
+                         "spmm-lanes-per-row=16"]:
+            o = sw.Options.parse(opts)
+            log(f"attention '{opts}'")
+            ms = time_steps(lambda: sw.sparse_attention(
+                *att, scores, rmax, rsum, outa, alpha, 0.0, options=o), K, Wm)
+            workloads.setdefault("attention_config5", {})[
+                opts or "reference defaults"] = {
+                "ms": ms, "GFLOP/s": 4 * mask.nnz * 64 / ms / 1e6}
+            log(f"  {ms * 1e3:.1f} us")
+
+    # ---- CPU baseline -------------------------------------------------------
+    cpu = None
+    if not args.no_cpu:
+        import oracle
+        oracle.build()
+        log("CPU baseline (oracle, 1 thread)")
+        reps, t0 = 0, time.time()
+        while time.time() - t0 < args.cpu_seconds or reps == 0:
+            oracle.spmv(csr.row_offsets, csr.column_indices, csr.values, x)
+            reps += 1
+        dt = (time.time() - t0) / reps
+        cpu = {"value": spmv_bytes / dt / 1e9, "unit": "GB/s", "cores": 1,
+               "kind": "port",
+               "sample": f"{reps} full configuration-2 SpMV passes "
+                         f"({dt * 1e3:.1f} ms each) of oracle/sw_oracle.c, "
+                         "the scalar restatement of "
+                         "benchmark/SparseBenchmarkUtils.cpp:211-229"}
+        reps_mt, t0 = 0, time.time()
+        while time.time() - t0 < args.cpu_seconds / 2 or reps_mt == 0:
+            oracle.spmv(csr.row_offsets, csr.column_indices, csr.values, x,
+                        threads=True)
+            reps_mt += 1
+        dtm = (time.time() - t0) / reps_mt
+        cpu["all_cores_extra"] = {"GB/s": spmv_bytes / dtm / 1e9,
+                                  "threads": oracle.num_threads()}
+
+    head = workloads["spmv_config2"]["mappings"][best]
+    gbs = head["GB/s"]
+    line = {
+        "metric": "SpMV/SpMM achieved HBM GB/s (% of peak) + GFLOP/s on "
+                  "1M-row CSR",
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": Wm,
+        "ms_per_step": head["ms"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic (seeded numpy generator, configuration 2)",
+        "config": {
+            "workload": "CSR SpMV fp32/i32 1,048,576 x 1,048,576, lognormal "
+                        "row lengths E=32 sigma=1.5 clip [1,4096], seed 0",
+            "rows": n, "nnz": nnz, "mapping": best,
+            "GFLOP/s": round(head["GFLOP/s"], 2),
+            "hbm_frac": round(head["hbm_frac"], 4),
+        },
+        "roofline": {
+            "bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "traffic": None,
+        },
+        "cpu_baseline": cpu,
+        "workloads": workloads,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,232 @@
+/*
+ * sparsewave_amd.h -- C ABI of the MI355X (gfx950, Wave64) SparseWave hot path.
+ *
+ * Plain pointers and sizes only.  Every pointer argument is a device pointer
+ * (hipMalloc / torch CUDA tensor memory) unless stated otherwise; the caller
+ * owns every buffer, outputs included.  All work is enqueued on `stream`
+ * (a hipStream_t passed as void*, NULL = the default stream) with no host
+ * synchronisation and no allocation.  Functions return SW_OK (0) or a
+ * negative SW_ERR_* code; sw_last_error() then returns a message that
+ * paraphrases the reference's diagnostic.  Index arrays are i32, values f32
+ * (bf16 where the name says so).
+ *
+ * Citations are path:line into the reference (sott0n/SparseWaveComp).
+ */
+#ifndef SPARSEWAVE_AMD_H
+#define SPARSEWAVE_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SW_OK 0
+#define SW_ERR_INVALID_OPTION (-1)   /* option value rejected */
+#define SW_ERR_INVALID_SHAPE (-2)    /* shapes inconsistent with the op */
+#define SW_ERR_INVALID_ARGUMENT (-3) /* null pointer, misaligned, bad kind */
+#define SW_ERR_HIP (-4)              /* a HIP runtime call failed */
+
+/*
+ * Lowering options.  Field names are the reference's option names with '-'
+ * replaced by '_' (sparsewave-to-amdgpu-pipeline,
+ * include/sparsewave/Target/AMDGPU/Pipelines.h:108-191, and
+ * convert-sparsewave-to-gpu,
+ * include/sparsewave/Dialect/SparseWave/Transforms/Passes.td:186-241).
+ * Defaults (sw_options_init) are the reference defaults except
+ * wavefront_size, which is 64 because gfx950 runs Wave64 only.
+ * The last block of fields is specific to this Wave64 build.
+ */
+typedef struct sw_options {
+  char spmv_mapping[32];            /* thread-per-row | wave-per-row | block-per-row |
+                                       thread-per-position | wave-per-position */
+  int64_t spmv_block_size;          /* 1..1024, default 256 */
+  int64_t spmv_position_chunk_size; /* thread-per-position chunk, default 1 */
+  char spmv_position_reduction[16]; /* atomic | segmented (thread-per-position) */
+  int64_t position_block_size;      /* position-parallel init kernels, default 256 */
+  char spmm_mapping[32];            /* thread-per-output | wave-per-row-tile |
+                                       thread-per-position */
+  int64_t spmm_block_size;          /* 1..1024, default 256 */
+  int64_t spmm_tile_size;           /* 1..32, default 4 */
+  int64_t spmm_position_chunk_size; /* default 1 */
+  int64_t sddmm_block_size;         /* default 256 */
+  int64_t row_reduction_block_size; /* default 256 */
+  int64_t rowwise_map_block_size;   /* default 256 */
+  int64_t elementwise_block_size;   /* default 256 (accepted, no op uses it) */
+  int64_t wavefront_size;           /* must be 64 */
+  /* Wave64 extensions (no reference counterpart). */
+  int64_t spmv_lanes_per_row;       /* wave-per-row: lanes per row group,
+                                       power of two 1..64, default 64 = one
+                                       wave per row */
+  int64_t spmv_positions_per_lane;  /* wave-per-position: consecutive
+                                       positions per lane 1,2,4,8,16;
+                                       default 1 = the reference schedule */
+  int64_t spmm_lanes_per_row;       /* wave-per-row-tile: lanes per (row,
+                                       tile) group, power of two, default 64 */
+  int64_t bsr_use_mfma;             /* BSR SpMM: 1 = MFMA tiles when the block
+                                       size allows it (default), 0 = the
+                                       thread-per-output kernel */
+  int64_t sddmm_lanes_per_row;      /* SDDMM: 1 = thread-per-row (reference,
+                                       default); 64 = one wave per row with
+                                       lanes split over the dot products */
+} sw_options;
+
+/* Fill `opts` with the defaults. */
+void sw_options_init(sw_options *opts);
+
+/* Set one option by its reference name, e.g. ("spmv-mapping",
+ * "wave-per-row") or ("spmv-block-size", "128").  Unknown names are
+ * SW_ERR_INVALID_OPTION.  Target options of the reference pipeline
+ * (chip, wavefront-size, rocm-path, ...) are accepted; chip must name
+ * gfx950. */
+int sw_options_set(sw_options *opts, const char *name, const char *value);
+
+/* Parse a reference pipeline option string: whitespace separated name=value
+ * pairs, optionally wrapped in the pass name and braces, e.g.
+ * "sparsewave-to-amdgpu-pipeline{chip=gfx950 spmv-mapping=wave-per-row}". */
+int sw_options_parse(sw_options *opts, const char *text);
+
+/* Check option values the way convert-sparsewave-to-gpu and
+ * schedule-sparsewave-position do
+ * (lib/Dialect/SparseWave/Transforms/SparseWaveToGPU.cpp:1265-1397,
+ *  lib/Dialect/SparseWave/Transforms/SparsePositionScheduling.cpp:411-465),
+ * with the Wave32 requirements restated for Wave64. */
+int sw_validate_options(const sw_options *opts);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char *sw_last_error(void);
+
+/* Library version string. */
+const char *sw_version(void);
+
+/*
+ * sparsewave.spmv: output[rows] = A * vector with A in CSR.
+ * Operands in op order (SparseWaveOps.td:17-52): row_offsets[rows+1],
+ * column_indices[nnz], values[nnz], vector[cols], output[rows].
+ * Replaces the kernels generated by ThreadPerRowSpMVPattern,
+ * WavePerRowSpMVPattern, BlockPerRowSpMVPattern (SparseWaveToGPU.cpp:216-487)
+ * and the position schedules (SparsePositionScheduling.cpp:135-403),
+ * selected by opts->spmv_mapping.  Row mappings overwrite output; position
+ * mappings zero it first (the reference's init kernel) then accumulate.
+ */
+int sw_spmv_csr_f32(const int32_t *row_offsets, const int32_t *column_indices,
+                    const float *values, const float *vector, float *output,
+                    int64_t rows, int64_t cols, int64_t nnz,
+                    const sw_options *opts, void *stream);
+
+/*
+ * sparsewave.spmm: output[rows][k] = A * rhs[cols][k], dense matrices
+ * row-major.  Operand order and the 5-buffer bundle ABI of
+ * SparseWaveOps.td:91-124 / tools/sparsewave-bundle/sparsewave_bundle_ir.py:11-17.
+ * Kernels of ThreadPerOutputSpMMPattern and WavePerRowTileSpMMPattern
+ * (SparseWaveToGPU.cpp:489-558, 1057-1256) and the thread-per-position
+ * schedule (PositionSpMMDecomposition.cpp:19-73).
+ */
+int sw_spmm_csr_f32(const int32_t *row_offsets, const int32_t *column_indices,
+                    const float *values, const float *rhs, float *output,
+                    int64_t rows, int64_t cols, int64_t nnz, int64_t k,
+                    const sw_options *opts, void *stream);
+
+/*
+ * sparsewave.bsr_spmm: output[rows][k] = A * rhs[cols][k], A in BSR with
+ * square block_size blocks stored row-major [nnzb][b][b]
+ * (SparseWaveOps.td:126-169; verifier SparseWaveOps.cpp:144-207,340-372;
+ * kernel ThreadPerOutputBSRSpMMPattern, SparseWaveToGPU.cpp:560-665).
+ * rows and cols must be divisible by block_size.
+ */
+int sw_bsr_spmm_f32(const int32_t *block_row_offsets,
+                    const int32_t *block_column_indices,
+                    const float *block_values, const float *rhs, float *output,
+                    int64_t rows, int64_t cols, int64_t nnzb, int64_t k,
+                    int64_t block_size, const sw_options *opts, void *stream);
+
+/* BSR SpMM with bf16 block values and bf16 rhs (raw bf16 bits as uint16),
+ * fp32 accumulation and fp32 output.  Same operands as sw_bsr_spmm_f32. */
+int sw_bsr_spmm_bf16(const int32_t *block_row_offsets,
+                     const int32_t *block_column_indices,
+                     const uint16_t *block_values, const uint16_t *rhs,
+                     float *output, int64_t rows, int64_t cols, int64_t nnzb,
+                     int64_t k, int64_t block_size, const sw_options *opts,
+                     void *stream);
+
+/* Scalar regions the reference attaches to sddmm
+ * (SparseWaveOps.td:171-223).  SW_SDDMM_AFFINE is the attention form
+ * sample*beta + dot*alpha (SparseAttentionToSparseWave.cpp:270-283). */
+#define SW_SDDMM_MUL 0    /* sample * dot */
+#define SW_SDDMM_AFFINE 1 /* sample * beta + dot * alpha */
+#define SW_SDDMM_DOT 2    /* dot */
+
+/*
+ * sparsewave.sddmm: output_values[p] = region(values[p], lhs[r,:] . rhs[:,c])
+ * for every stored (r, c) at position p.  lhs[rows][kdim], rhs[kdim][cols]
+ * row-major.  ThreadPerRowSDDMMPattern (SparseWaveToGPU.cpp:667-750).
+ */
+int sw_sddmm_csr_f32(const int32_t *row_offsets, const int32_t *column_indices,
+                     const float *values, const float *lhs, const float *rhs,
+                     float *output_values, int64_t rows, int64_t cols,
+                     int64_t nnz, int64_t kdim, int combine, float alpha,
+                     float beta, const sw_options *opts, void *stream);
+
+/*
+ * sparsewave.csr_row_reduce: output[r] = fold over row r's stored values.
+ * kind "sum" (identity 0) or "max" (identity -inf, NaN-propagating maximum)
+ * (SparseWaveOps.td:225-257; ThreadPerRowCSRRowReducePattern,
+ * SparseWaveToGPU.cpp:752-818).  column_indices may be NULL (unused).
+ */
+int sw_csr_row_reduce_f32(const int32_t *row_offsets,
+                          const int32_t *column_indices, const float *values,
+                          float *output, int64_t rows, int64_t nnz,
+                          const char *kind, const sw_options *opts,
+                          void *stream);
+
+/* Scalar regions of csr_rowwise_map (attention: exp-sub and div,
+ * SparseAttentionToSparseWave.cpp:288-309). */
+#define SW_MAP_EXP_SUB 0 /* exp(value - row_value) */
+#define SW_MAP_DIV 1     /* value / row_value */
+#define SW_MAP_SUB 2     /* value - row_value */
+#define SW_MAP_MUL 3     /* value * row_value */
+
+/*
+ * sparsewave.csr_rowwise_map: output_values[p] = f(values[p], row_values[r]).
+ * output_values may alias values (the attention chain maps in place).
+ * ThreadPerRowCSRRowwiseMapPattern (SparseWaveToGPU.cpp:820-878).
+ */
+int sw_csr_rowwise_map_f32(const int32_t *row_offsets,
+                           const int32_t *column_indices, const float *values,
+                           const float *row_values, float *output_values,
+                           int64_t rows, int64_t nnz, int map,
+                           const sw_options *opts, void *stream);
+
+/*
+ * The sparse-attention chain: the six ops of
+ * examples/pytorch/integration/SparseAttentionToSparseWave.cpp:230-315 in
+ * order -- scores = sddmm(affine alpha, beta), row_max, exp(s - max),
+ * row_sum, s / sum, output = scores * value.  Buffers follow the bundle's
+ * ten-buffer ABI (tools/sparsewave-bundle/sparsewave_bundle_ir.py:82-93):
+ * query[rows][d], transposed_key[d][cols], value[cols][dv],
+ * scores[nnz], row_maximum[rows], row_sum[rows], output[rows][dv].
+ */
+int sw_sparse_attention_f32(const int32_t *row_offsets,
+                            const int32_t *column_indices,
+                            const float *mask_values, const float *query,
+                            const float *transposed_key, const float *value,
+                            float *scores, float *row_maximum, float *row_sum,
+                            float *output, int64_t rows, int64_t cols,
+                            int64_t nnz, int64_t d, int64_t dv, float alpha,
+                            float beta, const sw_options *opts, void *stream);
+
+/*
+ * sparsewave.csr_row_at_position for a batch of positions:
+ * out_rows[i] = (first j in [1, rows+1) with row_offsets[j] > positions[i]) - 1,
+ * the row search of SparsePositionToSCF.cpp:225-271 that the position
+ * mappings run.  positions[i] must lie in [0, nnz).
+ */
+int sw_csr_row_at_position(const int32_t *row_offsets, int64_t rows,
+                           const int64_t *positions, int32_t *out_rows,
+                           int64_t count, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SPARSEWAVE_AMD_H */

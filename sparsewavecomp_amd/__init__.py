@@ -1,0 +1,346 @@
+"""sparsewavecomp_amd: the SparseWave sparse hot path on MI355X (gfx950).
+
+Python mirror of the op-level interface: each function takes the operands of
+the matching ``sparsewave`` op in the op's operand order
+(include/sparsewave/Dialect/SparseWave/IR/SparseWaveOps.td) as device
+tensors, plus lowering options under the reference's option names, and
+enqueues the hand-written HIP kernels of ``libsparsewave_amd.so`` through its
+C ABI (include/sparsewave_amd.h) on the current torch stream.
+
+Errors raise :class:`SparseWaveError` carrying the library's diagnostic.
+There is no CPU fallback: without the built library every call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+__all__ = [
+    "Options", "SparseWaveError", "library_path", "load_library", "spmv",
+    "spmm", "bsr_spmm", "sddmm", "csr_row_reduce", "csr_rowwise_map",
+    "sparse_attention", "csr_row_at_position", "SDDMM_MUL", "SDDMM_AFFINE",
+    "SDDMM_DOT", "MAP_EXP_SUB", "MAP_DIV", "MAP_SUB", "MAP_MUL",
+]
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_NAME = "libsparsewave_amd.so"
+
+SW_OK = 0
+SDDMM_MUL, SDDMM_AFFINE, SDDMM_DOT = 0, 1, 2
+MAP_EXP_SUB, MAP_DIV, MAP_SUB, MAP_MUL = 0, 1, 2, 3
+
+EXPORTED_SYMBOLS = (
+    "sw_options_init", "sw_options_set", "sw_options_parse",
+    "sw_validate_options", "sw_last_error", "sw_version", "sw_spmv_csr_f32",
+    "sw_spmm_csr_f32", "sw_bsr_spmm_f32", "sw_bsr_spmm_bf16",
+    "sw_sddmm_csr_f32", "sw_csr_row_reduce_f32", "sw_csr_rowwise_map_f32",
+    "sw_sparse_attention_f32", "sw_csr_row_at_position",
+)
+
+
+class SparseWaveError(RuntimeError):
+    """A C-ABI call returned a negative status."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(f"[{code}] {message}")
+        self.code = code
+        self.message = message
+
+
+class _COptions(ctypes.Structure):
+    _fields_ = [
+        ("spmv_mapping", ctypes.c_char * 32),
+        ("spmv_block_size", ctypes.c_int64),
+        ("spmv_position_chunk_size", ctypes.c_int64),
+        ("spmv_position_reduction", ctypes.c_char * 16),
+        ("position_block_size", ctypes.c_int64),
+        ("spmm_mapping", ctypes.c_char * 32),
+        ("spmm_block_size", ctypes.c_int64),
+        ("spmm_tile_size", ctypes.c_int64),
+        ("spmm_position_chunk_size", ctypes.c_int64),
+        ("sddmm_block_size", ctypes.c_int64),
+        ("row_reduction_block_size", ctypes.c_int64),
+        ("rowwise_map_block_size", ctypes.c_int64),
+        ("elementwise_block_size", ctypes.c_int64),
+        ("wavefront_size", ctypes.c_int64),
+        ("spmv_lanes_per_row", ctypes.c_int64),
+        ("spmv_positions_per_lane", ctypes.c_int64),
+        ("spmm_lanes_per_row", ctypes.c_int64),
+        ("bsr_use_mfma", ctypes.c_int64),
+        ("sddmm_lanes_per_row", ctypes.c_int64),
+    ]
+
+
+_lib = None
+
+
+def library_path() -> str:
+    return os.path.join(_HERE, _LIB_NAME)
+
+
+def load_library():
+    """Load the in-tree HIP library (built by sparsewavecomp_amd.build)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    path = library_path()
+    if not os.path.exists(path):
+        raise ImportError(
+            f"{path} is missing: build it with `python -m "
+            f"sparsewavecomp_amd.build` (hipcc, gfx950)")
+    lib = ctypes.CDLL(path)
+    P, I64, C = ctypes.c_void_p, ctypes.c_int64, ctypes.c_char_p
+    OP = ctypes.POINTER(_COptions)
+    F = ctypes.c_float
+    sig = {
+        "sw_options_init": (None, [OP]),
+        "sw_options_set": (ctypes.c_int, [OP, C, C]),
+        "sw_options_parse": (ctypes.c_int, [OP, C]),
+        "sw_validate_options": (ctypes.c_int, [OP]),
+        "sw_last_error": (C, []),
+        "sw_version": (C, []),
+        "sw_spmv_csr_f32": (ctypes.c_int, [P, P, P, P, P, I64, I64, I64, OP,
+                                           P]),
+        "sw_spmm_csr_f32": (ctypes.c_int, [P, P, P, P, P, I64, I64, I64, I64,
+                                           OP, P]),
+        "sw_bsr_spmm_f32": (ctypes.c_int, [P, P, P, P, P, I64, I64, I64, I64,
+                                           I64, OP, P]),
+        "sw_bsr_spmm_bf16": (ctypes.c_int, [P, P, P, P, P, I64, I64, I64, I64,
+                                            I64, OP, P]),
+        "sw_sddmm_csr_f32": (ctypes.c_int, [P, P, P, P, P, P, I64, I64, I64,
+                                            I64, ctypes.c_int, F, F, OP, P]),
+        "sw_csr_row_reduce_f32": (ctypes.c_int, [P, P, P, P, I64, I64, C, OP,
+                                                 P]),
+        "sw_csr_rowwise_map_f32": (ctypes.c_int, [P, P, P, P, P, I64, I64,
+                                                  ctypes.c_int, OP, P]),
+        "sw_sparse_attention_f32": (ctypes.c_int, [P, P, P, P, P, P, P, P, P,
+                                                   P, I64, I64, I64, I64, I64,
+                                                   F, F, OP, P]),
+        "sw_csr_row_at_position": (ctypes.c_int, [P, I64, P, P, I64, P]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def _check(rc: int):
+    if rc != SW_OK:
+        msg = load_library().sw_last_error().decode()
+        raise SparseWaveError(rc, msg)
+
+
+class Options:
+    """Lowering options under the reference's names.
+
+    ``Options(spmv_mapping="wave-per-row", spmv_block_size=128)`` or
+    ``Options.parse("spmv-mapping=wave-per-row spmv-block-size=128")``.
+    Keyword names are the option names with '-' replaced by '_'.
+    """
+
+    def __init__(self, **kwargs):
+        self._c = _COptions()
+        load_library().sw_options_init(ctypes.byref(self._c))
+        for key, value in kwargs.items():
+            self.set(key.replace("_", "-"), value)
+
+    @classmethod
+    def parse(cls, text: str) -> "Options":
+        o = cls()
+        _check(load_library().sw_options_parse(ctypes.byref(o._c),
+                                               text.encode()))
+        return o
+
+    def set(self, name: str, value) -> "Options":
+        _check(load_library().sw_options_set(ctypes.byref(self._c),
+                                             name.encode(),
+                                             str(value).encode()))
+        return self
+
+    def validate(self) -> "Options":
+        _check(load_library().sw_validate_options(ctypes.byref(self._c)))
+        return self
+
+    def __getattr__(self, item):
+        if item.startswith("_"):
+            raise AttributeError(item)
+        v = getattr(self._c, item)
+        return v.decode() if isinstance(v, bytes) else v
+
+    @property
+    def ref(self):
+        return ctypes.byref(self._c)
+
+    def __repr__(self):
+        fields = ", ".join(f"{n}={getattr(self, n)!r}"
+                           for n, _ in _COptions._fields_)
+        return f"Options({fields})"
+
+
+def _opts(options):
+    if options is None:
+        return None
+    if isinstance(options, str):
+        options = Options.parse(options)
+    return options.ref
+
+
+def _dev(t, dtype, name):
+    import torch
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must be a device tensor, got {t.device}")
+    if t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(stream):
+    import torch
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return ctypes.c_void_p(stream.cuda_stream)
+
+
+def spmv(row_offsets, column_indices, values, vector, output, options=None,
+         stream=None):
+    """sparsewave.spmv (SparseWaveOps.td:17-52): output = A @ vector."""
+    import torch
+    rows = row_offsets.numel() - 1
+    _check(load_library().sw_spmv_csr_f32(
+        _dev(row_offsets, torch.int32, "row_offsets"),
+        _dev(column_indices, torch.int32, "column_indices"),
+        _dev(values, torch.float32, "values"),
+        _dev(vector, torch.float32, "vector"),
+        _dev(output, torch.float32, "output"), rows, vector.numel(),
+        values.numel(), _opts(options), _stream(stream)))
+    return output
+
+
+def spmm(row_offsets, column_indices, values, rhs, output, options=None,
+         stream=None):
+    """sparsewave.spmm (SparseWaveOps.td:91-124): output = A @ rhs."""
+    import torch
+    rows = row_offsets.numel() - 1
+    if rhs.dim() != 2 or output.dim() != 2 or output.shape != (rows,
+                                                                 rhs.shape[1]):
+        raise ValueError("expected rhs [cols, k] and output [rows, k]")
+    _check(load_library().sw_spmm_csr_f32(
+        _dev(row_offsets, torch.int32, "row_offsets"),
+        _dev(column_indices, torch.int32, "column_indices"),
+        _dev(values, torch.float32, "values"),
+        _dev(rhs, torch.float32, "rhs"),
+        _dev(output, torch.float32, "output"), rows, rhs.shape[0],
+        values.numel(), rhs.shape[1], _opts(options), _stream(stream)))
+    return output
+
+
+def bsr_spmm(block_row_offsets, block_column_indices, block_values, rhs,
+             output, block_size, options=None, stream=None):
+    """sparsewave.bsr_spmm (SparseWaveOps.td:126-169); fp32 or bf16 inputs."""
+    import torch
+    rows = (block_row_offsets.numel() - 1) * block_size
+    if rhs.dim() != 2 or output.shape != (rows, rhs.shape[1]):
+        raise ValueError("expected rhs [cols, k] and output [rows, k]")
+    bf16 = block_values.dtype == torch.bfloat16
+    vdt = torch.bfloat16 if bf16 else torch.float32
+    fn = (load_library().sw_bsr_spmm_bf16 if bf16
+          else load_library().sw_bsr_spmm_f32)
+    nnzb = block_column_indices.numel()
+    _check(fn(_dev(block_row_offsets, torch.int32, "block_row_offsets"),
+              _dev(block_column_indices, torch.int32, "block_column_indices"),
+              _dev(block_values, vdt, "block_values"), _dev(rhs, vdt, "rhs"),
+              _dev(output, torch.float32, "output"), rows, rhs.shape[0], nnzb,
+              rhs.shape[1], block_size, _opts(options), _stream(stream)))
+    return output
+
+
+def sddmm(row_offsets, column_indices, values, lhs, rhs, output_values,
+          combine=SDDMM_MUL, alpha=1.0, beta=0.0, options=None, stream=None):
+    """sparsewave.sddmm (SparseWaveOps.td:171-223)."""
+    import torch
+    rows = row_offsets.numel() - 1
+    if lhs.dim() != 2 or rhs.dim() != 2 or lhs.shape[1] != rhs.shape[0]:
+        raise ValueError("expected lhs [rows, k] and rhs [k, cols]")
+    _check(load_library().sw_sddmm_csr_f32(
+        _dev(row_offsets, torch.int32, "row_offsets"),
+        _dev(column_indices, torch.int32, "column_indices"),
+        _dev(values, torch.float32, "values"),
+        _dev(lhs, torch.float32, "lhs"), _dev(rhs, torch.float32, "rhs"),
+        _dev(output_values, torch.float32, "output_values"), rows,
+        rhs.shape[1], column_indices.numel(), lhs.shape[1], combine, alpha,
+        beta, _opts(options), _stream(stream)))
+    return output_values
+
+
+def csr_row_reduce(row_offsets, column_indices, values, output, kind="sum",
+                   options=None, stream=None):
+    """sparsewave.csr_row_reduce (SparseWaveOps.td:225-257)."""
+    import torch
+    rows = row_offsets.numel() - 1
+    ci = (None if column_indices is None else
+          _dev(column_indices, torch.int32, "column_indices"))
+    _check(load_library().sw_csr_row_reduce_f32(
+        _dev(row_offsets, torch.int32, "row_offsets"), ci,
+        _dev(values, torch.float32, "values"),
+        _dev(output, torch.float32, "output"), rows, values.numel(),
+        kind.encode(), _opts(options), _stream(stream)))
+    return output
+
+
+def csr_rowwise_map(row_offsets, column_indices, values, row_values,
+                    output_values, kind=MAP_EXP_SUB, options=None,
+                    stream=None):
+    """sparsewave.csr_rowwise_map (SparseWaveOps.td:259-299)."""
+    import torch
+    rows = row_offsets.numel() - 1
+    ci = (None if column_indices is None else
+          _dev(column_indices, torch.int32, "column_indices"))
+    _check(load_library().sw_csr_rowwise_map_f32(
+        _dev(row_offsets, torch.int32, "row_offsets"), ci,
+        _dev(values, torch.float32, "values"),
+        _dev(row_values, torch.float32, "row_values"),
+        _dev(output_values, torch.float32, "output_values"), rows,
+        values.numel(), kind, _opts(options), _stream(stream)))
+    return output_values
+
+
+def sparse_attention(row_offsets, column_indices, mask_values, query,
+                     transposed_key, value, scores, row_maximum, row_sum,
+                     output, alpha, beta=0.0, options=None, stream=None):
+    """The six-op sparse attention chain
+    (SparseAttentionToSparseWave.cpp:230-315), ten-buffer ABI."""
+    import torch
+    rows = row_offsets.numel() - 1
+    d = query.shape[1]
+    dv = value.shape[1]
+    _check(load_library().sw_sparse_attention_f32(
+        _dev(row_offsets, torch.int32, "row_offsets"),
+        _dev(column_indices, torch.int32, "column_indices"),
+        _dev(mask_values, torch.float32, "mask_values"),
+        _dev(query, torch.float32, "query"),
+        _dev(transposed_key, torch.float32, "transposed_key"),
+        _dev(value, torch.float32, "value"),
+        _dev(scores, torch.float32, "scores"),
+        _dev(row_maximum, torch.float32, "row_maximum"),
+        _dev(row_sum, torch.float32, "row_sum"),
+        _dev(output, torch.float32, "output"), rows, transposed_key.shape[1],
+        column_indices.numel(), d, dv, alpha, beta, _opts(options),
+        _stream(stream)))
+    return output
+
+
+def csr_row_at_position(row_offsets, positions, out_rows, stream=None):
+    """sparsewave.csr_row_at_position for a batch (SparsePositionToSCF.cpp:225-271)."""
+    import torch
+    _check(load_library().sw_csr_row_at_position(
+        _dev(row_offsets, torch.int32, "row_offsets"),
+        row_offsets.numel() - 1, _dev(positions, torch.int64, "positions"),
+        _dev(out_rows, torch.int32, "out_rows"), positions.numel(),
+        _stream(stream)))
+    return out_rows

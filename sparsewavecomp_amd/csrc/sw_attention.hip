@@ -1,0 +1,422 @@
+// sparsewave.sddmm, csr_row_reduce, csr_rowwise_map and the six-kernel
+// sparse-attention chain on gfx950.
+//
+// Reference kernels (generated IR):
+//   sddmm            ThreadPerRowSDDMMPattern, SparseWaveToGPU.cpp:667-750
+//   csr_row_reduce   ThreadPerRowCSRRowReducePattern, SparseWaveToGPU.cpp:752-818
+//   csr_rowwise_map  ThreadPerRowCSRRowwiseMapPattern, SparseWaveToGPU.cpp:820-878
+//   attention chain  examples/pytorch/integration/SparseAttentionToSparseWave.cpp:230-315
+//
+// Each op has the reference's thread-per-row kernel and a Wave64 kernel that
+// gives a row to a wave (lanes over positions: coalesced CSR reads and, for
+// SDDMM, coalesced reads of the dense right-hand side when a row's columns
+// are contiguous, as in block masks).
+#include "sw_device.h"
+#include "sw_internal.h"
+
+#include <algorithm>
+#include <cmath>
+
+using namespace swd;
+
+namespace sw {
+int launch_spmm(const int32_t *ro, const int32_t *col, const float *val,
+                const float *rhs, float *out, int64_t rows, int64_t nnz,
+                int64_t k, const sw_options &o, const char *what,
+                hipStream_t st);
+}
+
+namespace {
+
+__device__ __forceinline__ float combine_sddmm(int kind, float sample,
+                                               float dot, float alpha,
+                                               float beta) {
+  if (kind == SW_SDDMM_MUL)
+    return sample * dot;
+  if (kind == SW_SDDMM_AFFINE)
+    return sample * beta + dot * alpha;
+  return dot;
+}
+
+// arith.maximumf: NaN propagates, +0 is above -0.
+__device__ __forceinline__ float maximumf(float a, float b) {
+  if (a != a || b != b)
+    return __builtin_nanf("");
+  if (a == b)
+    return __float_as_int(a) < 0 ? b : a;
+  return a > b ? a : b;
+}
+
+__device__ __forceinline__ float map_value(int kind, float v, float rv) {
+  switch (kind) {
+  case SW_MAP_EXP_SUB:
+    return expf(v - rv);
+  case SW_MAP_DIV:
+    return v / rv;
+  case SW_MAP_SUB:
+    return v - rv;
+  default:
+    return v * rv;
+  }
+}
+
+// ---- SDDMM -----------------------------------------------------------------
+__global__ __launch_bounds__(1024) void sddmm_thread_per_row(
+    const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
+    const float *__restrict__ val, const float *__restrict__ lhs,
+    const float *__restrict__ rhs, float *__restrict__ out, int32_t rows,
+    int64_t cols, int32_t kdim, int kind, float alpha, float beta) {
+  int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows)
+    return;
+  const float *a = lhs + r * kdim;
+  for (int32_t p = ro[r]; p < ro[r + 1]; ++p) {
+    int64_t c = col[p];
+    float dot = 0.0f;
+    for (int32_t i = 0; i < kdim; ++i)
+      dot = __builtin_fmaf(a[i], rhs[(int64_t)i * cols + c], dot);
+    out[p] = combine_sddmm(kind, val != nullptr ? val[p] : 0.0f, dot, alpha,
+                           beta);
+  }
+}
+
+// One wave per row; lane l computes the dot products of positions
+// start+l, start+l+64, ...; the row of lhs is held 64 values at a time, one
+// per lane, and broadcast with v_readlane.
+__global__ __launch_bounds__(256) void sddmm_wave_per_row(
+    const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
+    const float *__restrict__ val, const float *__restrict__ lhs,
+    const float *__restrict__ rhs, float *__restrict__ out, int32_t rows,
+    int64_t cols, int32_t kdim, int kind, float alpha, float beta) {
+  const int64_t r = (int64_t)blockIdx.x * (blockDim.x / kWave) +
+                    threadIdx.x / kWave;
+  if (r >= rows)
+    return; // wave-uniform
+  const int l = lane_id();
+  const int32_t s = ro[r], e = ro[r + 1];
+  const float *a = lhs + r * kdim;
+  for (int32_t p0 = s; p0 < e; p0 += 4 * kWave) {
+    float dot[4] = {0.f, 0.f, 0.f, 0.f};
+    int64_t c[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      int32_t p = p0 + j * kWave + l;
+      c[j] = p < e ? (int64_t)col[p] : 0;
+    }
+    for (int32_t i0 = 0; i0 < kdim; i0 += kWave) {
+      const float mine = (i0 + l < kdim) ? a[i0 + l] : 0.0f;
+      const int n = std::min<int32_t>(kWave, kdim - i0);
+      for (int t = 0; t < n; ++t) {
+        const float av =
+            __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), t));
+        const float *rrow = rhs + (int64_t)(i0 + t) * cols;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          dot[j] = __builtin_fmaf(av, rrow[c[j]], dot[j]);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      int32_t p = p0 + j * kWave + l;
+      if (p < e)
+        out[p] = combine_sddmm(kind, val != nullptr ? val[p] : 0.0f, dot[j],
+                               alpha, beta);
+    }
+  }
+}
+
+// ---- row reduce ----------------------------------------------------------
+template <bool MAX>
+__global__ __launch_bounds__(1024) void row_reduce_thread(
+    const int32_t *__restrict__ ro, const float *__restrict__ val,
+    float *__restrict__ out, int32_t rows) {
+  int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows)
+    return;
+  float acc = MAX ? -INFINITY : 0.0f;
+  for (int32_t p = ro[r]; p < ro[r + 1]; ++p)
+    acc = MAX ? maximumf(acc, val[p]) : acc + val[p];
+  out[r] = acc;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+  v = maximumf(v, dpp_f<kQuadXor1>(-INFINITY, v));
+  v = maximumf(v, dpp_f<kQuadXor2>(-INFINITY, v));
+  v = maximumf(v, dpp_f<kRowHalfMirror>(-INFINITY, v));
+  v = maximumf(v, dpp_f<kRowMirror>(-INFINITY, v));
+  v = maximumf(v, swizzle_xor16(v));
+  v = maximumf(v, shfl_xor32(v));
+  return v;
+}
+
+template <bool MAX>
+__global__ __launch_bounds__(256) void row_reduce_wave(
+    const int32_t *__restrict__ ro, const float *__restrict__ val,
+    float *__restrict__ out, int32_t rows) {
+  const int64_t r = (int64_t)blockIdx.x * (blockDim.x / kWave) +
+                    threadIdx.x / kWave;
+  if (r >= rows)
+    return;
+  const int l = lane_id();
+  float acc = MAX ? -INFINITY : 0.0f;
+  for (int32_t p = ro[r] + l; p < ro[r + 1]; p += kWave)
+    acc = MAX ? maximumf(acc, val[p]) : acc + val[p];
+  acc = MAX ? wave_max(acc) : group_sum<kWave>(acc);
+  if (l == 0)
+    out[r] = acc;
+}
+
+// ---- row-wise map ----------------------------------------------------------
+__global__ __launch_bounds__(1024) void rowwise_map_thread(
+    const int32_t *__restrict__ ro, const float *val,
+    const float *__restrict__ rowv, float *out, int32_t rows, int kind) {
+  int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows)
+    return;
+  const float rv = rowv[r];
+  for (int32_t p = ro[r]; p < ro[r + 1]; ++p)
+    out[p] = map_value(kind, val[p], rv);
+}
+
+__global__ __launch_bounds__(256) void rowwise_map_wave(
+    const int32_t *__restrict__ ro, const float *val,
+    const float *__restrict__ rowv, float *out, int32_t rows, int kind) {
+  const int64_t r = (int64_t)blockIdx.x * (blockDim.x / kWave) +
+                    threadIdx.x / kWave;
+  if (r >= rows)
+    return;
+  const float rv = rowv[r];
+  for (int32_t p = ro[r] + lane_id(); p < ro[r + 1]; p += kWave)
+    out[p] = map_value(kind, val[p], rv);
+}
+
+int grid_for(int64_t work, int64_t per_block, const char *what,
+             int64_t *grid) {
+  *grid = std::max<int64_t>(sw::ceil_div(work, per_block), 1);
+  return sw::check_grid(*grid, what);
+}
+
+} // namespace
+
+namespace sw {
+
+int launch_sddmm(const int32_t *ro, const int32_t *col, const float *val,
+                 const float *lhs, const float *rhs, float *out, int64_t rows,
+                 int64_t cols, int64_t kdim, int kind, float alpha, float beta,
+                 const sw_options &o, hipStream_t st) {
+  int64_t grid;
+  if (o.sddmm_lanes_per_row == 64) {
+    int rc = grid_for(rows, 4, "SDDMM", &grid);
+    if (rc)
+      return rc;
+    hipLaunchKernelGGL(sddmm_wave_per_row, dim3((unsigned)grid), dim3(256), 0,
+                       st, ro, col, val, lhs, rhs, out, (int32_t)rows, cols,
+                       (int32_t)kdim, kind, alpha, beta);
+  } else {
+    const int64_t B = o.sddmm_block_size;
+    int rc = grid_for(rows, B, "SDDMM", &grid);
+    if (rc)
+      return rc;
+    hipLaunchKernelGGL(sddmm_thread_per_row, dim3((unsigned)grid),
+                       dim3((unsigned)B), 0, st, ro, col, val, lhs, rhs, out,
+                       (int32_t)rows, cols, (int32_t)kdim, kind, alpha, beta);
+  }
+  return launch_check("SDDMM kernel");
+}
+
+int launch_row_reduce(const int32_t *ro, const float *val, float *out,
+                      int64_t rows, bool is_max, const sw_options &o,
+                      hipStream_t st) {
+  int64_t grid;
+  if (o.sddmm_lanes_per_row == 64) {
+    int rc = grid_for(rows, 4, "CSR row reduction", &grid);
+    if (rc)
+      return rc;
+    if (is_max)
+      hipLaunchKernelGGL(row_reduce_wave<true>, dim3((unsigned)grid), dim3(256),
+                         0, st, ro, val, out, (int32_t)rows);
+    else
+      hipLaunchKernelGGL(row_reduce_wave<false>, dim3((unsigned)grid),
+                         dim3(256), 0, st, ro, val, out, (int32_t)rows);
+  } else {
+    const int64_t B = o.row_reduction_block_size;
+    int rc = grid_for(rows, B, "CSR row reduction", &grid);
+    if (rc)
+      return rc;
+    if (is_max)
+      hipLaunchKernelGGL(row_reduce_thread<true>, dim3((unsigned)grid),
+                         dim3((unsigned)B), 0, st, ro, val, out, (int32_t)rows);
+    else
+      hipLaunchKernelGGL(row_reduce_thread<false>, dim3((unsigned)grid),
+                         dim3((unsigned)B), 0, st, ro, val, out, (int32_t)rows);
+  }
+  return launch_check("CSR row reduction kernel");
+}
+
+int launch_rowwise_map(const int32_t *ro, const float *val, const float *rowv,
+                       float *out, int64_t rows, int kind, const sw_options &o,
+                       hipStream_t st) {
+  int64_t grid;
+  if (o.sddmm_lanes_per_row == 64) {
+    int rc = grid_for(rows, 4, "CSR row-wise map", &grid);
+    if (rc)
+      return rc;
+    hipLaunchKernelGGL(rowwise_map_wave, dim3((unsigned)grid), dim3(256), 0,
+                       st, ro, val, rowv, out, (int32_t)rows, kind);
+  } else {
+    const int64_t B = o.rowwise_map_block_size;
+    int rc = grid_for(rows, B, "CSR row-wise map", &grid);
+    if (rc)
+      return rc;
+    hipLaunchKernelGGL(rowwise_map_thread, dim3((unsigned)grid),
+                       dim3((unsigned)B), 0, st, ro, val, rowv, out,
+                       (int32_t)rows, kind);
+  }
+  return launch_check("CSR row-wise map kernel");
+}
+
+} // namespace sw
+
+extern "C" int sw_sddmm_csr_f32(const int32_t *row_offsets,
+                                const int32_t *column_indices,
+                                const float *values, const float *lhs,
+                                const float *rhs, float *output_values,
+                                int64_t rows, int64_t cols, int64_t nnz,
+                                int64_t kdim, int combine, float alpha,
+                                float beta, const sw_options *opts,
+                                void *stream) {
+  sw::clear_error();
+  sw_options o;
+  int rc = sw::resolve_options(opts, &o);
+  if (rc)
+    return rc;
+  if (combine != SW_SDDMM_MUL && combine != SW_SDDMM_AFFINE &&
+      combine != SW_SDDMM_DOT)
+    return sw::fail(SW_ERR_INVALID_ARGUMENT, "unknown SDDMM combine kind %d",
+                    combine);
+  rc = sw::check_csr(row_offsets, column_indices,
+                     combine == SW_SDDMM_DOT ? output_values : values, rows,
+                     nnz, true);
+  if (rc)
+    return rc;
+  if (cols < 0 || kdim < 0 || kdim > INT32_MAX)
+    return sw::fail(SW_ERR_INVALID_SHAPE, "invalid SDDMM dense shapes");
+  if (rows == 0 || nnz == 0)
+    return SW_OK;
+  if (!output_values || (kdim > 0 && (!lhs || !rhs)))
+    return sw::fail(SW_ERR_INVALID_ARGUMENT, "SDDMM operand pointer is null");
+  return sw::launch_sddmm(row_offsets, column_indices,
+                          combine == SW_SDDMM_DOT ? nullptr : values, lhs, rhs,
+                          output_values, rows, cols, kdim, combine, alpha,
+                          beta, o, sw::as_stream(stream));
+}
+
+extern "C" int sw_csr_row_reduce_f32(const int32_t *row_offsets,
+                                     const int32_t *column_indices,
+                                     const float *values, float *output,
+                                     int64_t rows, int64_t nnz,
+                                     const char *kind, const sw_options *opts,
+                                     void *stream) {
+  (void)column_indices;
+  sw::clear_error();
+  sw_options o;
+  int rc = sw::resolve_options(opts, &o);
+  if (rc)
+    return rc;
+  if (!kind || (!sw::streq(kind, "sum") && !sw::streq(kind, "max")))
+    return sw::fail(SW_ERR_INVALID_ARGUMENT,
+                    "expected CSR row reduction kind 'sum' or 'max', but got "
+                    "'%s'",
+                    kind ? kind : "(null)");
+  rc = sw::check_csr(row_offsets, column_indices, values, rows, nnz, false);
+  if (rc)
+    return rc;
+  if (rows == 0)
+    return SW_OK;
+  if (!output)
+    return sw::fail(SW_ERR_INVALID_ARGUMENT, "output pointer is null");
+  return sw::launch_row_reduce(row_offsets, values, output, rows,
+                               sw::streq(kind, "max"), o,
+                               sw::as_stream(stream));
+}
+
+extern "C" int sw_csr_rowwise_map_f32(const int32_t *row_offsets,
+                                      const int32_t *column_indices,
+                                      const float *values,
+                                      const float *row_values,
+                                      float *output_values, int64_t rows,
+                                      int64_t nnz, int map,
+                                      const sw_options *opts, void *stream) {
+  (void)column_indices;
+  sw::clear_error();
+  sw_options o;
+  int rc = sw::resolve_options(opts, &o);
+  if (rc)
+    return rc;
+  if (map < SW_MAP_EXP_SUB || map > SW_MAP_MUL)
+    return sw::fail(SW_ERR_INVALID_ARGUMENT, "unknown row-wise map kind %d",
+                    map);
+  rc = sw::check_csr(row_offsets, column_indices, values, rows, nnz, false);
+  if (rc)
+    return rc;
+  if (rows == 0 || nnz == 0)
+    return SW_OK;
+  if (!output_values || !row_values)
+    return sw::fail(SW_ERR_INVALID_ARGUMENT, "row-wise map pointer is null");
+  return sw::launch_rowwise_map(row_offsets, values, row_values, output_values,
+                                rows, map, o, sw::as_stream(stream));
+}
+
+extern "C" int sw_sparse_attention_f32(
+    const int32_t *row_offsets, const int32_t *column_indices,
+    const float *mask_values, const float *query, const float *transposed_key,
+    const float *value, float *scores, float *row_maximum, float *row_sum,
+    float *output, int64_t rows, int64_t cols, int64_t nnz, int64_t d,
+    int64_t dv, float alpha, float beta, const sw_options *opts,
+    void *stream) {
+  sw::clear_error();
+  sw_options o;
+  int rc = sw::resolve_options(opts, &o);
+  if (rc)
+    return rc;
+  rc = sw::check_csr(row_offsets, column_indices, mask_values, rows, nnz, true);
+  if (rc)
+    return rc;
+  if (cols < 0 || d < 0 || dv < 0 || d > INT32_MAX)
+    return sw::fail(SW_ERR_INVALID_SHAPE, "invalid attention shapes");
+  if (rows == 0)
+    return SW_OK;
+  if (!row_maximum || !row_sum || (dv > 0 && !output) ||
+      (nnz > 0 && (!scores || !query || !transposed_key || (dv > 0 && !value))))
+    return sw::fail(SW_ERR_INVALID_ARGUMENT, "attention buffer pointer is null");
+  hipStream_t st = sw::as_stream(stream);
+  if (nnz > 0) {
+    rc = sw::launch_sddmm(row_offsets, column_indices, mask_values, query,
+                          transposed_key, scores, rows, cols, d,
+                          SW_SDDMM_AFFINE, alpha, beta, o, st);
+    if (rc)
+      return rc;
+  }
+  rc = sw::launch_row_reduce(row_offsets, scores, row_maximum, rows, true, o, st);
+  if (rc)
+    return rc;
+  if (nnz > 0) {
+    rc = sw::launch_rowwise_map(row_offsets, scores, row_maximum, scores, rows,
+                                SW_MAP_EXP_SUB, o, st);
+    if (rc)
+      return rc;
+  }
+  rc = sw::launch_row_reduce(row_offsets, scores, row_sum, rows, false, o, st);
+  if (rc)
+    return rc;
+  if (nnz > 0) {
+    rc = sw::launch_rowwise_map(row_offsets, scores, row_sum, scores, rows,
+                                SW_MAP_DIV, o, st);
+    if (rc)
+      return rc;
+  }
+  if (dv == 0)
+    return SW_OK;
+  return sw::launch_spmm(row_offsets, column_indices, scores, value, output,
+                         rows, nnz, dv, o, "attention output SpMM", st);
+}

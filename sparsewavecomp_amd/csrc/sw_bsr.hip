@@ -1,0 +1,247 @@
+// sparsewave.bsr_spmm on gfx950 behind sw_bsr_spmm_f32 / sw_bsr_spmm_bf16.
+//
+// Reference kernel: ThreadPerOutputBSRSpMMPattern
+// (lib/Dialect/SparseWave/Transforms/SparseWaveToGPU.cpp:560-665), blocks
+// row-major [nnzb][b][b] (SparseWaveOps.td:133-137), shape rules of the
+// verifier (lib/Dialect/SparseWave/IR/SparseWaveOps.cpp:144-207, 340-372).
+//
+// The MI355X path for 16 x 16 blocks runs each block product on the matrix
+// cores: a workgroup of four waves owns one block row (16 output rows) and
+// 128 output columns; each wave owns two 16 x 16 output tiles and issues
+//   fp32: v_mfma_f32_16x16x4_f32 four times per block and tile,
+//   bf16: v_mfma_f32_16x16x16_bf16 once per block and tile,
+// accumulating in fp32 registers across the block row's blocks.
+#include "sw_device.h"
+#include "sw_internal.h"
+
+#include <algorithm>
+
+using namespace swd;
+
+namespace {
+
+typedef short v4s __attribute__((ext_vector_type(4)));
+
+// thread-per-output for any block size: one thread per output element.
+template <typename T>
+__device__ __forceinline__ float to_f32(T v);
+template <>
+__device__ __forceinline__ float to_f32<float>(float v) {
+  return v;
+}
+template <>
+__device__ __forceinline__ float to_f32<uint16_t>(uint16_t v) {
+  return __uint_as_float((uint32_t)v << 16);
+}
+
+template <typename T>
+__global__ __launch_bounds__(1024) void bsr_thread_per_output(
+    const int32_t *__restrict__ bro, const int32_t *__restrict__ bcol,
+    const T *__restrict__ bval, const T *__restrict__ rhs,
+    float *__restrict__ out, int64_t rows, int64_t k, int32_t b) {
+  int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= rows * k)
+    return;
+  int64_t r = e / k, c = e - r * k;
+  int64_t br = r / b, lr = r - br * b;
+  float acc = 0.0f;
+  for (int32_t bp = bro[br]; bp < bro[br + 1]; ++bp) {
+    const T *blk = bval + (int64_t)bp * b * b + lr * b;
+    int64_t rb = (int64_t)bcol[bp] * b;
+    for (int32_t lc = 0; lc < b; ++lc)
+      acc = __builtin_fmaf(to_f32<T>(blk[lc]), to_f32<T>(rhs[(rb + lc) * k + c]),
+                           acc);
+  }
+  out[e] = acc;
+}
+
+// MFMA operand layouts (one 16 x 16 x K step, wave64, lane l):
+//   A[i][k] with i = l % 16, k from the lane group g = l / 16,
+//   B[k][j] with j = l % 16, same k,
+//   D[4*g + v][l % 16] in accumulator register v.
+// The k order inside a block is a free choice as long as A and B agree;
+// fp32 uses k = 4*g + s at step s so that one 128-bit load gives a lane its
+// four A values.
+__global__ __launch_bounds__(256) void bsr16_mfma_f32(
+    const int32_t *__restrict__ bro, const int32_t *__restrict__ bcol,
+    const float *__restrict__ bval, const float *__restrict__ rhs,
+    float *__restrict__ out, int64_t k) {
+  const int br = blockIdx.x;
+  const int wave = threadIdx.x / kWave;
+  const int l = lane_id();
+  const int i = l & 15, g = l >> 4;
+  const int64_t n0 = (int64_t)blockIdx.y * 128 + wave * 32;
+  const int64_t c0 = n0 + i, c1 = n0 + 16 + i;
+  const bool ok0 = c0 < k, ok1 = c1 < k;
+  v4f acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+  const int32_t s = bro[br], e = bro[br + 1];
+  for (int32_t bp = s; bp < e; ++bp) {
+    const int64_t bc = bcol[bp];
+    const v4f a = ld_stream(reinterpret_cast<const v4f *>(
+        bval + (int64_t)bp * 256 + i * 16 + g * 4));
+    const float *brow = rhs + (bc * 16 + g * 4) * k;
+    float b0[4], b1[4];
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      b0[st] = ok0 ? brow[st * k + c0] : 0.0f;
+      b1[st] = ok1 ? brow[st * k + c1] : 0.0f;
+    }
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a[st], b0[st], acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a[st], b1[st], acc1, 0, 0, 0);
+    }
+  }
+  float *o = out + ((int64_t)br * 16 + g * 4) * k;
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    if (ok0)
+      o[v * k + c0] = acc0[v];
+    if (ok1)
+      o[v * k + c1] = acc1[v];
+  }
+}
+
+__global__ __launch_bounds__(256) void bsr16_mfma_bf16(
+    const int32_t *__restrict__ bro, const int32_t *__restrict__ bcol,
+    const uint16_t *__restrict__ bval, const uint16_t *__restrict__ rhs,
+    float *__restrict__ out, int64_t k) {
+  const int br = blockIdx.x;
+  const int wave = threadIdx.x / kWave;
+  const int l = lane_id();
+  const int i = l & 15, g = l >> 4;
+  const int64_t n0 = (int64_t)blockIdx.y * 128 + wave * 32;
+  const int64_t c0 = n0 + i, c1 = n0 + 16 + i;
+  const bool ok0 = c0 < k, ok1 = c1 < k;
+  v4f acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+  const int32_t s = bro[br], e = bro[br + 1];
+  for (int32_t bp = s; bp < e; ++bp) {
+    const int64_t bc = bcol[bp];
+    // A[i][4g .. 4g+3]: 8 contiguous bytes of the row-major block
+    const v4s a = *reinterpret_cast<const v4s *>(bval + (int64_t)bp * 256 +
+                                                 i * 16 + g * 4);
+    const uint16_t *brow = rhs + (bc * 16 + g * 4) * k;
+    v4s b0, b1;
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      b0[st] = ok0 ? (short)brow[st * k + c0] : (short)0;
+      b1[st] = ok1 ? (short)brow[st * k + c1] : (short)0;
+    }
+    acc0 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b0, acc0, 0, 0, 0);
+    acc1 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b1, acc1, 0, 0, 0);
+  }
+  float *o = out + ((int64_t)br * 16 + g * 4) * k;
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    if (ok0)
+      o[v * k + c0] = acc0[v];
+    if (ok1)
+      o[v * k + c1] = acc1[v];
+  }
+}
+
+int check_bsr(const int32_t *bro, const int32_t *bcol, const void *bval,
+              const void *rhs, const float *out, int64_t rows, int64_t cols,
+              int64_t nnzb, int64_t k, int64_t b) {
+  if (b < 1)
+    return sw::fail(SW_ERR_INVALID_SHAPE,
+                    "BSR block size must be positive, but got %lld",
+                    (long long)b);
+  if (rows < 0 || cols < 0 || nnzb < 0 || k < 0)
+    return sw::fail(SW_ERR_INVALID_SHAPE, "negative BSR shape");
+  if (rows % b != 0 || cols % b != 0)
+    return sw::fail(SW_ERR_INVALID_SHAPE,
+                    "BSR matrix dimensions %lld x %lld must be divisible by "
+                    "block size %lld",
+                    (long long)rows, (long long)cols, (long long)b);
+  if (nnzb * b * b > (int64_t)INT32_MAX * 16)
+    return sw::fail(SW_ERR_INVALID_SHAPE, "too many BSR blocks");
+  if (rows / b > INT32_MAX - 1)
+    return sw::fail(SW_ERR_INVALID_SHAPE, "too many BSR block rows");
+  if (!bro)
+    return sw::fail(SW_ERR_INVALID_ARGUMENT, "block row offsets pointer is null");
+  if (rows > 0 && k > 0 && !out)
+    return sw::fail(SW_ERR_INVALID_ARGUMENT, "output pointer is null");
+  if (nnzb > 0 && (!bcol || !bval || (k > 0 && !rhs)))
+    return sw::fail(SW_ERR_INVALID_ARGUMENT, "BSR operand pointer is null");
+  return SW_OK;
+}
+
+template <typename T>
+int launch_bsr(const int32_t *bro, const int32_t *bcol, const T *bval,
+               const T *rhs, float *out, int64_t rows, int64_t nnzb,
+               int64_t k, int64_t b, const sw_options &o, hipStream_t st,
+               bool mfma_ok) {
+  (void)nnzb;
+  if (rows == 0 || k == 0)
+    return SW_OK;
+  if (mfma_ok) {
+    int64_t gy = sw::ceil_div(k, 128);
+    if (gy > 65535)
+      return sw::fail(SW_ERR_INVALID_SHAPE, "rhs has too many columns");
+    dim3 grid((unsigned)(rows / 16), (unsigned)gy);
+    if constexpr (sizeof(T) == 4)
+      hipLaunchKernelGGL(bsr16_mfma_f32, grid, dim3(256), 0, st, bro, bcol,
+                         bval, rhs, out, k);
+    else
+      hipLaunchKernelGGL(bsr16_mfma_bf16, grid, dim3(256), 0, st, bro, bcol,
+                         bval, rhs, out, k);
+    return sw::launch_check("BSR MFMA kernel");
+  }
+  const int64_t B = o.spmm_block_size;
+  int64_t grid = std::max<int64_t>(sw::ceil_div(rows * k, B), 1);
+  int rc = sw::check_grid(grid, "BSR SpMM");
+  if (rc)
+    return rc;
+  hipLaunchKernelGGL(bsr_thread_per_output<T>, dim3((unsigned)grid),
+                     dim3((unsigned)B), 0, st, bro, bcol, bval, rhs, out, rows,
+                     k, (int32_t)b);
+  return sw::launch_check("thread-per-output BSR SpMM kernel");
+}
+
+} // namespace
+
+extern "C" int sw_bsr_spmm_f32(const int32_t *block_row_offsets,
+                               const int32_t *block_column_indices,
+                               const float *block_values, const float *rhs,
+                               float *output, int64_t rows, int64_t cols,
+                               int64_t nnzb, int64_t k, int64_t block_size,
+                               const sw_options *opts, void *stream) {
+  sw::clear_error();
+  sw_options o;
+  int rc = sw::resolve_options(opts, &o);
+  if (rc)
+    return rc;
+  rc = check_bsr(block_row_offsets, block_column_indices, block_values, rhs,
+                 output, rows, cols, nnzb, k, block_size);
+  if (rc)
+    return rc;
+  bool mfma = o.bsr_use_mfma && block_size == 16 &&
+              sw::aligned16(block_values);
+  return launch_bsr<float>(block_row_offsets, block_column_indices,
+                           block_values, rhs, output, rows, nnzb, k,
+                           block_size, o, sw::as_stream(stream), mfma);
+}
+
+extern "C" int sw_bsr_spmm_bf16(const int32_t *block_row_offsets,
+                                const int32_t *block_column_indices,
+                                const uint16_t *block_values,
+                                const uint16_t *rhs, float *output,
+                                int64_t rows, int64_t cols, int64_t nnzb,
+                                int64_t k, int64_t block_size,
+                                const sw_options *opts, void *stream) {
+  sw::clear_error();
+  sw_options o;
+  int rc = sw::resolve_options(opts, &o);
+  if (rc)
+    return rc;
+  rc = check_bsr(block_row_offsets, block_column_indices, block_values, rhs,
+                 output, rows, cols, nnzb, k, block_size);
+  if (rc)
+    return rc;
+  bool mfma = o.bsr_use_mfma && block_size == 16 &&
+              (reinterpret_cast<uintptr_t>(block_values) & 7u) == 0;
+  return launch_bsr<uint16_t>(block_row_offsets, block_column_indices,
+                              block_values, rhs, output, rows, nnzb, k,
+                              block_size, o, sw::as_stream(stream), mfma);
+}

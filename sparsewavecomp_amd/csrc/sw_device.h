@@ -1,0 +1,187 @@
+// Device-side building blocks for gfx950 (CDNA4, Wave64).
+//
+// Cross-lane work uses DPP (row_shr, quad_perm, row_mirror, row_bcast) and
+// ds_swizzle, which move data through the VALU without LDS memory, and
+// v_readlane for wave-uniform results.  Streaming CSR arrays are read with
+// non-temporal loads so they do not evict the gathered vector from L2.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace swd {
+
+constexpr int kWave = 64;
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ int lane_id() { return __lane_id(); }
+
+// ---- DPP --------------------------------------------------------------
+// DPP control codes (GFX9 encoding).
+constexpr int kQuadXor1 = 0xB1;     // quad_perm [1,0,3,2]
+constexpr int kQuadXor2 = 0x4E;     // quad_perm [2,3,0,1]
+constexpr int kRowShr1 = 0x111;
+constexpr int kRowShr2 = 0x112;
+constexpr int kRowShr4 = 0x114;
+constexpr int kRowShr8 = 0x118;
+constexpr int kRowMirror = 0x140;      // lane i <- 15 - i within a row of 16
+constexpr int kRowHalfMirror = 0x141;  // lane i <- 7 - i within 8 lanes
+constexpr int kRowBcast15 = 0x142;     // lane 15 of row r -> row r+1
+constexpr int kRowBcast31 = 0x143;     // lane 31 -> rows 2 and 3
+
+// Lanes whose DPP source is invalid (or masked off) keep `old`.
+template <int CTRL, int ROW_MASK = 0xF, int BANK_MASK = 0xF>
+__device__ __forceinline__ int dpp_i(int old, int src) {
+  return __builtin_amdgcn_update_dpp(old, src, CTRL, ROW_MASK, BANK_MASK,
+                                     false);
+}
+template <int CTRL, int ROW_MASK = 0xF, int BANK_MASK = 0xF>
+__device__ __forceinline__ float dpp_f(float old, float src) {
+  return __int_as_float(dpp_i<CTRL, ROW_MASK, BANK_MASK>(__float_as_int(old),
+                                                         __float_as_int(src)));
+}
+
+// ds_swizzle bit mode: lane i reads lane ((i & and) | or) ^ xor within 32.
+__device__ __forceinline__ float swizzle_xor16(float v) {
+  return __int_as_float(
+      __builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x1F | (0x10 << 10)));
+}
+
+__device__ __forceinline__ float shfl_xor32(float v) {
+  // lane ^ 32: ds_bpermute with a byte address
+  int src = (lane_id() ^ 32) << 2;
+  return __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(v)));
+}
+
+// Sum over aligned groups of G lanes (G a power of two <= 64); every lane of
+// a group receives the group sum.
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+  if constexpr (G >= 2) v += dpp_f<kQuadXor1>(0.0f, v);
+  if constexpr (G >= 4) v += dpp_f<kQuadXor2>(0.0f, v);
+  if constexpr (G >= 8) v += dpp_f<kRowHalfMirror>(0.0f, v);
+  if constexpr (G >= 16) v += dpp_f<kRowMirror>(0.0f, v);
+  if constexpr (G >= 32) v += swizzle_xor16(v);
+  if constexpr (G >= 64) v += shfl_xor32(v);
+  return v;
+}
+
+// Whole-wave sum, returned wave-uniform.
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp_f<kQuadXor1>(0.0f, v);
+  v += dpp_f<kQuadXor2>(0.0f, v);
+  v += dpp_f<kRowHalfMirror>(0.0f, v);
+  v += dpp_f<kRowMirror>(0.0f, v);
+  float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return (a + b) + (c + d);
+}
+
+// Inclusive segmented scan over the wave: lane l adds the running value of
+// lane l - k whenever both carry the same key.  Keys must be non-decreasing
+// over the lanes that matter (CSR rows are), which makes the combine
+// associative, so the Hillis-Steele row_shr steps followed by the two
+// row_bcast steps give the segmented prefix sum.
+__device__ __forceinline__ float wave_segmented_scan(int key, float v) {
+  constexpr int kNoKey = INT32_MIN;
+  int k;
+  float s;
+  k = dpp_i<kRowShr1>(kNoKey, key);
+  s = dpp_f<kRowShr1>(0.0f, v);
+  v += (k == key) ? s : 0.0f;
+  k = dpp_i<kRowShr2>(kNoKey, key);
+  s = dpp_f<kRowShr2>(0.0f, v);
+  v += (k == key) ? s : 0.0f;
+  k = dpp_i<kRowShr4>(kNoKey, key);
+  s = dpp_f<kRowShr4>(0.0f, v);
+  v += (k == key) ? s : 0.0f;
+  k = dpp_i<kRowShr8>(kNoKey, key);
+  s = dpp_f<kRowShr8>(0.0f, v);
+  v += (k == key) ? s : 0.0f;
+  k = dpp_i<kRowBcast15, 0xA>(kNoKey, key);
+  s = dpp_f<kRowBcast15, 0xA>(0.0f, v);
+  v += (k == key) ? s : 0.0f;
+  k = dpp_i<kRowBcast31, 0xC>(kNoKey, key);
+  s = dpp_f<kRowBcast31, 0xC>(0.0f, v);
+  v += (k == key) ? s : 0.0f;
+  return v;
+}
+
+// Shift by one lane up / down across the whole wave (ds_bpermute).
+__device__ __forceinline__ int shfl_up1_i(int v, int fill) {
+  int l = lane_id();
+  int r = __builtin_amdgcn_ds_bpermute((l - 1) << 2, v);
+  return l == 0 ? fill : r;
+}
+__device__ __forceinline__ float shfl_up1_f(float v, float fill) {
+  return __int_as_float(shfl_up1_i(__float_as_int(v), __float_as_int(fill)));
+}
+__device__ __forceinline__ int shfl_down1_i(int v, int fill) {
+  int l = lane_id();
+  int r = __builtin_amdgcn_ds_bpermute((l + 1) << 2, v);
+  return l == kWave - 1 ? fill : r;
+}
+
+__device__ __forceinline__ uint64_t ballot(bool p) {
+  return __builtin_amdgcn_ballot_w64(p);
+}
+
+// ---- loads ---------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ T ld_stream(const T *p) {
+  return __builtin_nontemporal_load(p);
+}
+
+// ---- CSR row recovery -------------------------------------------------------
+// All variants return (first j in [lo, hi) with ro[j] > pos) - 1, or hi - 1
+// when there is none, i.e. the upper-bound search of the reference
+// (SparsePositionToSCF.cpp:225-271) restricted to a range known to hold the
+// answer.  For sorted row offsets the result is identical to the full search.
+
+// Per-lane binary search.
+__device__ __forceinline__ int row_search_lane(const int32_t *__restrict__ ro,
+                                               uint32_t lo, uint32_t hi,
+                                               int32_t pos) {
+  while (lo < hi) {
+    uint32_t mid = lo + ((hi - lo) >> 1);
+    if (ro[mid] <= pos)
+      lo = mid + 1;
+    else
+      hi = mid;
+  }
+  return (int)lo - 1;
+}
+
+// Wave-cooperative 64-ary search for a wave-uniform position: every round
+// each lane probes one offset and a ballot narrows the range 64-fold, so a
+// 1M-row matrix needs four dependent loads instead of twenty.
+__device__ __forceinline__ int row_search_wave(const int32_t *__restrict__ ro,
+                                               uint32_t lo, uint32_t hi,
+                                               int32_t pos) {
+  const uint32_t lane = (uint32_t)lane_id();
+  while (hi - lo > (uint32_t)kWave) {
+    uint32_t step = (hi - lo + kWave - 1) / kWave;
+    uint32_t idx = lo + lane * step;
+    bool pred = idx < hi && ro[idx] <= pos;
+    uint32_t cnt = (uint32_t)__builtin_popcountll(ballot(pred));
+    uint32_t base = lo;
+    if (cnt > 0)
+      lo = base + (cnt - 1) * step + 1;
+    uint32_t cap = base + cnt * step;
+    if (cap < hi)
+      hi = cap;
+    lo = __builtin_amdgcn_readfirstlane(lo);
+    hi = __builtin_amdgcn_readfirstlane(hi);
+  }
+  uint32_t idx = lo + lane;
+  bool pred = idx < hi && ro[idx] <= pos;
+  uint32_t cnt = (uint32_t)__builtin_popcountll(ballot(pred));
+  return (int)(lo + cnt) - 1;
+}
+
+} // namespace swd

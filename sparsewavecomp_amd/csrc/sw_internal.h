@@ -1,0 +1,79 @@
+// Host-side helpers shared by the launchers of the C ABI.
+#pragma once
+
+#include "../../include/sparsewave_amd.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstring>
+
+namespace sw {
+
+// Record a formatted message for sw_last_error() and return `code`.
+int fail(int code, const char *fmt, ...);
+void clear_error();
+
+inline int hip_check(hipError_t e, const char *what) {
+  if (e != hipSuccess)
+    return fail(SW_ERR_HIP, "%s failed: %s", what, hipGetErrorString(e));
+  return SW_OK;
+}
+
+// After a kernel launch: report a launch-configuration error if any.
+inline int launch_check(const char *kernel) {
+  return hip_check(hipGetLastError(), kernel);
+}
+
+inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+inline bool aligned16(const void *p) {
+  return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+}
+
+// Largest grid dimension x we launch in one go.
+constexpr int64_t kMaxGridX = 2147483647;
+
+inline int check_grid(int64_t grid, const char *what) {
+  if (grid > kMaxGridX)
+    return fail(SW_ERR_INVALID_SHAPE, "%s needs %lld workgroups, more than "
+                "one launch allows", what, (long long)grid);
+  return SW_OK;
+}
+
+// Validate options, or use defaults when `opts` is NULL.
+inline int resolve_options(const sw_options *opts, sw_options *out) {
+  if (opts) {
+    *out = *opts;
+  } else {
+    sw_options_init(out);
+  }
+  return sw_validate_options(out);
+}
+
+inline bool streq(const char *a, const char *b) { return std::strcmp(a, b) == 0; }
+
+// CSR shape checks mirroring verifyCSRStorage
+// (lib/Dialect/SparseWave/IR/SparseWaveOps.cpp:62-109): rows >= 0,
+// nnz within the i32 index range, and non-null arrays where data exists.
+inline int check_csr(const int32_t *ro, const int32_t *col, const float *val,
+                     int64_t rows, int64_t nnz, bool need_col) {
+  if (rows < 0 || nnz < 0)
+    return fail(SW_ERR_INVALID_SHAPE,
+                "expected non-negative rows and nnz, but got %lld and %lld",
+                (long long)rows, (long long)nnz);
+  if (rows > INT32_MAX - 1 || nnz > INT32_MAX)
+    return fail(SW_ERR_INVALID_SHAPE,
+                "i32 CSR indices cannot address %lld rows / %lld nonzeros",
+                (long long)rows, (long long)nnz);
+  if (!ro)
+    return fail(SW_ERR_INVALID_ARGUMENT, "row offsets pointer is null");
+  if (nnz > 0 && ((need_col && !col) || !val))
+    return fail(SW_ERR_INVALID_ARGUMENT,
+                "column index or value pointer is null");
+  return SW_OK;
+}
+
+} // namespace sw

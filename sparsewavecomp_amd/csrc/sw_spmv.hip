@@ -1,0 +1,466 @@
+// sparsewave.spmv on gfx950: the row mappings (thread, wave, block per row)
+// and the position mappings (thread and wave per position), with their
+// launchers behind sw_spmv_csr_f32.
+//
+// Reference kernels (generated IR, not hand-written code):
+//   thread-per-row     SparseWaveToGPU.cpp:216-274
+//   wave-per-row       SparseWaveToGPU.cpp:276-354, SparseGPUUtils.cpp:34-59,236-245
+//   block-per-row      SparseWaveToGPU.cpp:356-487
+//   thread-per-position SparsePositionScheduling.cpp:135-316
+//   wave-per-position  SparsePositionScheduling.cpp:318-403,
+//                      SparsePositionToSCF.cpp:190-271, SparseGPUUtils.cpp:247-292
+#include "sw_device.h"
+#include "sw_internal.h"
+
+using namespace swd;
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// thread-per-row: one thread accumulates one row sequentially from zero.
+__global__ __launch_bounds__(1024) void spmv_thread_per_row(
+    const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
+    const float *__restrict__ val, const float *__restrict__ x,
+    float *__restrict__ y, int32_t rows) {
+  int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows)
+    return;
+  int32_t s = ro[r], e = ro[r + 1];
+  float acc = 0.0f;
+  for (int32_t p = s; p < e; ++p)
+    acc = __builtin_fmaf(ld_stream(val + p), x[ld_stream(col + p)], acc);
+  y[r] = acc;
+}
+
+// ---------------------------------------------------------------------------
+// wave-per-row with G lanes per row (G = 64 is the reference's one wave per
+// row).  Lane l of a group sums positions start+l, start+l+G, ...; the group
+// sum uses DPP / swizzle butterflies; the group's first lane stores.
+template <int G>
+__global__ __launch_bounds__(1024) void spmv_group_per_row(
+    const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
+    const float *__restrict__ val, const float *__restrict__ x,
+    float *__restrict__ y, int32_t rows) {
+  const int groups_per_block = blockDim.x / G;
+  int64_t r = (int64_t)blockIdx.x * groups_per_block + threadIdx.x / G;
+  const int gl = threadIdx.x & (G - 1);
+  float acc = 0.0f;
+  if (r < rows) {
+    int32_t s = ro[r], e = ro[r + 1];
+    int32_t p = s + gl;
+    // two independent accumulators keep two gathers in flight per lane
+    float acc2 = 0.0f;
+    for (; p + G < e; p += 2 * G) {
+      int32_t c0 = ld_stream(col + p), c1 = ld_stream(col + p + G);
+      float v0 = ld_stream(val + p), v1 = ld_stream(val + p + G);
+      acc = __builtin_fmaf(v0, x[c0], acc);
+      acc2 = __builtin_fmaf(v1, x[c1], acc2);
+    }
+    if (p < e)
+      acc = __builtin_fmaf(ld_stream(val + p), x[ld_stream(col + p)], acc);
+    acc += acc2;
+  }
+  // every lane of the wave takes part in the butterfly
+  acc = group_sum<G>(acc);
+  if (r < rows && gl == 0)
+    y[r] = acc;
+}
+
+// ---------------------------------------------------------------------------
+// block-per-row: the block strides the row, each wave reduces its partial
+// sum, partials meet in LDS, wave 0 reduces them and lane 0 stores.
+__global__ __launch_bounds__(1024) void spmv_block_per_row(
+    const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
+    const float *__restrict__ val, const float *__restrict__ x,
+    float *__restrict__ y, int32_t rows) {
+  __shared__ float partial[1024 / kWave];
+  const int64_t r = blockIdx.x;
+  const int t = threadIdx.x;
+  const int B = blockDim.x;
+  float acc = 0.0f;
+  if (r < rows) {
+    int32_t s = ro[r], e = ro[r + 1];
+    for (int32_t p = s + t; p < e; p += B)
+      acc = __builtin_fmaf(ld_stream(val + p), x[ld_stream(col + p)], acc);
+  }
+  // blockDim.x is a multiple of 64 (validated), so every wave is full
+  float w = wave_sum(acc);
+  const int wave = t / kWave;
+  if ((t & (kWave - 1)) == 0)
+    partial[wave] = w;
+  __syncthreads();
+  if (wave == 0) {
+    const int waves = B / kWave;
+    float v = lane_id() < waves ? partial[lane_id()] : 0.0f;
+    v = wave_sum(v);
+    if (t == 0 && r < rows)
+      y[r] = v;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Output initialisation of the position mappings
+// (SparsePositionScheduling.cpp:31-47): one thread per output element.
+__global__ __launch_bounds__(1024) void fill_zero_f32(float *__restrict__ y,
+                                                      int64_t n) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n)
+    y[i] = 0.0f;
+}
+
+// ---------------------------------------------------------------------------
+// thread-per-position, atomic: worker w handles positions
+// [w*chunk, min((w+1)*chunk, nnz)), recovers each position's row by the row
+// search and adds val*x atomically (SparsePositionScheduling.cpp:135-194).
+__global__ __launch_bounds__(1024) void spmv_thread_position_atomic(
+    const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
+    const float *__restrict__ val, const float *__restrict__ x,
+    float *__restrict__ y, int32_t rows, int32_t nnz, int32_t chunk) {
+  int64_t w = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int64_t b = w * chunk;
+  if (b >= nnz)
+    return;
+  int64_t e = b + chunk < nnz ? b + chunk : nnz;
+  for (int64_t p = b; p < e; ++p) {
+    int r = row_search_lane(ro, 1u, (uint32_t)rows + 1u, (int32_t)p);
+    unsafeAtomicAdd(y + r, val[p] * x[col[p]]);
+  }
+}
+
+// thread-per-position, segmented: the chunk's first row comes from the row
+// search, later rows from walking the row offsets; a run of equal rows is
+// summed locally and added atomically when the row changes
+// (SparsePositionScheduling.cpp:196-316).
+__global__ __launch_bounds__(1024) void spmv_thread_position_segmented(
+    const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
+    const float *__restrict__ val, const float *__restrict__ x,
+    float *__restrict__ y, int32_t rows, int32_t nnz, int32_t chunk) {
+  int64_t w = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int64_t b = w * chunk;
+  if (b >= nnz)
+    return;
+  int64_t e = b + chunk < nnz ? b + chunk : nnz;
+  int r = row_search_lane(ro, 1u, (uint32_t)rows + 1u, (int32_t)b);
+  int32_t next = ro[r + 1];
+  float acc = val[b] * x[col[b]];
+  for (int64_t p = b + 1; p < e; ++p) {
+    int rr = r;
+    while (p >= next) {
+      ++rr;
+      next = ro[rr + 1];
+    }
+    float c = val[p] * x[col[p]];
+    if (rr == r) {
+      acc += c;
+    } else {
+      unsafeAtomicAdd(y + r, acc);
+      r = rr;
+      acc = c;
+    }
+  }
+  unsafeAtomicAdd(y + r, acc);
+}
+
+// ---------------------------------------------------------------------------
+// wave-per-position, Wave64 design.
+//
+// Positions are grouped in units of P consecutive positions (P = 1 is the
+// reference's one position per lane).  There are G = max(ceil(units/B), 1)
+// blocks and G*(B/64) waves; wave w owns the balanced partition
+// [w*base + min(w, rem), ...) of the units (SparsePositionToSCF.cpp:190-223)
+// and lane l the unit begin+l.  The wave finds the rows of its first and last
+// position with a 64-ary cooperative search, each lane then finds the row of
+// its first position inside that narrow range, walks its P positions
+// (col/val read with 128-bit non-temporal loads when P >= 4) and
+//   - stores rows that start and end inside the lane directly,
+//   - keeps the partial of its first row (head) and of its last row (tail).
+// One segmented scan over the tails joins rows that continue across lanes;
+// a lane whose first row continues from its left neighbour picks up that
+// neighbour's scanned tail ("carry"), and every other row segment ends with
+// one atomic add.  The output is zeroed first, as in the reference.
+template <int P, bool VEC>
+__global__ __launch_bounds__(1024) void spmv_wave_position(
+    const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
+    const float *__restrict__ val, const float *__restrict__ x,
+    float *__restrict__ y, int32_t rows, int32_t nnz, int64_t units,
+    int64_t wave_count) {
+  const int lane = lane_id();
+  const int64_t wave =
+      (int64_t)blockIdx.x * (blockDim.x / kWave) + (threadIdx.x / kWave);
+  const uint64_t base = (uint64_t)units / (uint64_t)wave_count;
+  const uint64_t rem = (uint64_t)units % (uint64_t)wave_count;
+  const uint64_t wv = (uint64_t)wave;
+  const uint64_t ub = wv * base + (wv < rem ? wv : rem);
+  const uint64_t ue = ub + base + (wv < rem ? 1u : 0u);
+  const int64_t wbeg = (int64_t)ub * P;
+  const int64_t wend = (int64_t)ue * P < nnz ? (int64_t)ue * P : nnz;
+  if (wbeg >= wend)
+    return; // wave-uniform: the whole wave leaves
+
+  const int first_row =
+      row_search_wave(ro, 1u, (uint32_t)rows + 1u, (int32_t)wbeg);
+  const int last_row = row_search_wave(ro, (uint32_t)first_row + 1u,
+                                       (uint32_t)rows + 1u,
+                                       (int32_t)(wend - 1));
+
+  const int64_t u = (int64_t)ub + lane;
+  const bool active = (uint64_t)u < ue && u * P < nnz;
+  const int32_t p0 = active ? (int32_t)(u * P) : 0;
+  const int32_t pe = active ? (int32_t)((u * P + P) < nnz ? u * P + P : nnz) : 0;
+
+  // operands of the lane's positions
+  float prod[P];
+  if (active) {
+    if constexpr (VEC && P >= 4) {
+      if (pe - p0 == P) {
+#pragma unroll
+        for (int q = 0; q < P; q += 4) {
+          v4i c = ld_stream(reinterpret_cast<const v4i *>(col + p0 + q));
+          v4f v = ld_stream(reinterpret_cast<const v4f *>(val + p0 + q));
+          prod[q + 0] = v.x * x[c.x];
+          prod[q + 1] = v.y * x[c.y];
+          prod[q + 2] = v.z * x[c.z];
+          prod[q + 3] = v.w * x[c.w];
+        }
+      } else {
+#pragma unroll
+        for (int q = 0; q < P; ++q)
+          prod[q] = (p0 + q < pe) ? ld_stream(val + p0 + q) *
+                                        x[ld_stream(col + p0 + q)]
+                                  : 0.0f;
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < P; ++q)
+        prod[q] = (p0 + q < pe)
+                      ? ld_stream(val + p0 + q) * x[ld_stream(col + p0 + q)]
+                      : 0.0f;
+    }
+  }
+
+  int lrow = 0, row = 0, closed = 0;
+  float head = 0.0f, acc = 0.0f;
+  if (active) {
+    lrow = row_search_lane(ro, (uint32_t)first_row + 1u,
+                           (uint32_t)last_row + 2u, p0);
+    row = lrow;
+    int32_t next = ro[row + 1];
+#pragma unroll
+    for (int q = 0; q < P; ++q) {
+      const int32_t p = p0 + q;
+      if (p < pe) {
+        while (p >= next) {
+          if (closed == 0)
+            head = acc;
+          else
+            y[row] = acc; // row began and ended inside this lane
+          ++closed;
+          acc = 0.0f;
+          ++row;
+          next = ro[row + 1];
+        }
+        acc += prod[q];
+      }
+    }
+  }
+
+  // segmented scan over the lanes' open tails
+  const int key = active ? row : -1;
+  const float scanned = wave_segmented_scan(key, active ? acc : 0.0f);
+  const int prev_key = shfl_up1_i(key, INT32_MIN);
+  const float prev_scanned = shfl_up1_f(scanned, 0.0f);
+  const int next_lrow = shfl_down1_i(active ? lrow : -2, -2);
+  if (active) {
+    if (closed > 0) {
+      float h = head + (prev_key == lrow ? prev_scanned : 0.0f);
+      unsafeAtomicAdd(y + lrow, h);
+    }
+    if (next_lrow != row)
+      unsafeAtomicAdd(y + row, scanned);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// batch row recovery (sw_csr_row_at_position)
+__global__ __launch_bounds__(256) void csr_row_at_position_kernel(
+    const int32_t *__restrict__ ro, int32_t rows,
+    const int64_t *__restrict__ pos, int32_t *__restrict__ out,
+    int64_t count) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < count)
+    out[i] = row_search_lane(ro, 1u, (uint32_t)rows + 1u, (int32_t)pos[i]);
+}
+
+template <int G>
+void launch_group(dim3 grid, dim3 block, hipStream_t st, const int32_t *ro,
+                  const int32_t *col, const float *val, const float *x,
+                  float *y, int32_t rows) {
+  hipLaunchKernelGGL(spmv_group_per_row<G>, grid, block, 0, st, ro, col, val,
+                     x, y, rows);
+}
+
+template <int P, bool VEC>
+void launch_wave_position(dim3 grid, dim3 block, hipStream_t st,
+                          const int32_t *ro, const int32_t *col,
+                          const float *val, const float *x, float *y,
+                          int32_t rows, int32_t nnz, int64_t units,
+                          int64_t waves) {
+  hipLaunchKernelGGL((spmv_wave_position<P, VEC>), grid, block, 0, st, ro,
+                     col, val, x, y, rows, nnz, units, waves);
+}
+
+} // namespace
+
+namespace sw {
+
+int launch_fill_zero(float *y, int64_t n, int64_t block, hipStream_t st) {
+  if (n <= 0)
+    return SW_OK;
+  int64_t grid = ceil_div(n, block);
+  int rc = check_grid(grid, "output initialisation");
+  if (rc)
+    return rc;
+  hipLaunchKernelGGL(fill_zero_f32, dim3((unsigned)grid), dim3((unsigned)block),
+                     0, st, y, n);
+  return launch_check("output initialisation kernel");
+}
+
+int launch_spmv(const int32_t *ro, const int32_t *col, const float *val,
+                const float *x, float *y, int64_t rows, int64_t nnz,
+                const sw_options &o, hipStream_t st) {
+  const int64_t B = o.spmv_block_size;
+  const int32_t n = (int32_t)rows;
+  if (streq(o.spmv_mapping, "thread-per-row")) {
+    int64_t grid = std::max<int64_t>(ceil_div(rows, B), 1);
+    hipLaunchKernelGGL(spmv_thread_per_row, dim3((unsigned)grid),
+                       dim3((unsigned)B), 0, st, ro, col, val, x, y, n);
+    return launch_check("thread-per-row SpMV kernel");
+  }
+  if (streq(o.spmv_mapping, "wave-per-row")) {
+    const int64_t G = o.spmv_lanes_per_row;
+    int64_t grid = std::max<int64_t>(ceil_div(rows, B / G), 1);
+    int rc = check_grid(grid, "wave-per-row SpMV");
+    if (rc)
+      return rc;
+    dim3 g((unsigned)grid), b((unsigned)B);
+    switch (G) {
+    case 1: launch_group<1>(g, b, st, ro, col, val, x, y, n); break;
+    case 2: launch_group<2>(g, b, st, ro, col, val, x, y, n); break;
+    case 4: launch_group<4>(g, b, st, ro, col, val, x, y, n); break;
+    case 8: launch_group<8>(g, b, st, ro, col, val, x, y, n); break;
+    case 16: launch_group<16>(g, b, st, ro, col, val, x, y, n); break;
+    case 32: launch_group<32>(g, b, st, ro, col, val, x, y, n); break;
+    default: launch_group<64>(g, b, st, ro, col, val, x, y, n); break;
+    }
+    return launch_check("wave-per-row SpMV kernel");
+  }
+  if (streq(o.spmv_mapping, "block-per-row")) {
+    int64_t grid = std::max<int64_t>(rows, 1);
+    int rc = check_grid(grid, "block-per-row SpMV");
+    if (rc)
+      return rc;
+    hipLaunchKernelGGL(spmv_block_per_row, dim3((unsigned)grid),
+                       dim3((unsigned)B), 0, st, ro, col, val, x, y, n);
+    return launch_check("block-per-row SpMV kernel");
+  }
+  // position mappings: zero the output, then accumulate
+  int rc = launch_fill_zero(y, rows, o.spmv_block_size, st);
+  if (rc)
+    return rc;
+  if (streq(o.spmv_mapping, "thread-per-position")) {
+    if (nnz == 0)
+      return SW_OK;
+    const int64_t chunk = o.spmv_position_chunk_size;
+    int64_t workers = ceil_div(nnz, chunk);
+    int64_t grid = std::max<int64_t>(ceil_div(workers, B), 1);
+    rc = check_grid(grid, "thread-per-position SpMV");
+    if (rc)
+      return rc;
+    if (streq(o.spmv_position_reduction, "segmented"))
+      hipLaunchKernelGGL(spmv_thread_position_segmented, dim3((unsigned)grid),
+                         dim3((unsigned)B), 0, st, ro, col, val, x, y, n,
+                         (int32_t)nnz, (int32_t)std::min<int64_t>(chunk, nnz));
+    else
+      hipLaunchKernelGGL(spmv_thread_position_atomic, dim3((unsigned)grid),
+                         dim3((unsigned)B), 0, st, ro, col, val, x, y, n,
+                         (int32_t)nnz, (int32_t)std::min<int64_t>(chunk, nnz));
+    return launch_check("thread-per-position SpMV kernel");
+  }
+  // wave-per-position
+  if (nnz == 0)
+    return SW_OK;
+  const int64_t P = o.spmv_positions_per_lane;
+  const int64_t units = ceil_div(nnz, P);
+  const int64_t grid = std::max<int64_t>(ceil_div(units, B), 1);
+  rc = check_grid(grid, "wave-per-position SpMV");
+  if (rc)
+    return rc;
+  const int64_t waves = grid * (B / 64);
+  const bool vec = aligned16(col) && aligned16(val);
+  dim3 g((unsigned)grid), b((unsigned)B);
+  const int32_t z = (int32_t)nnz;
+  switch (P) {
+  case 1: launch_wave_position<1, false>(g, b, st, ro, col, val, x, y, n, z, units, waves); break;
+  case 2: launch_wave_position<2, false>(g, b, st, ro, col, val, x, y, n, z, units, waves); break;
+  case 4:
+    if (vec) launch_wave_position<4, true>(g, b, st, ro, col, val, x, y, n, z, units, waves);
+    else launch_wave_position<4, false>(g, b, st, ro, col, val, x, y, n, z, units, waves);
+    break;
+  case 8:
+    if (vec) launch_wave_position<8, true>(g, b, st, ro, col, val, x, y, n, z, units, waves);
+    else launch_wave_position<8, false>(g, b, st, ro, col, val, x, y, n, z, units, waves);
+    break;
+  default:
+    if (vec) launch_wave_position<16, true>(g, b, st, ro, col, val, x, y, n, z, units, waves);
+    else launch_wave_position<16, false>(g, b, st, ro, col, val, x, y, n, z, units, waves);
+    break;
+  }
+  return launch_check("wave-per-position SpMV kernel");
+}
+
+} // namespace sw
+
+extern "C" int sw_spmv_csr_f32(const int32_t *row_offsets,
+                               const int32_t *column_indices,
+                               const float *values, const float *vector,
+                               float *output, int64_t rows, int64_t cols,
+                               int64_t nnz, const sw_options *opts,
+                               void *stream) {
+  sw::clear_error();
+  sw_options o;
+  int rc = sw::resolve_options(opts, &o);
+  if (rc)
+    return rc;
+  rc = sw::check_csr(row_offsets, column_indices, values, rows, nnz, true);
+  if (rc)
+    return rc;
+  if (cols < 0)
+    return sw::fail(SW_ERR_INVALID_SHAPE, "expected non-negative columns");
+  if (rows == 0)
+    return SW_OK;
+  if (!output || (nnz > 0 && cols > 0 && !vector))
+    return sw::fail(SW_ERR_INVALID_ARGUMENT, "vector or output pointer is null");
+  return sw::launch_spmv(row_offsets, column_indices, values, vector, output,
+                         rows, nnz, o, sw::as_stream(stream));
+}
+
+extern "C" int sw_csr_row_at_position(const int32_t *row_offsets, int64_t rows,
+                                      const int64_t *positions,
+                                      int32_t *out_rows, int64_t count,
+                                      void *stream) {
+  sw::clear_error();
+  if (rows < 0 || count < 0 || rows > INT32_MAX - 1)
+    return sw::fail(SW_ERR_INVALID_SHAPE, "invalid rows or count");
+  if (count == 0)
+    return SW_OK;
+  if (!row_offsets || !positions || !out_rows)
+    return sw::fail(SW_ERR_INVALID_ARGUMENT, "null pointer");
+  int64_t grid = sw::ceil_div(count, 256);
+  int rc = sw::check_grid(grid, "row recovery");
+  if (rc)
+    return rc;
+  hipLaunchKernelGGL(csr_row_at_position_kernel, dim3((unsigned)grid),
+                     dim3(256), 0, sw::as_stream(stream), row_offsets,
+                     (int32_t)rows, positions, out_rows, count);
+  return sw::launch_check("row recovery kernel");
+}

@@ -1,0 +1,141 @@
+"""Host-side tests of the C ABI: the library loads, exports every function
+the header declares, and validates options and shapes the way the
+reference's passes do -- all without touching a GPU (each call here returns
+before any HIP call)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+import sparsewavecomp_amd as sw
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared_functions():
+    text = open(os.path.join(ROOT, "include", "sparsewave_amd.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(sw_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_symbols_exported():
+    lib = sw.load_library()
+    declared = _declared_functions()
+    assert len(declared) >= 15
+    for name in declared:
+        assert hasattr(lib, name), f"{name} declared but not exported"
+    assert set(declared) == set(sw.EXPORTED_SYMBOLS)
+
+
+def test_version():
+    assert b"gfx950" in sw.load_library().sw_version()
+
+
+def test_defaults_match_reference():
+    o = sw.Options()
+    # Pipelines.h:114-178 / Passes.td:207-241 defaults
+    assert o.spmv_mapping == "thread-per-row"
+    assert o.spmv_block_size == 256
+    assert o.spmm_mapping == "thread-per-output"
+    assert o.spmm_block_size == 256
+    assert o.spmm_tile_size == 4
+    assert o.spmv_position_chunk_size == 1
+    assert o.spmv_position_reduction == "atomic"
+    assert o.position_block_size == 256
+    assert o.sddmm_block_size == 256
+    assert o.row_reduction_block_size == 256
+    assert o.rowwise_map_block_size == 256
+    assert o.wavefront_size == 64
+    o.validate()
+
+
+def test_parse_pipeline_string():
+    o = sw.Options.parse(
+        "sparsewave-to-amdgpu-pipeline{chip=gfx950 wavefront-size=64 "
+        "spmv-mapping=wave-per-row spmv-block-size=128 spmm-mapping="
+        "wave-per-row-tile spmm-tile-size=8 rocm-path=/opt/rocm}")
+    assert o.spmv_mapping == "wave-per-row"
+    assert o.spmv_block_size == 128
+    assert o.spmm_mapping == "wave-per-row-tile"
+    assert o.spmm_tile_size == 8
+    o.validate()
+    # pass-level names map onto the same fields
+    o2 = sw.Options.parse("mapping=block-per-row block-size=512 wave-size=64")
+    assert o2.spmv_mapping == "block-per-row" and o2.spmv_block_size == 512
+
+
+@pytest.mark.parametrize("text,needle", [
+    ("spmv-mapping=diagonal", "unsupported SpMV mapping strategy 'diagonal'"),
+    ("spmm-mapping=row", "unsupported SpMM mapping strategy 'row'"),
+    ("spmv-block-size=0", "SpMV block size must be between 1 and 1024, but got 0"),
+    ("spmv-block-size=1025", "SpMV block size must be between 1 and 1024, but got 1025"),
+    ("position-block-size=0", "position-parallel block size must be between 1 and 1024"),
+    ("spmm-block-size=2000", "SpMM block size must be between 1 and 1024"),
+    ("spmm-tile-size=0", "SpMM tile size must be between 1 and 32, but got 0"),
+    ("spmm-tile-size=33", "SpMM tile size must be between 1 and 32, but got 33"),
+    ("sddmm-block-size=0", "SDDMM block size must be between 1 and 1024"),
+    ("row-reduction-block-size=0", "CSR row-reduction block size must be between"),
+    ("rowwise-map-block-size=0", "CSR row-wise map block size must be between"),
+    ("elementwise-block-size=0", "elementwise block size must be between"),
+    ("spmv-mapping=wave-per-row wavefront-size=32", "wave-per-row currently requires Wave64"),
+    ("spmm-mapping=wave-per-row-tile wavefront-size=32", "wave-per-row-tile currently requires Wave64"),
+    ("wavefront-size=32", "gfx950 executes Wave64 only"),
+    ("spmv-mapping=wave-per-row spmv-block-size=96", "wave-per-row requires the SpMV block size to be a multiple of 64, but got 96"),
+    ("spmv-mapping=block-per-row spmv-block-size=32", "block-per-row requires the SpMV block size to be a multiple of 64"),
+    ("spmm-mapping=wave-per-row-tile spmm-block-size=100", "wave-per-row-tile requires the SpMM block size to be a multiple of 64, but got 100"),
+    ("spmv-mapping=wave-per-position spmv-block-size=100", "wave position mapping requires the block size to be a multiple of 64"),
+    ("spmv-position-chunk-size=0", "thread position chunk size must be positive, but got 0"),
+    ("spmv-position-reduction=tree", "unsupported thread position reduction 'tree'"),
+    ("spmv-mapping=wave-per-position spmv-position-chunk-size=4", "thread position chunk size applies only to thread mapping"),
+    ("spmv-mapping=wave-per-position spmv-position-reduction=segmented", "thread position reduction applies only to thread mapping"),
+    ("spmv-lanes-per-row=3", "spmv-lanes-per-row must be a power of two"),
+    ("spmv-positions-per-lane=3", "spmv-positions-per-lane must be 1, 2, 4, 8 or 16"),
+])
+def test_invalid_options(text, needle):
+    o = sw.Options.parse(text)
+    with pytest.raises(sw.SparseWaveError) as e:
+        o.validate()
+    assert e.value.code == -1
+    assert needle in e.value.message
+
+
+def test_unknown_option_and_chip():
+    with pytest.raises(sw.SparseWaveError, match="unknown option 'bogus'"):
+        sw.Options.parse("bogus=1")
+    with pytest.raises(sw.SparseWaveError, match="chip=gfx1101"):
+        sw.Options.parse("chip=gfx1101")
+    with pytest.raises(sw.SparseWaveError, match="expects an integer"):
+        sw.Options.parse("spmv-block-size=abc")
+
+
+def test_entry_points_reject_before_launch():
+    """Invalid options / shapes / kinds fail before any device work."""
+    lib = sw.load_library()
+    bad = sw.Options(spmv_block_size=0)
+    P = ctypes.c_void_p
+    fake = P(16)  # never dereferenced: validation fails first
+    rc = lib.sw_spmv_csr_f32(fake, fake, fake, fake, fake, 4, 4, 4, bad.ref,
+                             None)
+    assert rc == -1
+    assert b"SpMV block size" in lib.sw_last_error()
+    rc = lib.sw_spmv_csr_f32(fake, fake, fake, fake, fake, -1, 4, 4, None,
+                             None)
+    assert rc == -2
+    rc = lib.sw_spmv_csr_f32(None, fake, fake, fake, fake, 4, 4, 4, None, None)
+    assert rc == -3
+    rc = lib.sw_bsr_spmm_f32(fake, fake, fake, fake, fake, 10, 10, 1, 2, 4,
+                             None, None)
+    assert rc == -2 and b"divisible" in lib.sw_last_error()
+    rc = lib.sw_csr_row_reduce_f32(fake, None, fake, fake, 4, 4, b"min", None,
+                                   None)
+    assert rc == -3 and b"'sum' or 'max'" in lib.sw_last_error()
+    rc = lib.sw_csr_rowwise_map_f32(fake, None, fake, fake, fake, 4, 4, 9,
+                                    None, None)
+    assert rc == -3
+    rc = lib.sw_sddmm_csr_f32(fake, fake, fake, fake, fake, fake, 4, 4, 4, 4,
+                              7, 1.0, 0.0, None, None)
+    assert rc == -3
+    # empty problems are no-ops that never launch
+    assert lib.sw_spmv_csr_f32(fake, None, None, None, None, 0, 0, 0, None,
+                               None) == 0

@@ -1,0 +1,242 @@
+"""GPU parity of BSR SpMM (thread-per-output and MFMA, fp32 and bf16), SDDMM,
+CSR row reduce / row-wise map and the six-kernel sparse attention chain."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import sparsewavecomp_amd as sw
+from sparsewavecomp_amd import workloads as W
+from tests import gpu_util as G
+from tests._check import BF16_REL_L2, assert_within_bound, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+
+def _bsr_run(bsr, rhs, opts, bf16=False):
+    G.say(f"bsr rows={bsr.rows} nnzb={bsr.nnzb} b={bsr.block_size} "
+          f"k={rhs.shape[1]} bf16={bf16} opts='{opts}'")
+    dt = torch.bfloat16 if bf16 else None
+    out = torch.full((bsr.rows, rhs.shape[1]), float("nan"), device=G.DEV)
+    sw.bsr_spmm(G.t(bsr.block_row_offsets), G.t(bsr.block_column_indices),
+                G.t(bsr.block_values, dt), G.t(rhs, dt), out,
+                bsr.block_size, options=opts)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+BSR_OPTS = ["bsr-use-mfma=1", "bsr-use-mfma=0",
+            "bsr-use-mfma=0 spmm-block-size=64"]
+
+
+@pytest.mark.parametrize("opts", BSR_OPTS)
+def test_bsr_golden(dev, golden, opts):
+    g = golden["bsr_spmm"]
+    bsr = W.BSR(g["rows"], g["cols"], g["block_size"],
+                np.array(g["block_row_offsets"], np.int32),
+                np.array(g["block_column_indices"], np.int32),
+                np.array(g["block_values"], np.float32))
+    out = _bsr_run(bsr, np.array(g["rhs"], np.float32), opts)
+    np.testing.assert_array_equal(out, np.array(g["expected"], np.float32))
+
+
+@pytest.mark.parametrize("opts", BSR_OPTS)
+@pytest.mark.parametrize("b,k", [(16, 128), (16, 40), (16, 200), (4, 9)])
+def test_bsr_fp32(dev, orc, opts, b, k):
+    bsr = W.bsr_banded(seed=b + k, rows=b * 96, block_size=b,
+                       blocks_per_row=6, band=3, band_blocks=3,
+                       value_std=0.5)
+    rhs = np.random.default_rng(k).standard_normal((bsr.cols, k)).astype(
+        np.float32)
+    out = _bsr_run(bsr, rhs, opts)
+    ref = orc.bsr_spmm(bsr.block_row_offsets, bsr.block_column_indices,
+                       bsr.block_values, rhs, b)
+    bound = orc.bsr_abs_bound(bsr.block_row_offsets, bsr.block_column_indices,
+                              bsr.block_values, rhs, b)
+    assert_within_bound(out, ref, bound)
+
+
+@pytest.mark.parametrize("opts", ["bsr-use-mfma=1", "bsr-use-mfma=0"])
+def test_bsr_bf16(dev, orc, opts):
+    bsr = W.bsr_banded(seed=3, rows=16 * 128, block_size=16)
+    rhs = np.random.default_rng(3).standard_normal((bsr.cols, 128)).astype(
+        np.float32)
+    out = _bsr_run(bsr, rhs, opts, bf16=True)
+    ref = orc.bsr_spmm(bsr.block_row_offsets, bsr.block_column_indices,
+                       bsr.block_values, rhs, 16)
+    assert rel_l2(out, ref) <= BF16_REL_L2
+    # against the oracle on bf16-rounded inputs the fp32 bound holds
+    vb, rb = G.bf16_round(bsr.block_values), G.bf16_round(rhs)
+    ref_b = orc.bsr_spmm(bsr.block_row_offsets, bsr.block_column_indices, vb,
+                         rb, 16)
+    bound = orc.bsr_abs_bound(bsr.block_row_offsets, bsr.block_column_indices,
+                              vb, rb, 16)
+    assert_within_bound(out, ref_b, bound)
+
+
+def test_bsr_config4_sample(dev, orc):
+    bsr, rhs = W.config4(seed=0)
+    out = _bsr_run(bsr, rhs, "bsr-use-mfma=1")
+    # check 400 block rows (first, last, random) of the full-size product
+    brs = np.unique(np.concatenate([
+        [0, 1, bsr.rows // 16 - 1],
+        np.random.default_rng(0).choice(bsr.rows // 16, 400, replace=False)]))
+    bro = bsr.block_row_offsets
+    counts = bro[brs + 1] - bro[brs]
+    sub_ro = np.zeros(brs.size + 1, np.int64)
+    np.cumsum(counts, out=sub_ro[1:])
+    idx = np.concatenate([np.arange(bro[b], bro[b + 1]) for b in brs])
+    sub_vals = bsr.block_values.reshape(-1, 256)[idx].ravel()
+    ref = orc.bsr_spmm(sub_ro.astype(np.int32), bsr.block_column_indices[idx],
+                       sub_vals, rhs, 16)
+    bound = orc.bsr_abs_bound(sub_ro.astype(np.int32),
+                              bsr.block_column_indices[idx], sub_vals, rhs, 16)
+    rows = (brs[:, None] * 16 + np.arange(16)[None, :]).ravel()
+    assert_within_bound(out[rows], ref, bound)
+
+
+# ---- SDDMM / row reduce / row-wise map / attention -------------------------
+
+ROW_OPTS = ["", "sddmm-lanes-per-row=64", "sddmm-block-size=64"]
+
+
+@pytest.mark.parametrize("opts", ROW_OPTS)
+def test_sddmm_golden_and_random(dev, orc, golden, opts):
+    g = golden["sddmm"]
+    ro = np.array(g["row_offsets"], np.int32)
+    col = np.array(g["column_indices"], np.int32)
+    val = np.array(g["values"], np.float32)
+    lhs = np.array(g["lhs"], np.float32)
+    rhs = np.array(g["rhs"], np.float32)
+    out = torch.empty(3, device=G.DEV)
+    G.say(f"sddmm golden opts='{opts}'")
+    sw.sddmm(G.t(ro), G.t(col), G.t(val), G.t(lhs), G.t(rhs), out,
+             sw.SDDMM_MUL, options=opts)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(out.cpu().numpy(), g["expected"])
+    csr = W.random_csr(500, 300, 40.0, 2, empty_fraction=0.2)
+    rng = np.random.default_rng(2)
+    for kdim in (1, 64, 100):
+        lhs = rng.standard_normal((500, kdim)).astype(np.float32)
+        rhs = rng.standard_normal((kdim, 300)).astype(np.float32)
+        for kind in (sw.SDDMM_MUL, sw.SDDMM_AFFINE, sw.SDDMM_DOT):
+            out = torch.empty(csr.nnz, device=G.DEV)
+            G.say(f"sddmm kdim={kdim} kind={kind} opts='{opts}'")
+            sw.sddmm(G.t(csr.row_offsets), G.t(csr.column_indices),
+                     G.t(csr.values), G.t(lhs), G.t(rhs), out, kind, 0.3, 0.7,
+                     options=opts)
+            torch.cuda.synchronize()
+            ref = orc.sddmm(csr.row_offsets, csr.column_indices, csr.values,
+                            lhs, rhs, kind, 0.3, 0.7)
+            rows = np.repeat(np.arange(500), np.diff(csr.row_offsets))
+            absd = np.abs(lhs.astype(np.float64)) @ np.abs(
+                rhs.astype(np.float64))
+            b = absd[rows, csr.column_indices]
+            v = np.abs(csr.values.astype(np.float64))
+            bound = {sw.SDDMM_MUL: v * b, sw.SDDMM_AFFINE: 0.7 * v + 0.3 * b,
+                     sw.SDDMM_DOT: b}[kind]
+            assert_within_bound(out.cpu().numpy(), ref, bound + 1e-30)
+
+
+@pytest.mark.parametrize("opts", ROW_OPTS)
+def test_row_reduce_and_map(dev, orc, golden, opts):
+    g = golden["row_reduce"]
+    ro = G.t(np.array(g["row_offsets"], np.int32))
+    val = G.t(np.array(g["values"], np.float32))
+    s = torch.empty(3, device=G.DEV)
+    m = torch.empty(3, device=G.DEV)
+    G.say(f"row_reduce golden opts='{opts}'")
+    sw.csr_row_reduce(ro, None, val, s, "sum", options=opts)
+    sw.csr_row_reduce(ro, None, val, m, "max", options=opts)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(s.cpu().numpy(), g["expected_sum"])
+    np.testing.assert_array_equal(
+        m.cpu().numpy(), [float(v) for v in g["expected_max"]])
+    # softmax golden through the four row ops
+    gs = golden["softmax"]
+    e = torch.empty(4, device=G.DEV)
+    sw.csr_rowwise_map(ro, None, val, m, e, sw.MAP_EXP_SUB, options=opts)
+    sw.csr_row_reduce(ro, None, e, s, "sum", options=opts)
+    sw.csr_rowwise_map(ro, None, e, s, e, sw.MAP_DIV, options=opts)
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(e.cpu().numpy(), gs["expected"], rtol=0,
+                               atol=5e-7)
+    # random rows, NaN propagation in max
+    csr = W.random_csr(2000, 500, 30.0, 7, empty_fraction=0.2,
+                       lognormal=True, max_len=500)
+    vals = csr.values.copy()
+    vals[5] = np.nan
+    out = torch.empty(csr.rows, device=G.DEV)
+    for kind, okind in (("sum", orc.REDUCE_SUM), ("max", orc.REDUCE_MAX)):
+        sw.csr_row_reduce(G.t(csr.row_offsets), None, G.t(vals), out, kind,
+                          options=opts)
+        torch.cuda.synchronize()
+        ref = orc.row_reduce(csr.row_offsets, vals, okind)
+        got = out.cpu().numpy()
+        np.testing.assert_array_equal(np.isnan(got), np.isnan(ref))
+        ok = ~np.isnan(ref)
+        if kind == "max":
+            np.testing.assert_array_equal(got[ok], ref[ok])
+        else:
+            lens = np.diff(csr.row_offsets)
+            absb = np.array([np.abs(vals[a:b]).sum() for a, b in
+                             zip(csr.row_offsets[:-1], csr.row_offsets[1:])])
+            assert np.all(np.abs(got[ok] - ref[ok]) <= 1e-5 * absb[ok] + 0)
+            del lens
+    rowv = np.random.default_rng(1).uniform(0.5, 2, csr.rows).astype(
+        np.float32)
+    for kind in (sw.MAP_EXP_SUB, sw.MAP_DIV, sw.MAP_SUB, sw.MAP_MUL):
+        o = torch.empty(csr.nnz, device=G.DEV)
+        sw.csr_rowwise_map(G.t(csr.row_offsets), None, G.t(csr.values),
+                           G.t(rowv), o, kind, options=opts)
+        torch.cuda.synchronize()
+        ref = orc.rowwise_map(csr.row_offsets, csr.values, rowv, kind)
+        np.testing.assert_allclose(o.cpu().numpy(), ref, rtol=2e-6, atol=1e-7)
+
+
+def _attention(mask, q, kt, v, alpha, opts):
+    G.say(f"attention rows={mask.rows} nnz={mask.nnz} opts='{opts}'")
+    rows = mask.rows
+    scores = torch.empty(mask.nnz, device=G.DEV)
+    rmax = torch.empty(rows, device=G.DEV)
+    rsum = torch.empty(rows, device=G.DEV)
+    out = torch.full((rows, v.shape[1]), float("nan"), device=G.DEV)
+    sw.sparse_attention(G.t(mask.row_offsets), G.t(mask.column_indices),
+                        G.t(mask.values), G.t(q), G.t(kt), G.t(v), scores,
+                        rmax, rsum, out, alpha, 0.0, options=opts)
+    torch.cuda.synchronize()
+    return out.cpu().numpy(), scores.cpu().numpy()
+
+
+ATT_OPTS = ["", "sddmm-lanes-per-row=64 spmm-mapping=wave-per-row-tile "
+            "spmm-tile-size=32 spmm-lanes-per-row=16"]
+
+
+@pytest.mark.parametrize("opts", ATT_OPTS)
+def test_attention_golden(dev, golden, opts):
+    g = golden["attention"]
+    mask = W.CSR(2, 3, np.array(g["row_offsets"], np.int32),
+                 np.array(g["column_indices"], np.int32),
+                 np.array(g["mask_values"], np.float32))
+    out, _ = _attention(mask, np.array(g["query"], np.float32),
+                        np.array(g["transposed_key"], np.float32),
+                        np.array(g["value"], np.float32), g["alpha"], opts)
+    np.testing.assert_allclose(np.floor(out.astype(np.float64) * 1e4) / 1e4,
+                               g["expected"], rtol=0, atol=1e-9)
+
+
+@pytest.mark.parametrize("opts", ATT_OPTS)
+@pytest.mark.parametrize("seq", [1024, 8192])
+def test_attention_config5(dev, orc, opts, seq):
+    mask, q, kt, v, alpha = W.config5(seed=0, seq=seq)
+    out, scores = _attention(mask, q, kt, v, alpha, opts)
+    s_ref, _, _, ref = orc.sparse_attention(mask.row_offsets,
+                                            mask.column_indices, mask.values,
+                                            q, kt, v, alpha)
+    # probabilities are in [0, 1]: bound by sum_p |P_rp V_pc|
+    bound = orc.spmm_abs_bound(mask.row_offsets, mask.column_indices, s_ref,
+                               v)
+    assert_within_bound(out, ref, bound, rel=2e-5)
+    np.testing.assert_allclose(scores, s_ref, rtol=1e-4, atol=1e-6)
+    assert math.isfinite(float(out.sum()))

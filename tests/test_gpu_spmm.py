@@ -1,0 +1,89 @@
+"""GPU parity of sparsewave.spmm (thread-per-output, wave-per-row-tile,
+thread-per-position) against the CPU oracle, per output element
+|C - C_ref| <= 1e-5 * sum_p |a_rp * B[col_p, c]|."""
+import numpy as np
+import pytest
+
+from sparsewavecomp_amd import workloads as W
+from tests import gpu_util as G
+from tests._check import assert_within_bound
+
+pytestmark = pytest.mark.gpu
+
+MAPPINGS = [
+    "spmm-mapping=thread-per-output",
+    "spmm-mapping=thread-per-output spmm-block-size=96",
+    "spmm-mapping=wave-per-row-tile",
+    "spmm-mapping=wave-per-row-tile spmm-tile-size=1",
+    "spmm-mapping=wave-per-row-tile spmm-tile-size=2",
+    "spmm-mapping=wave-per-row-tile spmm-tile-size=3",
+    "spmm-mapping=wave-per-row-tile spmm-tile-size=8",
+    "spmm-mapping=wave-per-row-tile spmm-tile-size=16",
+    "spmm-mapping=wave-per-row-tile spmm-tile-size=32",
+    "spmm-mapping=wave-per-row-tile spmm-tile-size=4 spmm-lanes-per-row=16",
+    "spmm-mapping=wave-per-row-tile spmm-tile-size=4 spmm-lanes-per-row=4",
+    "spmm-mapping=wave-per-row-tile spmm-tile-size=32 spmm-lanes-per-row=8",
+    "spmm-mapping=wave-per-row-tile spmm-tile-size=5 spmm-block-size=128",
+    "spmm-mapping=thread-per-position",
+    "spmm-mapping=thread-per-position spmm-position-chunk-size=3",
+]
+
+
+def _check(orc, csr, rhs, out):
+    ref = orc.spmm(csr.row_offsets, csr.column_indices, csr.values, rhs)
+    bound = orc.spmm_abs_bound(csr.row_offsets, csr.column_indices,
+                               csr.values, rhs)
+    assert_within_bound(out, ref, bound)
+
+
+@pytest.mark.parametrize("opts", MAPPINGS)
+@pytest.mark.parametrize("case", ["spmm", "spmm_torch_example"])
+def test_golden(dev, golden, opts, case):
+    g = golden[case]
+    csr = W.CSR(g["rows"], g["cols"], np.array(g["row_offsets"], np.int32),
+                np.array(g["column_indices"], np.int32),
+                np.array(g["values"], np.float32))
+    out = G.spmm(csr, np.array(g["rhs"], np.float32), opts)
+    np.testing.assert_array_equal(out, np.array(g["expected"], np.float32))
+
+
+@pytest.mark.parametrize("opts", MAPPINGS)
+@pytest.mark.parametrize("k", [1, 4, 7, 64])
+def test_ragged(dev, orc, opts, k):
+    csr = W.random_csr(700, 600, 15.0, k, empty_fraction=0.25,
+                       max_len=600, lognormal=True)
+    rhs = np.random.default_rng(k).uniform(-1, 1, (600, k)).astype(np.float32)
+    _check(orc, csr, rhs, G.spmm(csr, rhs, opts))
+
+
+@pytest.fixture(scope="module")
+def config3():
+    csr, _ = W.config2(seed=0)
+    return csr
+
+
+@pytest.mark.parametrize("k,opts", [
+    (4, "spmm-mapping=wave-per-row-tile spmm-tile-size=4"),
+    (4, "spmm-mapping=wave-per-row-tile spmm-tile-size=4 spmm-lanes-per-row=16"),
+    (64, "spmm-mapping=wave-per-row-tile spmm-tile-size=32 spmm-lanes-per-row=16"),
+])
+def test_config3_full_size(dev, orc, config3, k, opts):
+    csr = config3
+    rhs = W.config3_rhs(csr.cols, k, seed=0)
+    out = G.spmm(csr, rhs, opts)
+    # full-size check on a row sample keeps the oracle within seconds
+    rows = np.sort(np.random.default_rng(k).choice(csr.rows, 20000,
+                                                   replace=False))
+    rows = np.concatenate([rows, np.argsort(np.diff(csr.row_offsets))[-50:]])
+    sub = _row_subset(csr, rows)
+    _check(orc, sub, rhs, out[rows])
+
+
+def _row_subset(csr, rows):
+    ro = csr.row_offsets
+    lengths = (ro[rows + 1] - ro[rows]).astype(np.int64)
+    new_ro = np.zeros(rows.size + 1, np.int64)
+    np.cumsum(lengths, out=new_ro[1:])
+    idx = np.concatenate([np.arange(ro[r], ro[r + 1]) for r in rows])
+    return W.CSR(rows.size, csr.cols, new_ro.astype(np.int32),
+                 csr.column_indices[idx], csr.values[idx])

@@ -1,0 +1,351 @@
+"""Pins of the CPU oracle (oracle/sw_oracle.c).
+
+Each oracle function is checked against (a) the golden vectors of the
+reference's own runtime tests, (b) an independent computation (scipy.sparse,
+dense numpy in float64, numpy.searchsorted, brute force), and (c) mutation
+cases showing that a plausible mistake -- a dropped term, a transposed
+operand, a wrong index -- fails the same check.
+"""
+import math
+
+import numpy as np
+import pytest
+import scipy.sparse as sp
+
+from sparsewavecomp_amd import workloads as W
+from tests._check import assert_within_bound, rel_l2
+
+
+def _csr(g):
+    return (np.array(g["row_offsets"], np.int32),
+            np.array(g["column_indices"], np.int32),
+            np.array(g["values"], np.float32))
+
+
+def _scipy(csr):
+    return sp.csr_matrix((csr.values.astype(np.float64),
+                          csr.column_indices, csr.row_offsets),
+                         shape=(csr.rows, csr.cols))
+
+
+# ---- golden vectors ------------------------------------------------------
+
+
+def test_golden_spmv(orc, golden):
+    g = golden["spmv"]
+    ro, col, val = _csr(g)
+    y = orc.spmv(ro, col, val, np.array(g["vector"], np.float32))
+    np.testing.assert_array_equal(y, np.array(g["expected"], np.float32))
+    y = orc.spmv_wave_position(ro, col, val, np.array(g["vector"], np.float32))
+    np.testing.assert_array_equal(y, np.array(g["expected"], np.float32))
+
+
+@pytest.mark.parametrize("case", ["spmm", "spmm_torch_example"])
+def test_golden_spmm(orc, golden, case):
+    g = golden[case]
+    ro, col, val = _csr(g)
+    out = orc.spmm(ro, col, val, np.array(g["rhs"], np.float32))
+    np.testing.assert_array_equal(out, np.array(g["expected"], np.float32))
+
+
+def test_golden_bsr(orc, golden):
+    g = golden["bsr_spmm"]
+    out = orc.bsr_spmm(np.array(g["block_row_offsets"], np.int32),
+                       np.array(g["block_column_indices"], np.int32),
+                       np.array(g["block_values"], np.float32),
+                       np.array(g["rhs"], np.float32), g["block_size"])
+    np.testing.assert_array_equal(out, np.array(g["expected"], np.float32))
+
+
+def test_golden_sddmm(orc, golden):
+    g = golden["sddmm"]
+    ro, col, val = _csr(g)
+    out = orc.sddmm(ro, col, val, np.array(g["lhs"], np.float32),
+                    np.array(g["rhs"], np.float32), orc.SDDMM_MUL)
+    np.testing.assert_array_equal(out, np.array(g["expected"], np.float32))
+
+
+def test_golden_row_reduce(orc, golden):
+    g = golden["row_reduce"]
+    ro, _, val = _csr(g)
+    np.testing.assert_array_equal(orc.row_reduce(ro, val, orc.REDUCE_SUM),
+                                  np.array(g["expected_sum"], np.float32))
+    want = np.array([float(v) for v in g["expected_max"]], np.float32)
+    np.testing.assert_array_equal(orc.row_reduce(ro, val, orc.REDUCE_MAX),
+                                  want)
+
+
+def test_golden_softmax(orc, golden):
+    g = golden["softmax"]
+    ro, _, val = _csr(g)
+    m = orc.row_reduce(ro, val, orc.REDUCE_MAX)
+    e = orc.rowwise_map(ro, val, m, orc.MAP_EXP_SUB)
+    s = orc.row_reduce(ro, e, orc.REDUCE_SUM)
+    p = orc.rowwise_map(ro, e, s, orc.MAP_DIV)
+    # the reference prints 6 significant digits
+    np.testing.assert_allclose(p, g["expected"], rtol=0, atol=5e-7)
+
+
+def test_golden_attention(orc, golden):
+    g = golden["attention"]
+    ro = np.array(g["row_offsets"], np.int32)
+    col = np.array(g["column_indices"], np.int32)
+    _, _, _, out = orc.sparse_attention(
+        ro, col, np.array(g["mask_values"], np.float32),
+        np.array(g["query"], np.float32),
+        np.array(g["transposed_key"], np.float32),
+        np.array(g["value"], np.float32), g["alpha"], g["beta"])
+    want = np.array(g["expected"], np.float64)
+    # CHECK matches 4.2177..., 5.2177..., 3, 4: compare the printed prefix
+    np.testing.assert_allclose(
+        np.floor(out.astype(np.float64) * 1e4) / 1e4, want, rtol=0, atol=1e-9)
+
+
+# ---- independent computations on random inputs ----------------------------
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_spmv_matches_scipy(orc, seed):
+    csr = W.random_csr(300, 200, 12.0, seed, empty_fraction=0.2)
+    x = np.random.default_rng(seed).uniform(-1, 1, 200).astype(np.float32)
+    y = orc.spmv(csr.row_offsets, csr.column_indices, csr.values, x)
+    exact = _scipy(csr) @ x.astype(np.float64)
+    bound = orc.spmv_abs_bound(csr.row_offsets, csr.column_indices,
+                               csr.values, x)
+    assert_within_bound(y, exact, bound)
+    # bound is sum|a*x| computed independently
+    np.testing.assert_allclose(bound, abs(_scipy(csr)) @ np.abs(x), rtol=1e-12)
+
+
+def test_spmv_mutations_fail(orc):
+    csr = W.random_csr(200, 150, 10.0, 5, empty_fraction=0.1)
+    x = np.random.default_rng(5).uniform(-1, 1, 150).astype(np.float32)
+    exact = _scipy(csr) @ x.astype(np.float64)
+    bound = orc.spmv_abs_bound(csr.row_offsets, csr.column_indices,
+                               csr.values, x)
+    mutants = {
+        "reversed vector": orc.spmv(csr.row_offsets, csr.column_indices,
+                                    csr.values, x[::-1].copy()),
+        "dropped last term": orc.spmv(
+            csr.row_offsets, csr.column_indices,
+            np.where(np.isin(np.arange(csr.nnz), csr.row_offsets[1:] - 1),
+                     0, csr.values).astype(np.float32), x),
+        "shifted row offsets": orc.spmv(
+            np.minimum(csr.row_offsets + 1, csr.nnz).astype(np.int32),
+            csr.column_indices, csr.values, x),
+    }
+    for name, y in mutants.items():
+        with pytest.raises(AssertionError):
+            assert_within_bound(y, exact, bound, what=name)
+
+
+@pytest.mark.parametrize("k", [1, 4, 7])
+def test_spmm_matches_scipy(orc, k):
+    csr = W.random_csr(120, 90, 8.0, 11, empty_fraction=0.2)
+    rhs = np.random.default_rng(3).uniform(-1, 1, (90, k)).astype(np.float32)
+    out = orc.spmm(csr.row_offsets, csr.column_indices, csr.values, rhs)
+    exact = _scipy(csr) @ rhs.astype(np.float64)
+    bound = orc.spmm_abs_bound(csr.row_offsets, csr.column_indices,
+                               csr.values, rhs)
+    assert_within_bound(out, exact, bound)
+    if k > 1:  # transposed-operand mutation: reversing rhs columns must fail
+        with pytest.raises(AssertionError):
+            assert_within_bound(out[:, ::-1], exact, bound)
+
+
+def _bsr_dense(bsr):
+    b = bsr.block_size
+    dense = np.zeros((bsr.rows, bsr.cols), np.float64)
+    blocks = bsr.block_values.reshape(-1, b, b)
+    for br in range(bsr.rows // b):
+        for bp in range(bsr.block_row_offsets[br],
+                        bsr.block_row_offsets[br + 1]):
+            bc = bsr.block_column_indices[bp]
+            dense[br * b:(br + 1) * b, bc * b:(bc + 1) * b] = blocks[bp]
+    return dense
+
+
+@pytest.mark.parametrize("b", [2, 4, 16])
+def test_bsr_matches_dense(orc, b):
+    bsr = W.bsr_banded(seed=b, rows=b * 24, block_size=b, blocks_per_row=5,
+                       band=2, band_blocks=2, value_std=1.0)
+    rhs = np.random.default_rng(b).standard_normal((bsr.cols, 6)).astype(
+        np.float32)
+    out = orc.bsr_spmm(bsr.block_row_offsets, bsr.block_column_indices,
+                       bsr.block_values, rhs, b)
+    dense = _bsr_dense(bsr)
+    exact = dense @ rhs.astype(np.float64)
+    bound = np.abs(dense) @ np.abs(rhs.astype(np.float64))
+    assert_within_bound(out, exact, bound)
+    np.testing.assert_allclose(
+        orc.bsr_abs_bound(bsr.block_row_offsets, bsr.block_column_indices,
+                          bsr.block_values, rhs, b), bound, rtol=1e-12)
+    # transposed blocks must fail
+    tb = bsr.block_values.reshape(-1, b, b).transpose(0, 2, 1).ravel()
+    bad = orc.bsr_spmm(bsr.block_row_offsets, bsr.block_column_indices, tb,
+                       rhs, b)
+    with pytest.raises(AssertionError):
+        assert_within_bound(bad, exact, bound)
+
+
+def test_sddmm_matches_dense(orc):
+    csr = W.random_csr(50, 40, 9.0, 21, empty_fraction=0.2)
+    rng = np.random.default_rng(21)
+    lhs = rng.standard_normal((50, 16)).astype(np.float32)
+    rhs = rng.standard_normal((16, 40)).astype(np.float32)
+    dense = lhs.astype(np.float64) @ rhs.astype(np.float64)
+    absd = np.abs(lhs.astype(np.float64)) @ np.abs(rhs.astype(np.float64))
+    rows = np.repeat(np.arange(50), np.diff(csr.row_offsets))
+    dot = dense[rows, csr.column_indices]
+    bound = absd[rows, csr.column_indices]
+    v = csr.values.astype(np.float64)
+    for kind, want, scale in [
+            (orc.SDDMM_MUL, v * dot, np.abs(v) * bound),
+            (orc.SDDMM_DOT, dot, bound),
+            (orc.SDDMM_AFFINE, 0.5 * v + 0.25 * dot,
+             0.5 * np.abs(v) + 0.25 * bound)]:
+        out = orc.sddmm(csr.row_offsets, csr.column_indices, csr.values, lhs,
+                        rhs, kind, 0.25, 0.5)
+        assert_within_bound(out, want, scale + 1e-30)
+    # using lhs rows of the wrong row (index mistake) must fail
+    out = orc.sddmm(csr.row_offsets, csr.column_indices, csr.values,
+                    lhs[::-1].copy(), rhs, orc.SDDMM_DOT)
+    with pytest.raises(AssertionError):
+        assert_within_bound(out, dot, bound)
+
+
+def test_row_reduce_and_map_match_numpy(orc):
+    csr = W.random_csr(80, 60, 6.0, 31, empty_fraction=0.3)
+    ro, v = csr.row_offsets, csr.values
+    s = orc.row_reduce(ro, v, orc.REDUCE_SUM)
+    m = orc.row_reduce(ro, v, orc.REDUCE_MAX)
+    for r in range(csr.rows):
+        seg = v[ro[r]:ro[r + 1]].astype(np.float64)
+        assert abs(s[r] - seg.sum()) <= 1e-6 * max(1.0, np.abs(seg).sum())
+        assert m[r] == (seg.max() if seg.size else -np.inf)
+    # NaN propagates through max (arith.maximumf)
+    v2 = v.copy()
+    if csr.nnz:
+        v2[ro[np.argmax(np.diff(ro) > 0)]] = np.nan
+        assert np.isnan(orc.row_reduce(ro, v2, orc.REDUCE_MAX)).any()
+    rowv = np.random.default_rng(1).uniform(0.5, 2, csr.rows).astype(
+        np.float32)
+    rows = np.repeat(np.arange(csr.rows), np.diff(ro))
+    for kind, fn in [(orc.MAP_EXP_SUB, lambda a, b: np.exp(a - b)),
+                     (orc.MAP_DIV, lambda a, b: a / b),
+                     (orc.MAP_SUB, lambda a, b: a - b),
+                     (orc.MAP_MUL, lambda a, b: a * b)]:
+        out = orc.rowwise_map(ro, v, rowv, kind)
+        want = fn(v.astype(np.float64), rowv[rows].astype(np.float64))
+        np.testing.assert_allclose(out, want, rtol=2e-6, atol=1e-7)
+
+
+def _dense_attention(mask, q, kt, v, alpha):
+    rows = np.repeat(np.arange(mask.rows), np.diff(mask.row_offsets))
+    s = alpha * (q.astype(np.float64) @ kt.astype(np.float64))
+    dense = np.full((mask.rows, mask.cols), -np.inf)
+    dense[rows, mask.column_indices] = s[rows, mask.column_indices]
+    mx = dense.max(axis=1, keepdims=True)
+    mx[~np.isfinite(mx)] = 0
+    e = np.exp(dense - mx)
+    den = e.sum(axis=1, keepdims=True)
+    den[den == 0] = 1
+    p = e / den
+    return p @ v.astype(np.float64), np.abs(p) @ np.abs(v.astype(np.float64))
+
+
+def test_attention_matches_dense_softmax(orc):
+    mask = W.attention_mask(seq=256, block=16, window=3, random_blocks=2,
+                            seed=4)
+    rng = np.random.default_rng(4)
+    q = rng.standard_normal((256, 8)).astype(np.float32)
+    k = rng.standard_normal((256, 8)).astype(np.float32)
+    v = rng.standard_normal((256, 8)).astype(np.float32)
+    kt = np.ascontiguousarray(k.T)
+    alpha = 1 / math.sqrt(8)
+    _, _, _, out = orc.sparse_attention(mask.row_offsets, mask.column_indices,
+                                        mask.values, q, kt, v, alpha)
+    want, bound = _dense_attention(mask, q, kt, v, alpha)
+    assert_within_bound(out, want, bound, rel=2e-5)
+    # a non-transposed key (operand mistake) must fail
+    _, _, _, bad = orc.sparse_attention(mask.row_offsets, mask.column_indices,
+                                        mask.values, q, np.ascontiguousarray(
+                                            kt.reshape(256, 8).T), v, alpha)
+    with pytest.raises(AssertionError):
+        assert_within_bound(bad, want, bound, rel=2e-5)
+
+
+# ---- index work: bit-exact ------------------------------------------------
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_row_search_matches_searchsorted(orc, seed):
+    csr = W.random_csr(500, 100, 3.0, seed, empty_fraction=0.4)
+    pos = np.arange(csr.nnz, dtype=np.int64)
+    rows = orc.rows_at_positions(csr.row_offsets, pos)
+    want = np.searchsorted(csr.row_offsets[1:], pos, side="right")
+    np.testing.assert_array_equal(rows, want)
+    # brute force: ro[r] <= p < ro[r+1]
+    ro = csr.row_offsets
+    assert np.all(ro[rows] <= pos) and np.all(pos < ro[rows + 1])
+
+
+def test_row_search_tiny_bruteforce(orc):
+    ro = np.array([0, 0, 3, 3, 3, 4, 8, 8], np.int32)
+    for p in range(8):
+        want = [r for r in range(7) if ro[r] <= p < ro[r + 1]][0]
+        assert orc.rows_at_positions(ro, [p])[0] == want
+
+
+@pytest.mark.parametrize("span,workers", [(0, 3), (10, 3), (64, 64),
+                                          (1000, 37), (7, 10)])
+def test_position_space_partition(orc, span, workers):
+    lo = 5
+    parts = [orc.position_space(lo, lo + span, w, workers)
+             for w in range(workers)]
+    assert parts[0][0] == lo and parts[-1][1] == lo + span
+    for (b0, e0), (b1, _) in zip(parts, parts[1:]):
+        assert e0 == b1
+    sizes = [e - b for b, e in parts]
+    assert max(sizes) - min(sizes) <= 1
+    assert sizes == sorted(sizes, reverse=True)
+
+
+def test_wave_segmented_scan_bruteforce(orc):
+    rng = np.random.default_rng(9)
+    for wave in (32, 64):
+        for _ in range(20):
+            n_active = int(rng.integers(0, wave + 1))
+            keys = np.sort(rng.integers(0, 6, wave)).astype(np.int64)
+            vals = rng.integers(-4, 5, wave).astype(np.float32)
+            act = np.arange(wave) < n_active
+            out, seg = orc.wave_segmented_scan(keys, vals, act)
+            for l in range(wave):
+                if not act[l]:
+                    assert not seg[l]
+                    continue
+                start = l
+                while start > 0 and keys[start - 1] == keys[l]:
+                    start -= 1
+                assert out[l] == vals[start:l + 1].sum()
+            # each segment emitted exactly once
+            ends = [l for l in range(n_active) if seg[l]]
+            assert len(ends) == len(np.unique(keys[:n_active]))
+
+
+@pytest.mark.parametrize("block", [64, 256])
+def test_wave_position_schedule_equals_row_sum(orc, block):
+    csr = W.random_csr(400, 300, 20.0, 8, empty_fraction=0.2, lognormal=True)
+    x = np.random.default_rng(8).uniform(-1, 1, 300).astype(np.float32)
+    ref = orc.spmv(csr.row_offsets, csr.column_indices, csr.values, x)
+    bound = orc.spmv_abs_bound(csr.row_offsets, csr.column_indices,
+                               csr.values, x)
+    y = orc.spmv_wave_position(csr.row_offsets, csr.column_indices,
+                               csr.values, x, block=block, wave=64)
+    assert_within_bound(y, ref, bound)
+
+
+def test_bf16_tolerance_helper():
+    a = np.ones(100)
+    assert rel_l2(a, a) == 0.0
+    assert abs(rel_l2(a * 1.01, a) - 0.01) < 1e-12
