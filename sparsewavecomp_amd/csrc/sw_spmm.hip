@@ -254,6 +254,9 @@ int launch_spmm(const int32_t *ro, const int32_t *col, const float *val,
   SW_CL_CASE(1, 16)
   SW_CL_CASE(1, 32)
 #undef SW_CL_CASE
+  if (grid == 0)
+    return fail(SW_ERR_INVALID_OPTION,
+                "no wave-per-row-tile kernel for tile size %d", T);
   int rc = check_grid(grid, what);
   if (rc)
     return rc;
