@@ -48,6 +48,9 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true",
                     help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--mappings", default="",
+                    help="';'-separated SpMV option strings to measure "
+                         "instead of the default list")
     return ap.parse_args()
 
 
@@ -116,6 +119,8 @@ def main():
     ]
     if args.only_headline:
         mappings = mappings[:4]
+    if args.mappings:
+        mappings = [m.strip() for m in args.mappings.split(";") if m.strip()]
     spmv_results = {}
     for opts in mappings:
         o = sw.Options.parse(opts)

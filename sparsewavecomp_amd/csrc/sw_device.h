@@ -157,6 +157,44 @@ __device__ __forceinline__ int row_search_lane(const int32_t *__restrict__ ro,
   return (int)lo - 1;
 }
 
+// Wave-uniform binary search: every lane follows the same path, so the
+// probes compile to scalar loads through the scalar data cache and cost no
+// vector-memory (TA/TCP) throughput, which the x gathers saturate.
+__device__ __forceinline__ int row_search_uniform(const int32_t *__restrict__ ro,
+                                                  uint32_t lo, uint32_t hi,
+                                                  int32_t pos) {
+  lo = __builtin_amdgcn_readfirstlane(lo);
+  hi = __builtin_amdgcn_readfirstlane(hi);
+  pos = __builtin_amdgcn_readfirstlane(pos);
+  while (lo < hi) {
+    uint32_t mid = lo + ((hi - lo) >> 1);
+    if (ro[mid] <= pos)
+      lo = mid + 1;
+    else
+      hi = mid;
+  }
+  return (int)lo - 1;
+}
+
+// Wave-uniform galloping search for an answer expected close to `lo`:
+// probes lo, lo+1, lo+3, lo+7, ... then bisects the last gap.
+__device__ __forceinline__ int row_search_gallop(const int32_t *__restrict__ ro,
+                                                 uint32_t lo, uint32_t hi,
+                                                 int32_t pos) {
+  lo = __builtin_amdgcn_readfirstlane(lo);
+  hi = __builtin_amdgcn_readfirstlane(hi);
+  pos = __builtin_amdgcn_readfirstlane(pos);
+  uint32_t probe = lo, step = 1;
+  while (probe < hi && ro[probe] <= pos) {
+    lo = probe + 1;
+    probe = lo + step;
+    step <<= 1;
+  }
+  if (probe < hi)
+    hi = probe + 1; // ro[probe] > pos: the answer is at most probe
+  return row_search_uniform(ro, lo, hi, pos);
+}
+
 // Wave-cooperative 64-ary search for a wave-uniform position: every round
 // each lane probes one offset and a ballot narrows the range 64-fold, so a
 // 1M-row matrix needs four dependent loads instead of twenty.

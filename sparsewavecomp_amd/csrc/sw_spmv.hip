@@ -101,11 +101,17 @@ __global__ __launch_bounds__(1024) void spmv_block_per_row(
 // ---------------------------------------------------------------------------
 // Output initialisation of the position mappings
 // (SparsePositionScheduling.cpp:31-47): one thread per output element.
+// Each thread clears four consecutive elements (one 128-bit store when the
+// output is 16-byte aligned).
 __global__ __launch_bounds__(1024) void fill_zero_f32(float *__restrict__ y,
                                                       int64_t n) {
-  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n)
-    y[i] = 0.0f;
+  int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (i + 4 <= n && (reinterpret_cast<uintptr_t>(y) & 15u) == 0) {
+    *reinterpret_cast<v4f *>(y + i) = v4f{0.f, 0.f, 0.f, 0.f};
+  } else {
+    for (int64_t j = i; j < n && j < i + 4; ++j)
+      y[j] = 0.0f;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -169,7 +175,7 @@ __global__ __launch_bounds__(1024) void spmv_thread_position_segmented(
 // blocks and G*(B/64) waves; wave w owns the balanced partition
 // [w*base + min(w, rem), ...) of the units (SparsePositionToSCF.cpp:190-223)
 // and lane l the unit begin+l.  The wave finds the rows of its first and last
-// position with a 64-ary cooperative search, each lane then finds the row of
+// position with wave-uniform searches (scalar loads), each lane then finds the row of
 // its first position inside that narrow range, walks its P positions
 // (col/val read with 128-bit non-temporal loads when P >= 4) and
 //   - stores rows that start and end inside the lane directly,
@@ -197,54 +203,92 @@ __global__ __launch_bounds__(1024) void spmv_wave_position(
   if (wbeg >= wend)
     return; // wave-uniform: the whole wave leaves
 
-  const int first_row =
-      row_search_wave(ro, 1u, (uint32_t)rows + 1u, (int32_t)wbeg);
-  const int last_row = row_search_wave(ro, (uint32_t)first_row + 1u,
-                                       (uint32_t)rows + 1u,
-                                       (int32_t)(wend - 1));
-
   const int64_t u = (int64_t)ub + lane;
   const bool active = (uint64_t)u < ue && u * P < nnz;
   const int32_t p0 = active ? (int32_t)(u * P) : 0;
   const int32_t pe = active ? (int32_t)((u * P + P) < nnz ? u * P + P : nnz) : 0;
 
-  // operands of the lane's positions
-  float prod[P];
+  // Issue the lane's column/value loads and x gathers first; the row
+  // searches below use scalar loads and overlap with them.  The products are
+  // formed in the walk, so nothing waits on the gathers before the searches.
+  float vv[P], xg[P];
+#pragma unroll
+  for (int q = 0; q < P; ++q) {
+    vv[q] = 0.0f;
+    xg[q] = 0.0f;
+  }
   if (active) {
+    bool full = false;
     if constexpr (VEC && P >= 4) {
-      if (pe - p0 == P) {
+      full = pe - p0 == P;
+      if (full) {
 #pragma unroll
         for (int q = 0; q < P; q += 4) {
           v4i c = ld_stream(reinterpret_cast<const v4i *>(col + p0 + q));
           v4f v = ld_stream(reinterpret_cast<const v4f *>(val + p0 + q));
-          prod[q + 0] = v.x * x[c.x];
-          prod[q + 1] = v.y * x[c.y];
-          prod[q + 2] = v.z * x[c.z];
-          prod[q + 3] = v.w * x[c.w];
+          vv[q + 0] = v.x;
+          vv[q + 1] = v.y;
+          vv[q + 2] = v.z;
+          vv[q + 3] = v.w;
+          xg[q + 0] = x[c.x];
+          xg[q + 1] = x[c.y];
+          xg[q + 2] = x[c.z];
+          xg[q + 3] = x[c.w];
         }
-      } else {
-#pragma unroll
-        for (int q = 0; q < P; ++q)
-          prod[q] = (p0 + q < pe) ? ld_stream(val + p0 + q) *
-                                        x[ld_stream(col + p0 + q)]
-                                  : 0.0f;
       }
-    } else {
+    }
+    if (!full) {
 #pragma unroll
       for (int q = 0; q < P; ++q)
-        prod[q] = (p0 + q < pe)
-                      ? ld_stream(val + p0 + q) * x[ld_stream(col + p0 + q)]
-                      : 0.0f;
+        if (p0 + q < pe) {
+          vv[q] = ld_stream(val + p0 + q);
+          xg[q] = x[ld_stream(col + p0 + q)];
+        }
     }
   }
 
+  const int first_row =
+      row_search_uniform(ro, 1u, (uint32_t)rows + 1u, (int32_t)wbeg);
+  const int last_row = row_search_gallop(ro, (uint32_t)first_row + 1u,
+                                         (uint32_t)rows + 1u,
+                                         (int32_t)(wend - 1));
+
+  // Row boundaries ro[first_row+1 .. first_row+64] staged in LDS (one
+  // coalesced load per wave) serve the lanes' row lookups whenever the wave
+  // spans at most 64 rows; otherwise lanes search the row offsets directly.
+  __shared__ int32_t window[1024 / kWave][kWave];
+  int32_t *win = window[threadIdx.x / kWave];
+  const int span = last_row - first_row; // wave-uniform
+  const bool use_win = span < kWave;
+  if (use_win) {
+    const int j = first_row + 1 + lane;
+    win[lane] = j <= first_row + 1 + span ? ro[j] : INT32_MAX;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
   int lrow = 0, row = 0, closed = 0;
   float head = 0.0f, acc = 0.0f;
   if (active) {
-    lrow = row_search_lane(ro, (uint32_t)first_row + 1u,
-                           (uint32_t)last_row + 2u, p0);
+    int32_t next;
+    if (use_win) {
+      // count of window boundaries <= p0, over entries [0, span]
+      int lo = 0, hi = span; // the answer lies in [0, span]
+      while (lo < hi) {
+        int mid = (lo + hi) >> 1;
+        if (win[mid] <= p0)
+          lo = mid + 1;
+        else
+          hi = mid;
+      }
+      lrow = first_row + lo;
+      next = win[lo];
+    } else {
+      lrow = row_search_lane(ro, (uint32_t)first_row + 1u,
+                             (uint32_t)last_row + 2u, p0);
+      next = ro[lrow + 1];
+    }
     row = lrow;
-    int32_t next = ro[row + 1];
 #pragma unroll
     for (int q = 0; q < P; ++q) {
       const int32_t p = p0 + q;
@@ -257,9 +301,9 @@ __global__ __launch_bounds__(1024) void spmv_wave_position(
           ++closed;
           acc = 0.0f;
           ++row;
-          next = ro[row + 1];
+          next = use_win ? win[row - first_row] : ro[row + 1];
         }
-        acc += prod[q];
+        acc = __builtin_fmaf(vv[q], xg[q], acc);
       }
     }
   }
@@ -316,7 +360,7 @@ namespace sw {
 int launch_fill_zero(float *y, int64_t n, int64_t block, hipStream_t st) {
   if (n <= 0)
     return SW_OK;
-  int64_t grid = ceil_div(n, block);
+  int64_t grid = ceil_div(ceil_div(n, 4), block);
   int rc = check_grid(grid, "output initialisation");
   if (rc)
     return rc;
