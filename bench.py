@@ -107,18 +107,20 @@ def main():
     spmv_bytes = W.algorithmic_bytes_spmv(n, m, nnz)
     spmv_flops = 2 * nnz
     mappings = [
-        "spmv-mapping=wave-per-position spmv-positions-per-lane=8",
-        "spmv-mapping=wave-per-position spmv-positions-per-lane=4",
-        "spmv-mapping=wave-per-position spmv-positions-per-lane=16",
-        "spmv-mapping=wave-per-row spmv-lanes-per-row=8",
+        "spmv-mapping=wave-per-position spmv-positions-per-lane=4 "
+        "spmv-block-size=64",
+        "spmv-mapping=wave-per-position spmv-positions-per-lane=8 "
+        "spmv-block-size=64",
+        "spmv-mapping=wave-per-position spmv-positions-per-lane=8 "
+        "spmv-block-size=128",
         "spmv-mapping=wave-per-row spmv-lanes-per-row=16",
         "spmv-mapping=wave-per-row",
-        "spmv-mapping=thread-per-row",
         "spmv-mapping=block-per-row spmv-block-size=128",
+        "spmv-mapping=thread-per-row",
         "spmv-mapping=wave-per-position",
     ]
     if args.only_headline:
-        mappings = mappings[:4]
+        mappings = mappings[:3]
     if args.mappings:
         mappings = [m.strip() for m in args.mappings.split(";") if m.strip()]
     spmv_results = {}

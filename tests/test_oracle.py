@@ -349,3 +349,13 @@ def test_bf16_tolerance_helper():
     a = np.ones(100)
     assert rel_l2(a, a) == 0.0
     assert abs(rel_l2(a * 1.01, a) - 0.01) < 1e-12
+
+
+def test_multithreaded_spmv_equals_scalar(orc):
+    """The all-cores CPU extra computes the same rows in the same order."""
+    csr = W.random_csr(5000, 3000, 20.0, 12, empty_fraction=0.1)
+    x = np.random.default_rng(12).uniform(-1, 1, 3000).astype(np.float32)
+    a = orc.spmv(csr.row_offsets, csr.column_indices, csr.values, x)
+    b = orc.spmv(csr.row_offsets, csr.column_indices, csr.values, x,
+                 threads=True)
+    np.testing.assert_array_equal(a, b)
