@@ -151,11 +151,11 @@ def main():
         workloads["spmv_config1"] = res1
 
         # ---- configuration 3: CSR SpMM K = 4 and 64 -------------------------
-        for k, opts in [(4, "spmm-mapping=wave-per-row-tile spmm-tile-size=4 "
-                            "spmm-lanes-per-row=16"),
+        for k, opts in [(4, "spmm-mapping=wave-per-position "
+                            "spmm-positions-per-lane=8 spmm-block-size=256"),
                         (4, "spmm-mapping=wave-per-row-tile spmm-tile-size=4"),
-                        (64, "spmm-mapping=wave-per-row-tile "
-                             "spmm-tile-size=32 spmm-lanes-per-row=16"),
+                        (64, "spmm-mapping=wave-per-position "
+                             "spmm-positions-per-lane=16 spmm-block-size=64"),
                         (64, "spmm-mapping=wave-per-row-tile "
                              "spmm-tile-size=32 spmm-lanes-per-row=64")]:
             rhs = T(W.config3_rhs(m, k, seed=0))
@@ -210,9 +210,8 @@ def main():
         rmax = torch.empty(mask.rows, device=dev)
         rsum = torch.empty(mask.rows, device=dev)
         outa = torch.empty((mask.rows, 64), device=dev)
-        for opts in ["", "sddmm-lanes-per-row=64 spmm-mapping="
-                         "wave-per-row-tile spmm-tile-size=32 "
-                         "spmm-lanes-per-row=16"]:
+        for opts in ["", "sddmm-mapping=row-tile-mfma sddmm-lanes-per-row=64 "
+                         "spmm-mapping=row-tile-mfma"]:
             o = sw.Options.parse(opts)
             log(f"attention '{opts}'")
             ms = time_steps(lambda: sw.sparse_attention(

@@ -45,7 +45,9 @@ typedef struct sw_options {
   char spmv_position_reduction[16]; /* atomic | segmented (thread-per-position) */
   int64_t position_block_size;      /* position-parallel init kernels, default 256 */
   char spmm_mapping[32];            /* thread-per-output | wave-per-row-tile |
-                                       thread-per-position */
+                                       thread-per-position | wave-per-position |
+                                       row-tile-mfma (the last two are Wave64
+                                       extensions) */
   int64_t spmm_block_size;          /* 1..1024, default 256 */
   int64_t spmm_tile_size;           /* 1..32, default 4 */
   int64_t spmm_position_chunk_size; /* default 1 */
@@ -69,6 +71,15 @@ typedef struct sw_options {
   int64_t sddmm_lanes_per_row;      /* SDDMM: 1 = thread-per-row (reference,
                                        default); 64 = one wave per row with
                                        lanes split over the dot products */
+  int64_t spmm_positions_per_lane;  /* SpMM wave-per-position: consecutive
+                                       positions per lane group 1,2,4,8,16;
+                                       default 4 */
+  char sddmm_mapping[32];           /* thread-per-row (reference, default) |
+                                       wave-per-row | row-tile-mfma (16-row
+                                       tiles on the matrix cores; tiles whose
+                                       rows do not share column structure,
+                                       and kdim not in {64,128,256}, use the
+                                       vector path) */
 } sw_options;
 
 /* Fill `opts` with the defaults. */

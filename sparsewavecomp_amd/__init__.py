@@ -68,6 +68,8 @@ class _COptions(ctypes.Structure):
         ("spmm_lanes_per_row", ctypes.c_int64),
         ("bsr_use_mfma", ctypes.c_int64),
         ("sddmm_lanes_per_row", ctypes.c_int64),
+        ("spmm_positions_per_lane", ctypes.c_int64),
+        ("sddmm_mapping", ctypes.c_char * 32),
     ]
 
 

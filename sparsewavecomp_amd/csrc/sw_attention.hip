@@ -80,18 +80,14 @@ __global__ __launch_bounds__(1024) void sddmm_thread_per_row(
   }
 }
 
-// One wave per row; lane l computes the dot products of positions
+// One wave computes the SDDMM entries of row r: lane l takes positions
 // start+l, start+l+64, ...; the row of lhs is held 64 values at a time, one
 // per lane, and broadcast with v_readlane.
-__global__ __launch_bounds__(256) void sddmm_wave_per_row(
+__device__ __forceinline__ void sddmm_row_wave(
     const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
     const float *__restrict__ val, const float *__restrict__ lhs,
-    const float *__restrict__ rhs, float *__restrict__ out, int32_t rows,
+    const float *__restrict__ rhs, float *__restrict__ out, int64_t r,
     int64_t cols, int32_t kdim, int kind, float alpha, float beta) {
-  const int64_t r = (int64_t)blockIdx.x * (blockDim.x / kWave) +
-                    threadIdx.x / kWave;
-  if (r >= rows)
-    return; // wave-uniform
   const int l = lane_id();
   const int32_t s = ro[r], e = ro[r + 1];
   const float *a = lhs + r * kdim;
@@ -125,7 +121,108 @@ __global__ __launch_bounds__(256) void sddmm_wave_per_row(
   }
 }
 
-// ---- row reduce ----------------------------------------------------------
+__global__ __launch_bounds__(256) void sddmm_wave_per_row(
+    const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
+    const float *__restrict__ val, const float *__restrict__ lhs,
+    const float *__restrict__ rhs, float *__restrict__ out, int32_t rows,
+    int64_t cols, int32_t kdim, int kind, float alpha, float beta) {
+  const int64_t r = (int64_t)blockIdx.x * (blockDim.x / kWave) +
+                    threadIdx.x / kWave;
+  if (r >= rows)
+    return; // wave-uniform
+  sddmm_row_wave(ro, col, val, lhs, rhs, out, r, cols, kdim, kind, alpha,
+                 beta);
+}
+
+// SDDMM over 16-row tiles on the matrix cores (kdim = 64 * KB).
+//
+// A workgroup of four waves owns rows r0 .. r0+15.  When every row's columns
+// are a prefix of the last row's (tile_prefix_ok_block), the tile's dot products
+// for 16 of the last row's columns at a time are one 16 x 16 x kdim product
+//   D = lhs[r0 .. r0+15][:] * rhs[:][c_t0 .. c_t0+15]
+// computed with v_mfma_f32_16x16x4_f32 (lane (i, g) supplies
+// lhs[r0+i][16g+s] at step s, lane (j, g) supplies rhs[16g+s][c_j]); wave w
+// takes the column chunks w, w+4, ...  Each result lands at its CSR position
+// ro[row] + t when t is inside that row.  Tiles without the shared structure
+// are computed row by row on the vector ALUs.
+template <int KB>
+__global__ __launch_bounds__(256) void sddmm_tile_mfma(
+    const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
+    const float *__restrict__ val, const float *__restrict__ lhs,
+    const float *__restrict__ rhs, float *__restrict__ out, int32_t rows,
+    int64_t cols, int32_t kdim, int kind, float alpha, float beta) {
+  const int r0 = blockIdx.x * 16;
+  const int nt = std::min(16, rows - r0);
+  const int wave = threadIdx.x / kWave;
+  __shared__ int verdict;
+  if (!tile_prefix_ok_block(ro, col, r0, nt, &verdict)) {
+    for (int r = r0 + wave; r < r0 + nt; r += 4)
+      sddmm_row_wave(ro, col, val, lhs, rhs, out, r, cols, kdim, kind, alpha,
+                     beta);
+    return;
+  }
+  const int l = lane_id(), i = l & 15, g = l >> 4;
+  const int last = r0 + nt - 1;
+  const int32_t bl = ro[last];
+  const int32_t len_last = ro[last + 1] - bl;
+  int32_t rb[4], rl[4];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int rr = r0 + 4 * g + v;
+    rb[v] = rr < r0 + nt ? ro[rr] : 0;
+    rl[v] = rr < r0 + nt ? ro[rr + 1] - rb[v] : 0;
+  }
+  float qa[16 * KB];
+#pragma unroll
+  for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+    for (int st = 0; st < 16; ++st)
+      qa[kb * 16 + st] = i < nt ? lhs[(int64_t)(r0 + i) * kdim + kb * 64 +
+                                      16 * g + st]
+                                : 0.0f;
+  // two column chunks per iteration (waves w and w+4 apart): two
+  // independent accumulators and 32 outstanding rhs loads per lane
+  for (int32_t t0 = wave * 16; t0 < len_last; t0 += 128) {
+    const int32_t t1 = t0 + 64;
+    const bool two = t1 < len_last; // wave-uniform
+    const int64_t cj0 = t0 + i < len_last ? (int64_t)col[bl + t0 + i] : 0;
+    const int64_t cj1 = two && t1 + i < len_last ? (int64_t)col[bl + t1 + i] : 0;
+    v4f acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+      float bv0[16], bv1[16];
+#pragma unroll
+      for (int st = 0; st < 16; ++st) {
+        const float *rrow = rhs + (int64_t)(kb * 64 + 16 * g + st) * cols;
+        bv0[st] = rrow[cj0];
+        bv1[st] = two ? rrow[cj1] : 0.0f;
+      }
+#pragma unroll
+      for (int st = 0; st < 16; ++st) {
+        acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[kb * 16 + st], bv0[st],
+                                                    acc0, 0, 0, 0);
+        if (two)
+          acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[kb * 16 + st],
+                                                      bv1[st], acc1, 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int32_t ta = t0 + i, tb = t1 + i;
+      if (ta < rl[v]) {
+        const int32_t p = rb[v] + ta;
+        out[p] = combine_sddmm(kind, val != nullptr ? val[p] : 0.0f, acc0[v],
+                               alpha, beta);
+      }
+      if (two && tb < rl[v]) {
+        const int32_t p = rb[v] + tb;
+        out[p] = combine_sddmm(kind, val != nullptr ? val[p] : 0.0f, acc1[v],
+                               alpha, beta);
+      }
+    }
+  }
+}
+
 template <bool MAX>
 __global__ __launch_bounds__(1024) void row_reduce_thread(
     const int32_t *__restrict__ ro, const float *__restrict__ val,
@@ -205,7 +302,28 @@ int launch_sddmm(const int32_t *ro, const int32_t *col, const float *val,
                  int64_t cols, int64_t kdim, int kind, float alpha, float beta,
                  const sw_options &o, hipStream_t st) {
   int64_t grid;
-  if (o.sddmm_lanes_per_row == 64) {
+  if (streq(o.sddmm_mapping, "row-tile-mfma") &&
+      (kdim == 64 || kdim == 128 || kdim == 256)) {
+    int rc = grid_for(rows, 16, "SDDMM", &grid);
+    if (rc)
+      return rc;
+    const int kb = (int)(kdim / 64);
+#define SW_SDDMM_TILE(KB)                                                     \
+  hipLaunchKernelGGL(sddmm_tile_mfma<KB>, dim3((unsigned)grid), dim3(256), 0, \
+                     st, ro, col, val, lhs, rhs, out, (int32_t)rows, cols,    \
+                     (int32_t)kdim, kind, alpha, beta)
+    if (kb == 1)
+      SW_SDDMM_TILE(1);
+    else if (kb == 2)
+      SW_SDDMM_TILE(2);
+    else
+      SW_SDDMM_TILE(4);
+#undef SW_SDDMM_TILE
+    return launch_check("SDDMM tile MFMA kernel");
+  }
+  if (streq(o.sddmm_mapping, "wave-per-row") ||
+      (streq(o.sddmm_mapping, "row-tile-mfma")) ||
+      o.sddmm_lanes_per_row == 64) {
     int rc = grid_for(rows, 4, "SDDMM", &grid);
     if (rc)
       return rc;

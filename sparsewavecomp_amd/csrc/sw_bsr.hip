@@ -62,11 +62,28 @@ __global__ __launch_bounds__(1024) void bsr_thread_per_output(
 // The k order inside a block is a free choice as long as A and B agree;
 // fp32 uses k = 4*g + s at step s so that one 128-bit load gives a lane its
 // four A values.
+// Block rows are visited XCD-aware: workgroups are dispatched to the eight
+// XCDs round-robin, so workgroup w runs block row
+// (w % 8) * (nbr / 8) + w / 8 and each XCD walks a contiguous range of block
+// rows, keeping the RHS tiles of a banded matrix in its own L2.
+__device__ __forceinline__ int xcd_block_row(int w, int nbr) {
+  constexpr int kXcds = 8;
+  if (nbr % kXcds != 0)
+    return w;
+  return (w % kXcds) * (nbr / kXcds) + w / kXcds;
+}
+
+// Blocks are processed in batches of NB: the batch's column indices arrive
+// with one load (lane j holds block j's column, broadcast by v_readlane),
+// then every A and B operand of the batch is requested before the first
+// MFMA, so a block row waits for two memory latencies per batch instead of
+// two per block.
+template <int NB>
 __global__ __launch_bounds__(256) void bsr16_mfma_f32(
     const int32_t *__restrict__ bro, const int32_t *__restrict__ bcol,
     const float *__restrict__ bval, const float *__restrict__ rhs,
-    float *__restrict__ out, int64_t k) {
-  const int br = blockIdx.x;
+    float *__restrict__ out, int64_t k, int nbr) {
+  const int br = xcd_block_row(blockIdx.x, nbr);
   const int wave = threadIdx.x / kWave;
   const int l = lane_id();
   const int i = l & 15, g = l >> 4;
@@ -75,38 +92,56 @@ __global__ __launch_bounds__(256) void bsr16_mfma_f32(
   const bool ok0 = c0 < k, ok1 = c1 < k;
   v4f acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
   const int32_t s = bro[br], e = bro[br + 1];
-  for (int32_t bp = s; bp < e; ++bp) {
-    const int64_t bc = bcol[bp];
-    const v4f a = ld_stream(reinterpret_cast<const v4f *>(
-        bval + (int64_t)bp * 256 + i * 16 + g * 4));
-    const float *brow = rhs + (bc * 16 + g * 4) * k;
-    float b0[4], b1[4];
+  for (int32_t b0 = s; b0 < e; b0 += NB) {
+    const int nb = e - b0 < NB ? e - b0 : NB; // wave-uniform
+    const int bcl = l < nb ? bcol[b0 + l] : 0;
+    v4f a[NB];
+    float bv0[NB][4], bv1[NB][4];
 #pragma unroll
-    for (int st = 0; st < 4; ++st) {
-      b0[st] = ok0 ? brow[st * k + c0] : 0.0f;
-      b1[st] = ok1 ? brow[st * k + c1] : 0.0f;
+    for (int j = 0; j < NB; ++j) {
+      if (j < nb) {
+        const int64_t bc = __builtin_amdgcn_readlane(bcl, j);
+        a[j] = ld_stream(reinterpret_cast<const v4f *>(
+            bval + (int64_t)(b0 + j) * 256 + i * 16 + g * 4));
+        const float *brow = rhs + (bc * 16 + g * 4) * k;
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+          bv0[j][st] = ok0 ? brow[st * k + c0] : 0.0f;
+          bv1[j][st] = ok1 ? brow[st * k + c1] : 0.0f;
+        }
+      }
     }
 #pragma unroll
-    for (int st = 0; st < 4; ++st) {
-      acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a[st], b0[st], acc0, 0, 0, 0);
-      acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a[st], b1[st], acc1, 0, 0, 0);
+    for (int j = 0; j < NB; ++j) {
+      if (j < nb) {
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+          acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j][st], bv0[j][st],
+                                                      acc0, 0, 0, 0);
+          acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j][st], bv1[j][st],
+                                                      acc1, 0, 0, 0);
+        }
+      }
     }
   }
+  // non-temporal stores: the output is not re-read, so it should not
+  // displace RHS tiles from the caches
   float *o = out + ((int64_t)br * 16 + g * 4) * k;
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
     if (ok0)
-      o[v * k + c0] = acc0[v];
+      __builtin_nontemporal_store(acc0[v], o + v * k + c0);
     if (ok1)
-      o[v * k + c1] = acc1[v];
+      __builtin_nontemporal_store(acc1[v], o + v * k + c1);
   }
 }
 
+template <int NB>
 __global__ __launch_bounds__(256) void bsr16_mfma_bf16(
     const int32_t *__restrict__ bro, const int32_t *__restrict__ bcol,
     const uint16_t *__restrict__ bval, const uint16_t *__restrict__ rhs,
-    float *__restrict__ out, int64_t k) {
-  const int br = blockIdx.x;
+    float *__restrict__ out, int64_t k, int nbr) {
+  const int br = xcd_block_row(blockIdx.x, nbr);
   const int wave = threadIdx.x / kWave;
   const int l = lane_id();
   const int i = l & 15, g = l >> 4;
@@ -115,28 +150,44 @@ __global__ __launch_bounds__(256) void bsr16_mfma_bf16(
   const bool ok0 = c0 < k, ok1 = c1 < k;
   v4f acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
   const int32_t s = bro[br], e = bro[br + 1];
-  for (int32_t bp = s; bp < e; ++bp) {
-    const int64_t bc = bcol[bp];
-    // A[i][4g .. 4g+3]: 8 contiguous bytes of the row-major block
-    const v4s a = *reinterpret_cast<const v4s *>(bval + (int64_t)bp * 256 +
-                                                 i * 16 + g * 4);
-    const uint16_t *brow = rhs + (bc * 16 + g * 4) * k;
-    v4s b0, b1;
+  for (int32_t b0 = s; b0 < e; b0 += NB) {
+    const int nb = e - b0 < NB ? e - b0 : NB;
+    const int bcl = l < nb ? bcol[b0 + l] : 0;
+    v4s a[NB], bv0[NB], bv1[NB];
 #pragma unroll
-    for (int st = 0; st < 4; ++st) {
-      b0[st] = ok0 ? (short)brow[st * k + c0] : (short)0;
-      b1[st] = ok1 ? (short)brow[st * k + c1] : (short)0;
+    for (int j = 0; j < NB; ++j) {
+      if (j < nb) {
+        const int64_t bc = __builtin_amdgcn_readlane(bcl, j);
+        // A[i][4g .. 4g+3]: 8 contiguous bytes of the row-major block
+        a[j] = *reinterpret_cast<const v4s *>(bval + (int64_t)(b0 + j) * 256 +
+                                              i * 16 + g * 4);
+        const uint16_t *brow = rhs + (bc * 16 + g * 4) * k;
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+          bv0[j][st] = ok0 ? (short)brow[st * k + c0] : (short)0;
+          bv1[j][st] = ok1 ? (short)brow[st * k + c1] : (short)0;
+        }
+      }
     }
-    acc0 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b0, acc0, 0, 0, 0);
-    acc1 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b1, acc1, 0, 0, 0);
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      if (j < nb) {
+        acc0 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a[j], bv0[j], acc0, 0,
+                                                         0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a[j], bv1[j], acc1, 0,
+                                                         0, 0);
+      }
+    }
   }
+  // non-temporal stores: the output is not re-read, so it should not
+  // displace RHS tiles from the caches
   float *o = out + ((int64_t)br * 16 + g * 4) * k;
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
     if (ok0)
-      o[v * k + c0] = acc0[v];
+      __builtin_nontemporal_store(acc0[v], o + v * k + c0);
     if (ok1)
-      o[v * k + c1] = acc1[v];
+      __builtin_nontemporal_store(acc1[v], o + v * k + c1);
   }
 }
 
@@ -179,13 +230,14 @@ int launch_bsr(const int32_t *bro, const int32_t *bcol, const T *bval,
     int64_t gy = sw::ceil_div(k, 128);
     if (gy > 65535)
       return sw::fail(SW_ERR_INVALID_SHAPE, "rhs has too many columns");
-    dim3 grid((unsigned)(rows / 16), (unsigned)gy);
+    const int nbr = (int)(rows / 16);
+    dim3 grid((unsigned)nbr, (unsigned)gy);
     if constexpr (sizeof(T) == 4)
-      hipLaunchKernelGGL(bsr16_mfma_f32, grid, dim3(256), 0, st, bro, bcol,
-                         bval, rhs, out, k);
+      hipLaunchKernelGGL(bsr16_mfma_f32<8>, grid, dim3(256), 0, st, bro, bcol,
+                         bval, rhs, out, k, nbr);
     else
-      hipLaunchKernelGGL(bsr16_mfma_bf16, grid, dim3(256), 0, st, bro, bcol,
-                         bval, rhs, out, k);
+      hipLaunchKernelGGL(bsr16_mfma_bf16<8>, grid, dim3(256), 0, st, bro,
+                         bcol, bval, rhs, out, k, nbr);
     return sw::launch_check("BSR MFMA kernel");
   }
   const int64_t B = o.spmm_block_size;

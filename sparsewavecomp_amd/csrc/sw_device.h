@@ -195,6 +195,46 @@ __device__ __forceinline__ int row_search_gallop(const int32_t *__restrict__ ro,
   return row_search_uniform(ro, lo, hi, pos);
 }
 
+// ---- 16-row tiles with shared column structure ------------------------------
+// Rows r0 .. r0+nt-1 (nt <= 16) form an MFMA tile when every row's column
+// list is a prefix of the tile's last row's list -- true for block masks and
+// for causal diagonal blocks, where later rows extend earlier ones.  Then the
+// tile's dense products over the last row's columns give every stored entry.
+// The check reads every column index of the tile once.
+//
+// tile_prefix_ok_block splits the rows over the four waves of a 256-thread
+// workgroup (wave w checks rows w, w+4, ...) and combines their verdicts in
+// LDS; every thread of the workgroup must call it (it has a barrier).
+__device__ __forceinline__ bool tile_prefix_ok_block(
+    const int32_t *__restrict__ ro, const int32_t *__restrict__ col, int r0,
+    int nt, int *verdict /* __shared__ int[1] */) {
+  const int lane = lane_id();
+  const int wave = threadIdx.x / kWave;
+  if (threadIdx.x == 0)
+    *verdict = 1;
+  __syncthreads();
+  // lanes 0..nt hold ro[r0 .. r0+nt]: one load instead of a chain
+  const int32_t my_ro = lane <= nt ? ro[r0 + lane] : 0;
+  const int32_t base_last = __builtin_amdgcn_readlane(my_ro, nt - 1);
+  const int32_t len_last = __builtin_amdgcn_readlane(my_ro, nt) - base_last;
+  bool ok = true;
+  for (int i = wave; i < nt - 1; i += 4) {
+    const int32_t b = __builtin_amdgcn_readlane(my_ro, i);
+    const int32_t len = __builtin_amdgcn_readlane(my_ro, i + 1) - b;
+    if (len > len_last) {
+      ok = false;
+      break; // wave-uniform
+    }
+#pragma unroll 4
+    for (int32_t t = lane; t < len; t += kWave)
+      ok &= col[b + t] == col[base_last + t];
+  }
+  if (__builtin_amdgcn_ballot_w64(!ok) != 0 && lane == 0)
+    *verdict = 0;
+  __syncthreads();
+  return *verdict != 0;
+}
+
 // Wave-cooperative 64-ary search for a wave-uniform position: every round
 // each lane probes one offset and a ballot narrows the range 64-fold, so a
 // 1M-row matrix needs four dependent loads instead of twenty.

@@ -94,6 +94,8 @@ void sw_options_init(sw_options *o) {
   o->spmm_lanes_per_row = 64;
   o->bsr_use_mfma = 1;
   o->sddmm_lanes_per_row = 1;
+  o->spmm_positions_per_lane = 4;
+  std::strcpy(o->sddmm_mapping, "thread-per-row");
 }
 
 int sw_options_set(sw_options *o, const char *name, const char *value) {
@@ -126,6 +128,8 @@ int sw_options_set(sw_options *o, const char *name, const char *value) {
       {"spmm-lanes-per-row", "spmm-lanes-per-row", &o->spmm_lanes_per_row},
       {"bsr-use-mfma", "bsr-use-mfma", &o->bsr_use_mfma},
       {"sddmm-lanes-per-row", "sddmm-lanes-per-row", &o->sddmm_lanes_per_row},
+      {"spmm-positions-per-lane", "spmm-positions-per-lane",
+       &o->spmm_positions_per_lane},
   };
   for (const IntOpt &opt : ints) {
     if ((opt.pass_name && n == opt.pass_name) ||
@@ -139,6 +143,8 @@ int sw_options_set(sw_options *o, const char *name, const char *value) {
                       sizeof(o->spmv_position_reduction), value);
   if (n == "spmm-mapping")
     return set_string(o->spmm_mapping, sizeof(o->spmm_mapping), value);
+  if (n == "sddmm-mapping")
+    return set_string(o->sddmm_mapping, sizeof(o->sddmm_mapping), value);
   if (n == "chip") {
     if (std::strcmp(value, "gfx950") != 0)
       return sw::fail(SW_ERR_INVALID_OPTION,
@@ -215,12 +221,21 @@ int sw_validate_options(const sw_options *o) {
                     "'thread-per-position', or 'wave-per-position'",
                     o->spmv_mapping);
   if (spmm != "thread-per-output" && spmm != "wave-per-row-tile" &&
-      spmm != "thread-per-position")
+      spmm != "thread-per-position" && spmm != "wave-per-position" &&
+      spmm != "row-tile-mfma")
     return sw::fail(SW_ERR_INVALID_OPTION,
                     "unsupported SpMM mapping strategy '%s'; expected "
-                    "'thread-per-output', 'wave-per-row-tile', or "
-                    "'thread-per-position'",
+                    "'thread-per-output', 'wave-per-row-tile', "
+                    "'thread-per-position', 'wave-per-position', or "
+                    "'row-tile-mfma'",
                     o->spmm_mapping);
+  std::string sddmm(o->sddmm_mapping);
+  if (sddmm != "thread-per-row" && sddmm != "wave-per-row" &&
+      sddmm != "row-tile-mfma")
+    return sw::fail(SW_ERR_INVALID_OPTION,
+                    "unsupported SDDMM mapping strategy '%s'; expected "
+                    "'thread-per-row', 'wave-per-row', or 'row-tile-mfma'",
+                    o->sddmm_mapping);
   int rc;
   if ((rc = check_block("SpMV", o->spmv_block_size)))
     return rc;
@@ -241,14 +256,15 @@ int sw_validate_options(const sw_options *o) {
   if ((rc = check_block("elementwise", o->elementwise_block_size)))
     return rc;
   const int64_t w = o->wavefront_size;
-  bool wave_spmm = spmm == "wave-per-row-tile";
+  bool wave_spmm = spmm == "wave-per-row-tile" ||
+                   spmm == "wave-per-position" || spmm == "row-tile-mfma";
   bool wave_spmv = spmv == "wave-per-row" || spmv == "block-per-row" ||
                    spmv == "wave-per-position";
   if ((wave_spmm || wave_spmv) && w != 64)
     return sw::fail(SW_ERR_INVALID_OPTION,
                     "%s currently requires Wave64 on gfx950, but got wave "
                     "size %lld",
-                    wave_spmm ? "wave-per-row-tile" : o->spmv_mapping,
+                    wave_spmm ? o->spmm_mapping : o->spmv_mapping,
                     (long long)w);
   if (w != 64)
     return sw::fail(SW_ERR_INVALID_OPTION,
@@ -256,9 +272,10 @@ int sw_validate_options(const sw_options *o) {
                     (long long)w);
   if (wave_spmm && o->spmm_block_size % w != 0)
     return sw::fail(SW_ERR_INVALID_OPTION,
-                    "wave-per-row-tile requires the SpMM block size to be a "
-                    "multiple of %lld, but got %lld",
-                    (long long)w, (long long)o->spmm_block_size);
+                    "%s requires the SpMM block size to be a multiple of "
+                    "%lld, but got %lld",
+                    o->spmm_mapping, (long long)w,
+                    (long long)o->spmm_block_size);
   if (wave_spmv && o->spmv_block_size % w != 0) {
     if (spmv == "wave-per-position")
       return sw::fail(SW_ERR_INVALID_OPTION,
@@ -310,6 +327,12 @@ int sw_validate_options(const sw_options *o) {
                     "spmm-lanes-per-row must be a power of two between 1 and "
                     "64, but got %lld",
                     (long long)o->spmm_lanes_per_row);
+  int64_t sppl = o->spmm_positions_per_lane;
+  if (sppl != 1 && sppl != 2 && sppl != 4 && sppl != 8 && sppl != 16)
+    return sw::fail(SW_ERR_INVALID_OPTION,
+                    "spmm-positions-per-lane must be 1, 2, 4, 8 or 16, but "
+                    "got %lld",
+                    (long long)sppl);
   if (o->bsr_use_mfma != 0 && o->bsr_use_mfma != 1)
     return sw::fail(SW_ERR_INVALID_OPTION,
                     "bsr-use-mfma must be 0 or 1, but got %lld",

@@ -5,6 +5,9 @@
 //   wave-per-row-tile    SparseWaveToGPU.cpp:1057-1256
 //   thread-per-position  PositionSpMMDecomposition.cpp:19-73 +
 //                        SparsePositionScheduling.cpp:135-194
+//   wave-per-position    Wave64 extension: the SpMV position schedule
+//                        (SparsePositionScheduling.cpp:318-403) over
+//                        (position, column tile) pairs
 #include "sw_device.h"
 #include "sw_internal.h"
 
@@ -138,6 +141,350 @@ __global__ __launch_bounds__(1024) void spmm_thread_position(
   }
 }
 
+
+// wave-per-position SpMM (Wave64 extension of the position schedule).
+//
+// The nonzeros are cut into units of P consecutive positions exactly as in
+// the SpMV position kernel, and the output columns into tiles of CL*V.  A
+// wave owns one (position chunk, column tile): its 64 lanes form PL = 64/CL
+// "virtual lanes" of CL lanes each; virtual lane vl walks unit chunk*PL+vl
+// and each of its CL lanes accumulates V consecutive output columns
+// (V = 4: 128-bit RHS gathers).  Row recovery (wave-uniform scalar searches
+// plus an LDS window of row boundaries), the in-lane walk, the segmented scan
+// over the virtual lanes (stride CL) and the one-atomic-per-segment emission
+// follow the SpMV kernel.  Position balance makes rows of any length cost the
+// same, which the row-tile mapping cannot offer for rows thousands long.
+template <int V, int CL, int P>
+__global__ __launch_bounds__(1024) void spmm_wave_position(
+    const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
+    const float *__restrict__ val, const float *__restrict__ rhs,
+    float *__restrict__ out, int32_t rows, int32_t nnz, int64_t k,
+    int64_t units, int64_t chunks, int64_t tiles, bool vec) {
+  constexpr int PL = kWave / CL;
+  const int lane = lane_id();
+  const int64_t wave =
+      (int64_t)blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+  if (wave >= chunks * tiles)
+    return;
+  const int64_t chunk = wave / tiles;
+  const int64_t tile = wave - chunk * tiles;
+  const int64_t wbeg = chunk * PL * P;
+  const int64_t wend = std::min<int64_t>((chunk + 1) * PL * P, nnz);
+  if (wbeg >= wend)
+    return;
+  const int vl = lane / CL, cl = lane % CL;
+  const int64_t cb = tile * (CL * V) + (int64_t)cl * V;
+  const bool col_ok = cb < k;
+  const int64_t u = chunk * PL + vl;
+  const bool active = u < units;
+  const int32_t p0 = active ? (int32_t)(u * P) : 0;
+  const int32_t pe =
+      active ? (int32_t)std::min<int64_t>(u * P + P, (int64_t)nnz) : 0;
+
+  float vv[P];
+  float g[P][V];
+#pragma unroll
+  for (int q = 0; q < P; ++q) {
+    vv[q] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < V; ++i)
+      g[q][i] = 0.0f;
+  }
+  if (active && col_ok) {
+    int32_t cc[P];
+    bool full = false;
+    if constexpr (P >= 4) {
+      full = vec && pe - p0 == P;
+      if (full) {
+#pragma unroll
+        for (int q = 0; q < P; q += 4) {
+          v4i c4 = ld_stream(reinterpret_cast<const v4i *>(col + p0 + q));
+          v4f v4 = ld_stream(reinterpret_cast<const v4f *>(val + p0 + q));
+          cc[q] = c4.x, cc[q + 1] = c4.y, cc[q + 2] = c4.z, cc[q + 3] = c4.w;
+          vv[q] = v4.x, vv[q + 1] = v4.y, vv[q + 2] = v4.z, vv[q + 3] = v4.w;
+        }
+      }
+    }
+    if (!full) {
+#pragma unroll
+      for (int q = 0; q < P; ++q) {
+        cc[q] = -1;
+        if (p0 + q < pe) {
+          cc[q] = ld_stream(col + p0 + q);
+          vv[q] = ld_stream(val + p0 + q);
+        }
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < P; ++q) {
+      if (full || p0 + q < pe) {
+        const float *b = rhs + (int64_t)cc[q] * k + cb;
+        if constexpr (V == 4) {
+          const v4f b4 = *reinterpret_cast<const v4f *>(b);
+          g[q][0] = b4.x;
+          g[q][V > 1 ? 1 : 0] = b4.y;
+          g[q][V > 2 ? 2 : 0] = b4.z;
+          g[q][V > 3 ? 3 : 0] = b4.w;
+        } else {
+          g[q][0] = b[0];
+        }
+      }
+    }
+  }
+
+  const int first_row =
+      row_search_uniform(ro, 1u, (uint32_t)rows + 1u, (int32_t)wbeg);
+  const int last_row = row_search_gallop(ro, (uint32_t)first_row + 1u,
+                                         (uint32_t)rows + 1u,
+                                         (int32_t)(wend - 1));
+  __shared__ int32_t window[1024 / kWave][kWave];
+  int32_t *win = window[threadIdx.x / kWave];
+  const int span = last_row - first_row;
+  const bool use_win = span < kWave;
+  if (use_win) {
+    const int j = first_row + 1 + lane;
+    win[lane] = j <= first_row + 1 + span ? ro[j] : INT32_MAX;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+
+  int lrow = 0, row = 0, closed = 0;
+  float head[V], acc[V];
+#pragma unroll
+  for (int i = 0; i < V; ++i)
+    head[i] = acc[i] = 0.0f;
+  if (active) {
+    int32_t next;
+    if (use_win) {
+      int lo = 0, hi = span;
+      while (lo < hi) {
+        int mid = (lo + hi) >> 1;
+        if (win[mid] <= p0)
+          lo = mid + 1;
+        else
+          hi = mid;
+      }
+      lrow = first_row + lo;
+      next = win[lo];
+    } else {
+      lrow = row_search_lane(ro, (uint32_t)first_row + 1u,
+                             (uint32_t)last_row + 2u, p0);
+      next = ro[lrow + 1];
+    }
+    row = lrow;
+#pragma unroll
+    for (int q = 0; q < P; ++q) {
+      const int32_t p = p0 + q;
+      if (p < pe) {
+        while (p >= next) {
+          if (closed == 0) {
+#pragma unroll
+            for (int i = 0; i < V; ++i)
+              head[i] = acc[i];
+          } else if (col_ok) {
+            float *o = out + (int64_t)row * k + cb;
+#pragma unroll
+            for (int i = 0; i < V; ++i)
+              o[i] = acc[i]; // row began and ended inside this lane
+          }
+          ++closed;
+#pragma unroll
+          for (int i = 0; i < V; ++i)
+            acc[i] = 0.0f;
+          ++row;
+          next = use_win ? win[row - first_row] : ro[row + 1];
+        }
+#pragma unroll
+        for (int i = 0; i < V; ++i)
+          acc[i] = __builtin_fmaf(vv[q], g[q][i], acc[i]);
+      }
+    }
+  }
+
+  // segmented scan of the virtual lanes' tails (lanes l and l - CL*j share
+  // a column slot)
+  const int key = active ? row : -1;
+  float sc[V];
+#pragma unroll
+  for (int i = 0; i < V; ++i)
+    sc[i] = active ? acc[i] : 0.0f;
+  if constexpr (CL == 1) {
+#pragma unroll
+    for (int i = 0; i < V; ++i)
+      sc[i] = wave_segmented_scan(key, sc[i]);
+  } else {
+#pragma unroll
+    for (int off = CL; off < kWave; off <<= 1) {
+      const int k2 = __shfl_up(key, off, kWave);
+      const bool take = lane >= off && k2 == key;
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        const float v2 = __shfl_up(sc[i], off, kWave);
+        sc[i] += take ? v2 : 0.0f;
+      }
+    }
+  }
+  int prev_key = __shfl_up(key, CL, kWave);
+  if (lane < CL)
+    prev_key = INT32_MIN;
+  float prev_sc[V];
+#pragma unroll
+  for (int i = 0; i < V; ++i)
+    prev_sc[i] = __shfl_up(sc[i], CL, kWave);
+  int next_lrow = __shfl_down(active ? lrow : -2, CL, kWave);
+  if (lane >= kWave - CL)
+    next_lrow = -2;
+  if (active && col_ok) {
+    if (closed > 0) {
+      float *o = out + (int64_t)lrow * k + cb;
+      const bool carry = prev_key == lrow;
+#pragma unroll
+      for (int i = 0; i < V; ++i)
+        unsafeAtomicAdd(o + i, head[i] + (carry ? prev_sc[i] : 0.0f));
+    }
+    if (next_lrow != row) {
+      float *o = out + (int64_t)row * k + cb;
+#pragma unroll
+      for (int i = 0; i < V; ++i)
+        unsafeAtomicAdd(o + i, sc[i]);
+    }
+  }
+}
+
+template <int V, int CL, int P>
+void launch_wpos(int64_t grid, int64_t B, hipStream_t st, const int32_t *ro,
+                 const int32_t *col, const float *val, const float *rhs,
+                 float *out, int32_t rows, int32_t nnz, int64_t k,
+                 int64_t units, int64_t chunks, int64_t tiles, bool vec) {
+  hipLaunchKernelGGL((spmm_wave_position<V, CL, P>), dim3((unsigned)grid),
+                     dim3((unsigned)B), 0, st, ro, col, val, rhs, out, rows,
+                     nnz, k, units, chunks, tiles, vec);
+}
+
+template <int V, int CL>
+bool dispatch_wpos_p(int P, int64_t grid, int64_t B, hipStream_t st,
+                     const int32_t *ro, const int32_t *col, const float *val,
+                     const float *rhs, float *out, int32_t rows, int32_t nnz,
+                     int64_t k, int64_t units, int64_t chunks, int64_t tiles,
+                     bool vec) {
+  switch (P) {
+  case 1: launch_wpos<V, CL, 1>(grid, B, st, ro, col, val, rhs, out, rows, nnz, k, units, chunks, tiles, vec); return true;
+  case 2: launch_wpos<V, CL, 2>(grid, B, st, ro, col, val, rhs, out, rows, nnz, k, units, chunks, tiles, vec); return true;
+  case 4: launch_wpos<V, CL, 4>(grid, B, st, ro, col, val, rhs, out, rows, nnz, k, units, chunks, tiles, vec); return true;
+  case 8: launch_wpos<V, CL, 8>(grid, B, st, ro, col, val, rhs, out, rows, nnz, k, units, chunks, tiles, vec); return true;
+  case 16: launch_wpos<V, CL, 16>(grid, B, st, ro, col, val, rhs, out, rows, nnz, k, units, chunks, tiles, vec); return true;
+  }
+  return false;
+}
+
+
+// Row r of C computed by one wave: lanes over the output columns, sequential
+// over the row's positions (the fallback of the tile kernel).
+__device__ __forceinline__ void spmm_row_wave(const int32_t *__restrict__ ro,
+                                              const int32_t *__restrict__ col,
+                                              const float *__restrict__ val,
+                                              const float *__restrict__ rhs,
+                                              float *__restrict__ out,
+                                              int64_t r, int64_t k) {
+  const int32_t s = ro[r], e = ro[r + 1];
+  for (int64_t c = lane_id(); c < k; c += kWave) {
+    float acc = 0.0f;
+    for (int32_t p = s; p < e; ++p)
+      acc = __builtin_fmaf(val[p], rhs[(int64_t)col[p] * k + c], acc);
+    out[r * k + c] = acc;
+  }
+}
+
+// SpMM over 16-row tiles on the matrix cores (k % 16 == 0).
+//
+// For a tile whose rows share the last row's column structure
+// (tile_prefix_ok_block), C[r0 .. r0+15][n0 .. n0+15] is a dense product of
+// the tile's values (zero past each row's end) with the rhs rows of the last
+// row's columns, 16 stored entries (four v_mfma_f32_16x16x4_f32 steps) at a
+// time: lane (i, g) supplies val[ro[r0+i] + t0+4g+s], lane (j, g) supplies
+// rhs[c_{t0+4g+s}][n0+j].  The four waves split the stored entries (wave w
+// takes the 32-entry chunks w, w+4, ...), each accumulates four 16-column
+// output tiles, and the partial tiles are summed through LDS.  Tiles without
+// the shared structure are computed row by row.
+__global__ __launch_bounds__(256) void spmm_tile_mfma(
+    const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
+    const float *__restrict__ val, const float *__restrict__ rhs,
+    float *__restrict__ out, int32_t rows, int64_t k) {
+  constexpr int CH = 2; // 16-entry chunks per step
+  __shared__ float part[4][4][4][kWave]; // [wave][n tile][v][lane]
+  const int r0 = blockIdx.x * 16;
+  const int nt = std::min(16, rows - r0);
+  const int wave = threadIdx.x / kWave;
+  __shared__ int verdict;
+  if (!tile_prefix_ok_block(ro, col, r0, nt, &verdict)) {
+    for (int r = r0 + wave; r < r0 + nt; r += 4)
+      spmm_row_wave(ro, col, val, rhs, out, r, k);
+    return;
+  }
+  const int l = lane_id(), i = l & 15, g = l >> 4;
+  const int last = r0 + nt - 1;
+  const int32_t bl = ro[last];
+  const int32_t len_last = ro[last + 1] - bl;
+  const int32_t ra = i < nt ? ro[r0 + i] : 0;
+  const int32_t la = i < nt ? ro[r0 + i + 1] - ra : 0;
+  for (int64_t nb = 0; nb < k; nb += 64) {
+    const int ntiles = (int)std::min<int64_t>(4, (k - nb) / 16);
+    v4f acc[4];
+#pragma unroll
+    for (int n = 0; n < 4; ++n)
+      acc[n] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int32_t t0 = wave * 16 * CH; t0 < len_last; t0 += 4 * 16 * CH) {
+      float a[CH][4];
+      int64_t c[CH][4];
+#pragma unroll
+      for (int h = 0; h < CH; ++h)
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+          const int32_t t = t0 + 16 * h + 4 * g + st;
+          a[h][st] = t < la ? val[ra + t] : 0.0f;
+          c[h][st] = t < len_last ? (int64_t)col[bl + t] : -1;
+        }
+      float bv[CH][4][4];
+#pragma unroll
+      for (int h = 0; h < CH; ++h)
+#pragma unroll
+        for (int n = 0; n < 4; ++n)
+#pragma unroll
+          for (int st = 0; st < 4; ++st)
+            bv[h][n][st] = (n < ntiles && c[h][st] >= 0)
+                               ? rhs[c[h][st] * k + nb + 16 * n + i]
+                               : 0.0f;
+#pragma unroll
+      for (int h = 0; h < CH; ++h)
+#pragma unroll
+        for (int n = 0; n < 4; ++n)
+#pragma unroll
+          for (int st = 0; st < 4; ++st)
+            acc[n] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[h][st],
+                                                          bv[h][n][st], acc[n],
+                                                          0, 0, 0);
+    }
+#pragma unroll
+    for (int n = 0; n < 4; ++n)
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        part[wave][n][v][l] = acc[n][v];
+    __syncthreads();
+    if (wave < ntiles) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const float sum = part[0][wave][v][l] + part[1][wave][v][l] +
+                          part[2][wave][v][l] + part[3][wave][v][l];
+        const int rr = 4 * g + v;
+        if (rr < nt)
+          out[(int64_t)(r0 + rr) * k + nb + 16 * wave + i] = sum;
+      }
+    }
+    __syncthreads();
+  }
+}
+
 template <int V, int CL, int G>
 void launch_tile(int64_t grid, int64_t B, hipStream_t st, const int32_t *ro,
                  const int32_t *col, const float *val, const float *rhs,
@@ -187,6 +534,8 @@ int next_pow2(int v) {
 
 namespace sw {
 
+int launch_fill_zero(float *y, int64_t n, int64_t block, hipStream_t st);
+
 int launch_spmm(const int32_t *ro, const int32_t *col, const float *val,
                 const float *rhs, float *out, int64_t rows, int64_t nnz,
                 int64_t k, const sw_options &o, const char *what,
@@ -228,6 +577,50 @@ int launch_spmm(const int32_t *ro, const int32_t *col, const float *val,
                        dim3((unsigned)B), 0, st, ro, col, val, rhs, out,
                        (int32_t)rows, k, iters, chunk);
     return launch_check("thread-per-position SpMM kernel");
+  }
+  if (streq(o.spmm_mapping, "row-tile-mfma") && k % 16 == 0) {
+    int64_t grid = ceil_div(rows, 16);
+    int rc = check_grid(grid, what);
+    if (rc)
+      return rc;
+    hipLaunchKernelGGL(spmm_tile_mfma, dim3((unsigned)grid), dim3(256), 0, st,
+                       ro, col, val, rhs, out, (int32_t)rows, k);
+    return launch_check("SpMM tile MFMA kernel");
+  }
+  // row-tile-mfma with k not a multiple of 16 takes the position schedule
+  if (streq(o.spmm_mapping, "wave-per-position") ||
+      streq(o.spmm_mapping, "row-tile-mfma")) {
+    int rc = launch_fill_zero(out, rows * k, B, st);
+    if (rc)
+      return rc;
+    if (nnz == 0)
+      return SW_OK;
+    const bool v4 = (k % 4 == 0) && aligned16(rhs) && aligned16(out);
+    const int V = v4 ? 4 : 1;
+    const int CL = std::min(16, next_pow2((int)std::min<int64_t>(
+                                    ceil_div(k, V), 16)));
+    const int P = (int)o.spmm_positions_per_lane;
+    const int64_t PL = 64 / CL;
+    const int64_t units = ceil_div(nnz, P);
+    const int64_t chunks = ceil_div(units, PL);
+    const int64_t tiles = ceil_div(k, (int64_t)CL * V);
+    const int64_t grid = ceil_div(chunks * tiles, B / 64);
+    rc = check_grid(grid, what);
+    if (rc)
+      return rc;
+    const bool vec = aligned16(col) && aligned16(val);
+    bool ok = false;
+#define SW_WPOS(VV, CC)                                                       \
+  if (V == VV && CL == CC)                                                    \
+    ok = dispatch_wpos_p<VV, CC>(P, grid, B, st, ro, col, val, rhs, out,      \
+                                 (int32_t)rows, (int32_t)nnz, k, units,       \
+                                 chunks, tiles, vec);
+    SW_WPOS(4, 1) SW_WPOS(4, 2) SW_WPOS(4, 4) SW_WPOS(4, 8) SW_WPOS(4, 16)
+    SW_WPOS(1, 1) SW_WPOS(1, 2) SW_WPOS(1, 4) SW_WPOS(1, 8) SW_WPOS(1, 16)
+#undef SW_WPOS
+    if (!ok)
+      return fail(SW_ERR_INVALID_OPTION, "no wave-per-position SpMM kernel");
+    return launch_check("wave-per-position SpMM kernel");
   }
   // wave-per-row-tile
   const int T = (int)o.spmm_tile_size;

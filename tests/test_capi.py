@@ -68,6 +68,8 @@ def test_parse_pipeline_string():
 @pytest.mark.parametrize("text,needle", [
     ("spmv-mapping=diagonal", "unsupported SpMV mapping strategy 'diagonal'"),
     ("spmm-mapping=row", "unsupported SpMM mapping strategy 'row'"),
+    ("spmm-mapping=wave-per-position spmm-block-size=96", "wave-per-position requires the SpMM block size to be a multiple of 64, but got 96"),
+    ("spmm-positions-per-lane=3", "spmm-positions-per-lane must be 1, 2, 4, 8 or 16"),
     ("spmv-block-size=0", "SpMV block size must be between 1 and 1024, but got 0"),
     ("spmv-block-size=1025", "SpMV block size must be between 1 and 1024, but got 1025"),
     ("position-block-size=0", "position-parallel block size must be between 1 and 1024"),

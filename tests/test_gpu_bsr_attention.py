@@ -98,7 +98,8 @@ def test_bsr_config4_sample(dev, orc):
 
 # ---- SDDMM / row reduce / row-wise map / attention -------------------------
 
-ROW_OPTS = ["", "sddmm-lanes-per-row=64", "sddmm-block-size=64"]
+ROW_OPTS = ["", "sddmm-lanes-per-row=64", "sddmm-block-size=64",
+            "sddmm-mapping=row-tile-mfma", "sddmm-mapping=wave-per-row"]
 
 
 @pytest.mark.parametrize("opts", ROW_OPTS)
@@ -117,7 +118,7 @@ def test_sddmm_golden_and_random(dev, orc, golden, opts):
     np.testing.assert_array_equal(out.cpu().numpy(), g["expected"])
     csr = W.random_csr(500, 300, 40.0, 2, empty_fraction=0.2)
     rng = np.random.default_rng(2)
-    for kdim in (1, 64, 100):
+    for kdim in (1, 64, 100, 128):
         lhs = rng.standard_normal((500, kdim)).astype(np.float32)
         rhs = rng.standard_normal((kdim, 300)).astype(np.float32)
         for kind in (sw.SDDMM_MUL, sw.SDDMM_AFFINE, sw.SDDMM_DOT):
@@ -210,7 +211,9 @@ def _attention(mask, q, kt, v, alpha, opts):
 
 
 ATT_OPTS = ["", "sddmm-lanes-per-row=64 spmm-mapping=wave-per-row-tile "
-            "spmm-tile-size=32 spmm-lanes-per-row=16"]
+            "spmm-tile-size=32 spmm-lanes-per-row=16",
+            "sddmm-mapping=row-tile-mfma sddmm-lanes-per-row=64 "
+            "spmm-mapping=row-tile-mfma"]
 
 
 @pytest.mark.parametrize("opts", ATT_OPTS)
@@ -240,3 +243,26 @@ def test_attention_config5(dev, orc, opts, seq):
     assert_within_bound(out, ref, bound, rel=2e-5)
     np.testing.assert_allclose(scores, s_ref, rtol=1e-4, atol=1e-6)
     assert math.isfinite(float(out.sum()))
+
+
+@pytest.mark.parametrize("kdim", [64, 128, 32])
+def test_sddmm_tile_mfma_block_mask(dev, orc, kdim):
+    """Block-structured masks take the 16-row MFMA tiles."""
+    mask = W.attention_mask(seq=2048, block=64, window=4, random_blocks=2,
+                            seed=3)
+    rng = np.random.default_rng(kdim)
+    lhs = rng.standard_normal((mask.rows, kdim)).astype(np.float32)
+    rhs = rng.standard_normal((kdim, mask.cols)).astype(np.float32)
+    vals = rng.uniform(-1, 1, mask.nnz).astype(np.float32)
+    out = torch.empty(mask.nnz, device=G.DEV)
+    G.say(f"sddmm tile mfma kdim={kdim}")
+    sw.sddmm(G.t(mask.row_offsets), G.t(mask.column_indices), G.t(vals),
+             G.t(lhs), G.t(rhs), out, sw.SDDMM_AFFINE, 0.125, 0.5,
+             options="sddmm-mapping=row-tile-mfma")
+    torch.cuda.synchronize()
+    ref = orc.sddmm(mask.row_offsets, mask.column_indices, vals, lhs, rhs,
+                    sw.SDDMM_AFFINE, 0.125, 0.5)
+    rows = np.repeat(np.arange(mask.rows), np.diff(mask.row_offsets))
+    absd = np.abs(lhs.astype(np.float64)) @ np.abs(rhs.astype(np.float64))
+    bound = 0.5 * np.abs(vals) + 0.125 * absd[rows, mask.column_indices]
+    assert_within_bound(out.cpu().numpy(), ref, bound)

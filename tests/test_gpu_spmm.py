@@ -26,7 +26,49 @@ MAPPINGS = [
     "spmm-mapping=wave-per-row-tile spmm-tile-size=5 spmm-block-size=128",
     "spmm-mapping=thread-per-position",
     "spmm-mapping=thread-per-position spmm-position-chunk-size=3",
+    "spmm-mapping=wave-per-position",
+    "spmm-mapping=wave-per-position spmm-positions-per-lane=1",
+    "spmm-mapping=wave-per-position spmm-positions-per-lane=2 "
+    "spmm-block-size=64",
+    "spmm-mapping=wave-per-position spmm-positions-per-lane=8",
+    "spmm-mapping=wave-per-position spmm-positions-per-lane=16 "
+    "spmm-block-size=128",
+    "spmm-mapping=row-tile-mfma",
 ]
+
+
+@pytest.mark.parametrize("opts", ["spmm-mapping=row-tile-mfma",
+                                  "spmm-mapping=wave-per-position"])
+@pytest.mark.parametrize("k", [16, 64, 80, 8])
+@pytest.mark.parametrize("block,window", [(64, 4), (16, 3), (32, 2)])
+def test_block_structured(dev, orc, opts, k, block, window):
+    """Block / causal masks: the 16-row tiles take the MFMA path (rows in a
+    tile are prefixes of the tile's last row); a few rows are perturbed so
+    some tiles fall back."""
+    mask = W.attention_mask(seq=1024, block=block, window=window,
+                            random_blocks=2, seed=block)
+    vals = np.random.default_rng(k).uniform(-1, 1, mask.nnz).astype(
+        np.float32)
+    csr = W.CSR(mask.rows, mask.cols, mask.row_offsets,
+                mask.column_indices.copy(), vals)
+    # break the shared structure of a few tiles: drop the first column of
+    # rows 37 and 500 (shift their entries left by one position)
+    for r in (37, 500):
+        a, b = csr.row_offsets[r], csr.row_offsets[r + 1]
+        if b - a > 1:
+            csr.column_indices[a:b - 1] = csr.column_indices[a + 1:b]
+            csr.column_indices[b - 1] = min(csr.column_indices[b - 2] + 1,
+                                            mask.cols - 1)
+            if csr.column_indices[b - 1] <= csr.column_indices[b - 2]:
+                csr.column_indices[b - 1] = csr.column_indices[b - 2]
+    # keep columns strictly increasing inside each row
+    ok = all(np.all(np.diff(csr.column_indices[a:b]) > 0) for a, b in
+             zip(csr.row_offsets[:-1], csr.row_offsets[1:]))
+    if not ok:
+        pytest.skip("perturbation produced a duplicate column")
+    rhs = np.random.default_rng(7).uniform(-1, 1, (mask.cols, k)).astype(
+        np.float32)
+    _check(orc, csr, rhs, G.spmm(csr, rhs, opts))
 
 
 def _check(orc, csr, rhs, out):
@@ -48,7 +90,7 @@ def test_golden(dev, golden, opts, case):
 
 
 @pytest.mark.parametrize("opts", MAPPINGS)
-@pytest.mark.parametrize("k", [1, 4, 7, 64])
+@pytest.mark.parametrize("k", [1, 4, 7, 64, 100])
 def test_ragged(dev, orc, opts, k):
     csr = W.random_csr(700, 600, 15.0, k, empty_fraction=0.25,
                        max_len=600, lognormal=True)
@@ -66,6 +108,10 @@ def config3():
     (4, "spmm-mapping=wave-per-row-tile spmm-tile-size=4"),
     (4, "spmm-mapping=wave-per-row-tile spmm-tile-size=4 spmm-lanes-per-row=16"),
     (64, "spmm-mapping=wave-per-row-tile spmm-tile-size=32 spmm-lanes-per-row=16"),
+    (4, "spmm-mapping=wave-per-position spmm-positions-per-lane=4 "
+        "spmm-block-size=64"),
+    (64, "spmm-mapping=wave-per-position spmm-positions-per-lane=8 "
+         "spmm-block-size=64"),
 ])
 def test_config3_full_size(dev, orc, config3, k, opts):
     csr = config3
