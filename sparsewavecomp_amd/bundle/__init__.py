@@ -1,0 +1,666 @@
+"""lrrt bundle producer and verifier for gfx950 (Wave64).
+
+A bundle is a directory holding ``manifest.json`` plus HSACO code objects --
+``kernels.hsaco`` for a fixed-shape SpMM, ``kernels/<name>.hsaco`` for the
+six sparse-attention kernels -- consumed by a runtime through
+``Bundle::launch(n, args)``: the runtime evaluates the manifest's grid
+expression for ``n`` (output rows, or output elements for the attention
+``output`` kernel), packs the pointer arguments at the recorded kernarg
+offsets and launches the named symbol.
+
+The manifest schema, the argument and buffer ABI and every verifier check
+mirror the reference tool (tools/sparsewave-bundle/sparsewave_bundle_manifest.py:64-193,
+sparsewave_bundle_verify.py:28-300, sparsewave_bundle_ir.py:4-93); the
+supported target constants are gfx950 / Wave64 instead of gfx1101 / Wave32.
+The kernels are this package's HIP sources specialised with -D shape
+constants and compiled by hipcc; HSACO metadata is read with llvm-readobj.
+"""
+from __future__ import annotations
+
+import hashlib
+import json
+import math
+import os
+import re
+import shutil
+import subprocess
+from pathlib import Path
+
+import yaml
+
+MANIFEST_VERSION = 1
+CODE_OBJECT = "kernels.hsaco"
+SUPPORTED_TARGET = "gfx950"
+SUPPORTED_WAVEFRONT_SIZE = 64
+SUPPORTED_BLOCK_SIZE = 64
+SUPPORTED_OPERATION = "spmm"
+SUPPORTED_MAPPING = "wave-per-row-tile"
+SUPPORTED_TILE_SIZES = (1, 2, 4, 8, 16, 32)
+DEFAULT_TILE_SIZE = 4
+SPARSE_ATTENTION = "sparse-attention"
+SPMM_ARGUMENT_NAMES = ("rowOffsets", "columnIndices", "values", "rhs",
+                       "output")
+SCALAR_TYPE_SIZES = {"i32": 4, "i64": 8, "fp32": 4, "fp16": 2, "bf16": 2}
+
+# Stable attention kernel set: role, operation, mapping, launch n, arguments
+# (sparsewave_bundle_ir.py:25-81).
+ATTENTION_KERNELS = {
+    "sparse_attention_scores": {
+        "role": "scores", "operation": "sddmm", "mapping": "thread-per-row",
+        "launch_n": "output_rows",
+        "args": ("rowOffsets", "columnIndices", "maskValues", "query",
+                 "transposedKey", "scores"),
+        "code": 1},
+    "sparse_attention_row_max": {
+        "role": "row_max", "operation": "csr_row_reduce_max",
+        "mapping": "thread-per-row", "launch_n": "output_rows",
+        "args": ("rowOffsets", "scores", "rowMaximum"), "code": 2},
+    "sparse_attention_exp": {
+        "role": "exp", "operation": "csr_rowwise_map",
+        "mapping": "thread-per-row", "launch_n": "output_rows",
+        "args": ("rowOffsets", "rowMaximum", "scores"), "code": 3},
+    "sparse_attention_row_sum": {
+        "role": "row_sum", "operation": "csr_row_reduce_sum",
+        "mapping": "thread-per-row", "launch_n": "output_rows",
+        "args": ("rowOffsets", "scores", "rowSum"), "code": 4},
+    "sparse_attention_normalize": {
+        "role": "normalize", "operation": "csr_rowwise_map",
+        "mapping": "thread-per-row", "launch_n": "output_rows",
+        "args": ("rowOffsets", "rowSum", "scores"), "code": 5},
+    "sparse_attention_output": {
+        "role": "output", "operation": "spmm",
+        "mapping": "thread-per-output", "launch_n": "output_elements",
+        "args": ("rowOffsets", "columnIndices", "scores", "value", "output"),
+        "code": 6},
+}
+ATTENTION_BUFFER_NAMES = ("rowOffsets", "columnIndices", "maskValues",
+                          "query", "transposedKey", "value", "scores",
+                          "rowMaximum", "rowSum", "output")
+
+_HERE = Path(__file__).resolve().parent
+_KERNELS = _HERE / "kernels"
+
+
+class BundleError(ValueError):
+    """A bundle request or a manifest failed validation."""
+
+
+def fail(message: str):
+    raise BundleError(message)
+
+
+# ---- tools ---------------------------------------------------------------
+
+
+def find_tool(name: str) -> str:
+    for cand in (shutil.which(name), f"/opt/rocm/llvm/bin/{name}",
+                 f"/opt/rocm/bin/{name}"):
+        if cand and os.path.exists(cand):
+            return cand
+    fail(f"cannot find {name}")
+
+
+def run(cmd, **kw):
+    res = subprocess.run(cmd, capture_output=True, text=True, **kw)
+    if res.returncode:
+        raise RuntimeError(f"command failed ({res.returncode}): "
+                           f"{' '.join(map(str, cmd))}\n{res.stderr}")
+    return res
+
+
+def compile_hsaco(source: Path, out: Path, defines: dict) -> Path:
+    """hipcc a single-kernel device code object (raw ELF, no bundle)."""
+    cmd = [find_tool("hipcc"), f"--offload-arch={SUPPORTED_TARGET}",
+           "--genco", "--no-gpu-bundle-output", "-O3", "-std=c++17",
+           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+           "-Wno-unused-command-line-argument"]
+    for k, v in defines.items():
+        cmd.append(f"-D{k}={v}")
+    cmd += [str(source), "-o", str(out)]
+    run(cmd)
+    return out
+
+
+# ---- HSACO metadata --------------------------------------------------------
+
+
+def _metadata_text(readobj_json: str) -> str:
+    found = []
+
+    def visit(v):
+        if isinstance(v, dict):
+            for key, child in v.items():
+                if key == "AMDGPU Metadata":
+                    found.append(child)
+                else:
+                    visit(child)
+        elif isinstance(v, list):
+            for child in v:
+                visit(child)
+
+    visit(json.loads(readobj_json))
+    if len(found) != 1:
+        fail(f"expected one AMDGPU metadata document, found {len(found)}")
+    return found[0]
+
+
+def parse_metadata(text: str) -> dict:
+    """Target and kernel descriptors from AMDGPU code-object metadata."""
+    doc = yaml.safe_load(text)
+    if not isinstance(doc, dict) or "amdhsa.kernels" not in doc:
+        fail("AMDGPU metadata has no amdhsa.kernels")
+    target = str(doc.get("amdhsa.target", ""))
+    m = re.search(r"(gfx[0-9a-z]+)(?::[^-]+)?$", target)
+    if not m:
+        fail(f"cannot determine the AMDGPU chip from target '{target}'")
+    kernels = []
+    for k in doc["amdhsa.kernels"]:
+        for field in (".name", ".symbol", ".kernarg_segment_size",
+                      ".group_segment_fixed_size",
+                      ".max_flat_workgroup_size", ".wavefront_size"):
+            if field not in k:
+                fail(f"kernel metadata is missing {field}")
+        args = []
+        for a in k.get(".args", []) or []:
+            args.append({key.lstrip("."): val for key, val in a.items()})
+        block = k.get(".reqd_workgroup_size") or [
+            k[".max_flat_workgroup_size"], 1, 1]
+        kernels.append({
+            "name": k[".name"],
+            "descriptor_symbol": k[".symbol"],
+            "args": args,
+            "kernarg_size": k[".kernarg_segment_size"],
+            "block": list(block),
+            "fixed_group_segment_bytes": k[".group_segment_fixed_size"],
+            "wavefront_size": k[".wavefront_size"],
+        })
+    return {"target": m.group(1), "kernels": kernels}
+
+
+def inspect_hsaco(hsaco: Path, readobj: str | None = None) -> dict:
+    readobj = readobj or find_tool("llvm-readobj")
+    out = run([readobj, "--notes", "--elf-output-style=JSON",
+               str(hsaco)]).stdout
+    return parse_metadata(_metadata_text(out))
+
+
+# ---- manifest ----------------------------------------------------------------
+
+
+def grid_expression(block_size: int, wavefront_size: int) -> str:
+    """Total work-items for wave-per-unit mappings."""
+    return f"ceil_div(n, {block_size // wavefront_size}) * {block_size}"
+
+
+def linear_grid_expression(block_size: int) -> str:
+    return f"ceil_div(n, {block_size}) * {block_size}"
+
+
+def evaluate_grid(expr: str, n: int) -> int:
+    """Evaluate the manifest's total-work-item expression for n."""
+    m = re.fullmatch(r"ceil_div\(n, (\d+)\) \* (\d+)", expr)
+    if not m:
+        fail(f"unsupported grid expression '{expr}'")
+    d, b = int(m.group(1)), int(m.group(2))
+    return -(-n // d) * b
+
+
+def merge_arguments(ir_args, metadata_args):
+    if len(ir_args) != len(metadata_args):
+        fail("compiler IR and HSACO kernel argument counts differ: "
+             f"{len(ir_args)} != {len(metadata_args)}")
+    merged = []
+    for ir, md in zip(ir_args, metadata_args):
+        if "offset" not in md or "size" not in md:
+            fail("HSACO kernel argument is missing offset or size")
+        if ir["type"] == "ptr":
+            if md.get("value_kind") != "global_buffer":
+                fail(f"IR pointer argument '{ir['name']}' does not map to an "
+                     "HSACO global_buffer argument")
+            if md.get("size") != 8:
+                fail(f"IR pointer argument '{ir['name']}' must have an "
+                     "8-byte HSACO entry")
+        else:
+            size = SCALAR_TYPE_SIZES.get(ir["type"])
+            if size is None:
+                fail(f"unsupported scalar ABI type '{ir['type']}'")
+            if md.get("value_kind") != "by_value" or md.get("size") != size:
+                fail(f"IR scalar argument '{ir['name']}' does not match its "
+                     "HSACO by_value entry")
+        merged.append({**ir, "offset": md["offset"], "size": md["size"]})
+    return merged
+
+
+def _sha256(path: Path) -> str:
+    return hashlib.sha256(path.read_bytes()).hexdigest()
+
+
+def _prepare_output(output: Path) -> Path:
+    output = Path(output).resolve()
+    if output.exists() and (not output.is_dir() or any(output.iterdir())):
+        fail(f"output directory is not empty: {output}")
+    output.mkdir(parents=True, exist_ok=True)
+    return output
+
+
+# ---- producers ---------------------------------------------------------------
+
+
+def _check_target(chip, wavefront_size, block_size):
+    expected = {"chip": (chip, SUPPORTED_TARGET),
+                "wavefront size": (wavefront_size, SUPPORTED_WAVEFRONT_SIZE),
+                "block size": (block_size, SUPPORTED_BLOCK_SIZE)}
+    for label, (actual, supported) in expected.items():
+        if actual != supported:
+            fail(f"gfx950 lrrt bundle support requires {label} {supported}, "
+                 f"got {actual}")
+
+
+def build_spmm_bundle(output, rows: int, rhs_columns: int,
+                      tile_size: int = DEFAULT_TILE_SIZE,
+                      mapping: str = SUPPORTED_MAPPING,
+                      block_size: int = SUPPORTED_BLOCK_SIZE,
+                      wavefront_size: int = SUPPORTED_WAVEFRONT_SIZE,
+                      chip: str = SUPPORTED_TARGET) -> dict:
+    """Fixed-shape SpMM bundle: rowOffsets[rows+1], rhs[*][K], output[rows][K]
+    with K == tile size (one tile per output row)."""
+    _check_target(chip, wavefront_size, block_size)
+    if mapping != SUPPORTED_MAPPING:
+        fail(f"gfx950 lrrt bundle support requires mapping "
+             f"{SUPPORTED_MAPPING}, got {mapping}")
+    if tile_size not in SUPPORTED_TILE_SIZES:
+        fail(f"gfx950 lrrt bundle support requires a tile size in "
+             f"{SUPPORTED_TILE_SIZES}, got {tile_size}")
+    if rows <= 0:
+        fail("output and RHS row extents must be positive")
+    if rhs_columns != tile_size:
+        fail("lrrt bundle support requires RHS/output columns equal tile "
+             f"size {tile_size}")
+    output = _prepare_output(output)
+    hsaco = compile_hsaco(_KERNELS / "bundle_spmm.hip", output / CODE_OBJECT,
+                          {"SW_ROWS": rows, "SW_K": rhs_columns})
+    metadata = inspect_hsaco(hsaco)
+    if metadata["target"] != chip:
+        fail(f"requested target {chip} does not match HSACO target "
+             f"{metadata['target']}")
+    if len(metadata["kernels"]) != 1:
+        fail(f"expected one HSACO kernel, found {len(metadata['kernels'])}")
+    kernel = metadata["kernels"][0]
+    if kernel["wavefront_size"] != wavefront_size:
+        fail("HSACO wavefront size does not match the requested Wave64 target")
+    if kernel["block"] != [block_size, 1, 1]:
+        fail("HSACO workgroup size does not match the requested block")
+    ir_args = [{"name": n, "type": "ptr"} for n in SPMM_ARGUMENT_NAMES]
+    manifest = {
+        "manifest_version": MANIFEST_VERSION,
+        "target": metadata["target"],
+        "kernels": [{
+            "name": SUPPORTED_OPERATION,
+            "symbol": kernel["name"],
+            "code_object": CODE_OBJECT,
+            "args": merge_arguments(ir_args, kernel["args"]),
+            "kernarg_size": kernel["kernarg_size"],
+            "block": kernel["block"],
+            "grid": [grid_expression(block_size, wavefront_size), 1, 1],
+            "shared_memory_bytes": 0,
+            "workspace_bytes": 0,
+            "sparsewave": {
+                "operation": SUPPORTED_OPERATION,
+                "mapping": mapping,
+                "tile_size": tile_size,
+                "wavefront_size": wavefront_size,
+                "hsaco_sha256": _sha256(hsaco),
+                "fixed_group_segment_bytes":
+                    kernel["fixed_group_segment_bytes"],
+                "launch_n": "output_rows",
+                "fixed_output_rows": rows,
+            },
+        }],
+    }
+    (output / "manifest.json").write_text(json.dumps(manifest, indent=2) +
+                                          "\n")
+    return manifest
+
+
+def attention_buffers(rows, key_rows, head_dim, value_cols) -> dict:
+    """The ten-buffer ABI with dtype/shape/kind (sparsewave_bundle_ir.py:82-93,
+    specialised shapes as parse_sparse_attention_ir_text records them)."""
+    spec = {
+        "rowOffsets": ("i32", [rows + 1], "input"),
+        "columnIndices": ("i32", [None], "input"),
+        "maskValues": ("fp32", [None], "input"),
+        "query": ("fp32", [rows, head_dim], "input"),
+        "transposedKey": ("fp32", [head_dim, key_rows], "input"),
+        "value": ("fp32", [key_rows, value_cols], "input"),
+        "scores": ("fp32", [None], "intermediate"),
+        "rowMaximum": ("fp32", [rows], "intermediate"),
+        "rowSum": ("fp32", [rows], "intermediate"),
+        "output": ("fp32", [rows, value_cols], "output"),
+    }
+    buffers = {}
+    for name in ATTENTION_BUFFER_NAMES:
+        dtype, shape, kind = spec[name]
+        tensor = {"dtype": dtype, "rank": len(shape), "shape": shape,
+                  "specialized": None not in shape}
+        if None in shape:
+            tensor["dynamic_dimensions"] = [{"index": 0, "name": "nnz"}]
+        buffers[name] = {"name": name, "type": "ptr", "tensor": tensor,
+                         "kind": kind}
+    return buffers
+
+
+def build_attention_bundle(output, rows: int, key_rows: int, head_dim: int,
+                           value_cols: int, alpha: float | None = None,
+                           beta: float = 0.0,
+                           block_size: int = SUPPORTED_BLOCK_SIZE,
+                           wavefront_size: int = SUPPORTED_WAVEFRONT_SIZE,
+                           chip: str = SUPPORTED_TARGET) -> dict:
+    """Six-kernel sparse-attention bundle, kernels/<name>.hsaco each."""
+    _check_target(chip, wavefront_size, block_size)
+    for label, v in (("output rows", rows), ("key/value rows", key_rows),
+                     ("head dimension", head_dim),
+                     ("value columns", value_cols)):
+        if type(v) is not int or v <= 0:
+            fail(f"SparseAttention {label} must be a positive integer")
+    if alpha is None:
+        alpha = 1.0 / math.sqrt(head_dim)
+    output = _prepare_output(output)
+    (output / "kernels").mkdir()
+    buffers = attention_buffers(rows, key_rows, head_dim, value_cols)
+    specialization = {"output_rows": rows, "key_value_rows": key_rows,
+                      "head_dimension": head_dim,
+                      "value_columns": value_cols}
+    entries = []
+    for name in sorted(ATTENTION_KERNELS):
+        spec = ATTENTION_KERNELS[name]
+        rel = f"kernels/{name}.hsaco"
+        hsaco = compile_hsaco(
+            _KERNELS / "bundle_attention.hip", output / rel,
+            {"SW_ATTENTION_ROLE": spec["code"], "SW_ROWS": rows,
+             "SW_KEY_ROWS": key_rows, "SW_HEAD_DIM": head_dim,
+             "SW_VALUE_COLS": value_cols,
+             "SW_ALPHA": f"{float(alpha)!r}f".replace("inf", "INFINITY"),
+             "SW_BETA": f"{float(beta)!r}f"})
+        md = inspect_hsaco(hsaco)
+        if md["target"] != chip:
+            fail(f"requested target {chip} does not match HSACO target "
+                 f"{md['target']}")
+        if len(md["kernels"]) != 1:
+            fail(f"expected one kernel in {hsaco}, found {len(md['kernels'])}")
+        k = md["kernels"][0]
+        if k["name"] != name:
+            fail(f"stable kernel name '{name}' does not match HSACO .name "
+                 f"'{k['name']}'")
+        if k["wavefront_size"] != wavefront_size:
+            fail(f"kernel '{name}' does not use the requested wavefront size")
+        if k["block"] != [block_size, 1, 1]:
+            fail(f"kernel '{name}' does not use the requested block size")
+        producer = {
+            "application": SPARSE_ATTENTION, "role": spec["role"],
+            "operation": spec["operation"], "mapping": spec["mapping"],
+            "launch_n": spec["launch_n"], "hsaco_sha256": _sha256(hsaco),
+            "fixed_group_segment_bytes": k["fixed_group_segment_bytes"],
+            "specialization": specialization,
+        }
+        if spec["role"] == "scores":
+            producer["scale"] = {"alpha": float(alpha), "beta": float(beta)}
+        entries.append({
+            "name": name, "symbol": k["name"], "code_object": rel,
+            "args": merge_arguments([buffers[a] for a in spec["args"]],
+                                    k["args"]),
+            "kernarg_size": k["kernarg_size"], "block": k["block"],
+            "grid": [linear_grid_expression(block_size), 1, 1],
+            "shared_memory_bytes": 0, "workspace_bytes": 0,
+            "sparsewave": producer,
+        })
+    manifest = {
+        "manifest_version": MANIFEST_VERSION,
+        "target": chip,
+        "kernels": entries,
+        "sparsewave": {
+            "application": SPARSE_ATTENTION,
+            "buffers": [buffers[n] for n in sorted(buffers)],
+            "specialization": specialization,
+        },
+    }
+    (output / "manifest.json").write_text(json.dumps(manifest, indent=2) +
+                                          "\n")
+    return manifest
+
+
+# ---- verifier ----------------------------------------------------------------
+
+
+def _validate_arguments(kernel, hsaco_kernel, expected_names):
+    margs = kernel.get("args")
+    hargs = hsaco_kernel["args"]
+    if not isinstance(margs, list) or len(margs) != len(hargs):
+        fail("manifest and HSACO kernel argument counts differ")
+    if len(expected_names) != len(hargs):
+        fail("manifest argument names do not match the kernel ABI contract")
+    for i, (ma, ha) in enumerate(zip(margs, hargs)):
+        if ma.get("name") != expected_names[i]:
+            fail("manifest argument name does not match the ABI contract")
+        if ma.get("offset") != ha.get("offset"):
+            fail("manifest argument offset does not match HSACO metadata")
+        if ma.get("size") != ha.get("size"):
+            fail("manifest argument size does not match HSACO metadata")
+        if ma.get("type") == "ptr":
+            if ha.get("value_kind") != "global_buffer":
+                fail("manifest ptr argument does not match HSACO "
+                     "global_buffer")
+            if ha.get("size") != 8:
+                fail("manifest ptr argument must occupy 8 bytes")
+        else:
+            t = ma.get("type")
+            if t not in SCALAR_TYPE_SIZES:
+                fail(f"unsupported manifest argument type '{t}'")
+            if ha.get("value_kind") != "by_value":
+                fail("manifest scalar argument does not match HSACO by_value")
+            if ha.get("size") != SCALAR_TYPE_SIZES[t]:
+                fail("manifest scalar argument has the wrong bit width")
+
+
+def _validate_common(kernel, hsaco_kernel, digest):
+    if kernel.get("symbol") != hsaco_kernel["name"]:
+        fail("manifest kernel symbol does not match HSACO .name")
+    if kernel.get("kernarg_size") != hsaco_kernel["kernarg_size"]:
+        fail("manifest kernarg_size does not match HSACO metadata")
+    if kernel.get("block") != hsaco_kernel["block"]:
+        fail("manifest block does not match HSACO metadata")
+    if kernel.get("shared_memory_bytes") != 0:
+        fail("fixed HSACO group segment must not be dynamic shared memory")
+    if kernel.get("workspace_bytes") != 0:
+        fail("SparseWave bundles do not support workspace")
+    producer = kernel.get("sparsewave")
+    if not isinstance(producer, dict):
+        fail("kernel is missing sparsewave producer metadata")
+    if producer.get("hsaco_sha256") != digest:
+        fail("invalid sparsewave producer field 'hsaco_sha256'")
+    if producer.get("fixed_group_segment_bytes") != hsaco_kernel[
+            "fixed_group_segment_bytes"]:
+        fail("invalid sparsewave producer field 'fixed_group_segment_bytes'")
+
+
+def _validate_spmm(kernel, hsaco_kernel, digest):
+    if kernel.get("name") != SUPPORTED_OPERATION:
+        fail("SparseWave SpMM logical kernel name must be 'spmm'")
+    if kernel.get("code_object") != CODE_OBJECT:
+        fail(f"kernel code_object must be '{CODE_OBJECT}'")
+    _validate_common(kernel, hsaco_kernel, digest)
+    _validate_arguments(kernel, hsaco_kernel, SPMM_ARGUMENT_NAMES)
+    producer = kernel["sparsewave"]
+    expected = {"operation": SUPPORTED_OPERATION,
+                "mapping": SUPPORTED_MAPPING,
+                "wavefront_size": SUPPORTED_WAVEFRONT_SIZE,
+                "launch_n": "output_rows"}
+    for field, value in expected.items():
+        if producer.get(field) != value:
+            fail(f"invalid sparsewave producer field '{field}'")
+    if producer.get("tile_size") not in SUPPORTED_TILE_SIZES:
+        fail("invalid sparsewave producer field 'tile_size'")
+    rows = producer.get("fixed_output_rows")
+    if type(rows) is not int or rows <= 0:
+        fail("invalid sparsewave producer field 'fixed_output_rows'")
+    if kernel.get("grid") != [grid_expression(SUPPORTED_BLOCK_SIZE,
+                                              SUPPORTED_WAVEFRONT_SIZE), 1, 1]:
+        fail("manifest grid is not the supported total-work-item expression")
+
+
+def _validate_attention(manifest, artifacts):
+    producer = manifest.get("sparsewave")
+    if not isinstance(producer, dict) or producer.get(
+            "application") != SPARSE_ATTENTION:
+        fail("SparseAttention manifest is missing application metadata")
+    if "execution_order" in manifest or "execution_order" in producer:
+        fail("SparseAttention execution order belongs to the runtime Executor")
+    buffers = producer.get("buffers")
+    if not isinstance(buffers, list):
+        fail("SparseAttention manifest is missing buffer ABI metadata")
+    by_name = {b.get("name"): b for b in buffers}
+    if len(by_name) != len(buffers):
+        fail("SparseAttention buffer names must be unique")
+    if set(by_name) != set(ATTENTION_BUFFER_NAMES):
+        fail("SparseAttention manifest does not contain the stable buffer ABI")
+    spec = producer.get("specialization")
+    keys = {"output_rows", "key_value_rows", "head_dimension",
+            "value_columns"}
+    if not isinstance(spec, dict) or set(spec) != keys:
+        fail("SparseAttention specialization metadata is incomplete")
+    if any(type(v) is not int or v <= 0 for v in spec.values()):
+        fail("SparseAttention specialization values must be positive integers")
+    expected_buffers = attention_buffers(spec["output_rows"],
+                                         spec["key_value_rows"],
+                                         spec["head_dimension"],
+                                         spec["value_columns"])
+    for name, want in expected_buffers.items():
+        got = by_name[name]
+        if got.get("type") != "ptr" or got.get("kind") != want["kind"]:
+            fail(f"SparseAttention buffer '{name}' has an invalid ABI role")
+        if got.get("tensor") != want["tensor"]:
+            fail(f"SparseAttention buffer '{name}' has invalid tensor "
+                 "metadata")
+    kernels = manifest.get("kernels")
+    if not isinstance(kernels, list):
+        fail("manifest kernels must be an array")
+    kernels_by_name = {k.get("name"): k for k in kernels}
+    if set(kernels_by_name) != set(ATTENTION_KERNELS):
+        fail("SparseAttention manifest does not contain the stable kernel set")
+    if [k.get("name") for k in kernels] != sorted(ATTENTION_KERNELS):
+        fail("SparseAttention kernels must be emitted deterministically")
+    for name, kspec in ATTENTION_KERNELS.items():
+        kernel = kernels_by_name[name]
+        if kernel.get("code_object") != f"kernels/{name}.hsaco":
+            fail(f"kernel '{name}' has an unstable artifact path")
+        art = artifacts[kernel["code_object"]]
+        if len(art["metadata"]["kernels"]) != 1:
+            fail(f"kernel '{name}' artifact must contain one entry point")
+        _validate_common(kernel, art["kernel"], art["digest"])
+        _validate_arguments(kernel, art["kernel"], kspec["args"])
+        if kernel.get("grid") != [linear_grid_expression(
+                SUPPORTED_BLOCK_SIZE), 1, 1]:
+            fail(f"kernel '{name}' has an invalid total-work-item grid")
+        kp = kernel["sparsewave"]
+        expected = {"application": SPARSE_ATTENTION, "role": kspec["role"],
+                    "operation": kspec["operation"],
+                    "mapping": kspec["mapping"],
+                    "launch_n": kspec["launch_n"], "specialization": spec}
+        for field, value in expected.items():
+            if kp.get(field) != value:
+                fail(f"kernel '{name}' has invalid producer field '{field}'")
+        for arg in kernel["args"]:
+            if arg["name"] not in by_name:
+                fail(f"kernel '{name}' refers to an unknown buffer")
+            semantic = {k: arg[k] for k in ("name", "type", "tensor", "kind")
+                        if k in arg}
+            if semantic != by_name[arg["name"]]:
+                fail(f"kernel '{name}' buffer ABI metadata is inconsistent")
+
+
+def verify_bundle(bundle, inspect=inspect_hsaco) -> dict:
+    """Check a bundle directory the way the reference verifier does
+    (sparsewave_bundle_verify.py:236-300); returns the manifest."""
+    bundle = Path(bundle)
+    manifest = json.loads((bundle / "manifest.json").read_text())
+    if type(manifest.get("manifest_version")) is not int or manifest[
+            "manifest_version"] != MANIFEST_VERSION:
+        fail(f"unsupported manifest_version: "
+             f"{manifest.get('manifest_version')}")
+    if manifest.get("target") != SUPPORTED_TARGET:
+        fail(f"SparseWave gfx950 bundle target must be {SUPPORTED_TARGET}")
+    kernels = manifest.get("kernels")
+    if not isinstance(kernels, list) or not kernels:
+        fail("manifest kernels must be a non-empty array")
+    artifacts, names = {}, set()
+    for kernel in kernels:
+        if not isinstance(kernel, dict):
+            fail("manifest kernel entries must be objects")
+        name = kernel.get("name")
+        if not isinstance(name, str) or not name:
+            fail("manifest kernel name must be a non-empty string")
+        if name in names:
+            fail(f"duplicate manifest kernel name '{name}'")
+        names.add(name)
+        rel = kernel.get("code_object")
+        if not isinstance(rel, str):
+            fail("kernel code_object must be a relative path")
+        rp = Path(rel)
+        if rp.is_absolute() or ".." in rp.parts:
+            fail("kernel code_object must be relative to the bundle directory")
+        if rel not in artifacts:
+            hsaco = bundle / rp
+            md = inspect(hsaco)
+            if manifest["target"] != md["target"]:
+                fail("manifest target does not match HSACO architecture")
+            artifacts[rel] = {"metadata": md, "digest": _sha256(hsaco)}
+        md = artifacts[rel]["metadata"]
+        by_name = {k["name"]: k for k in md["kernels"]}
+        symbol = kernel.get("symbol")
+        if symbol not in by_name:
+            fail(f"manifest kernel symbol '{symbol}' is missing from HSACO")
+        artifacts[rel]["kernel"] = by_name[symbol]
+    if manifest.get("sparsewave", {}).get("application") == SPARSE_ATTENTION:
+        _validate_attention(manifest, artifacts)
+    else:
+        if len(kernels) != 1 or len(artifacts) != 1:
+            fail("SpMM bundle must contain exactly one kernel artifact")
+        k = kernels[0]
+        art = artifacts[k["code_object"]]
+        _validate_spmm(k, art["kernel"], art["digest"])
+    return manifest
+
+
+# ---- fixed-shape IR input ----------------------------------------------------
+
+
+def parse_spmm_signature(text: str) -> dict:
+    """Shapes of a fixed-shape function holding ``sparsewave.spmm`` on
+    memrefs (the input form sparsewave_bundle_ir.py:161-208 accepts):
+    returns rows and rhs columns."""
+    op = re.search(r"^\s*sparsewave\.spmm\b", text, re.MULTILINE)
+    if op is None:
+        fail("expected one fixed-shape function containing sparsewave.spmm")
+    funcs = list(re.finditer(r"func\.func\s+@[\w.$-]+\s*\((.*?)\)\s*\{",
+                             text[:op.start()], re.DOTALL))
+    if not funcs:
+        fail("expected a function containing the SparseWave application")
+    types = re.findall(r"%[\w.$-]+\s*:\s*(memref<[^>]+>)", funcs[-1].group(1))
+    if len(types) != len(SPMM_ARGUMENT_NAMES):
+        fail("fixed-shape SpMM bundle requires exactly five kernel arguments")
+    pats = (r"memref<(\d+)xi32>", r"memref<(\d+|\?)xi32>",
+            r"memref<(\d+|\?)xf32>", r"memref<(\d+)x(\d+)xf32>",
+            r"memref<(\d+)x(\d+)xf32>")
+    ms = [re.fullmatch(p, t) for p, t in zip(pats, types)]
+    if not all(ms):
+        fail("bundle input must use fixed-shape CSR i32 and FP32 SpMM memrefs")
+    rows, k = int(ms[4].group(1)), int(ms[3].group(2))
+    if int(ms[0].group(1)) != rows + 1:
+        fail("rowOffsets extent must equal output rows plus one")
+    if k != int(ms[4].group(2)):
+        fail("RHS and output column extents must match")
+    if ms[1].group(1) != "?" and ms[2].group(1) != "?" and \
+            ms[1].group(1) != ms[2].group(1):
+        fail("columnIndices and values extents must match")
+    if rows <= 0 or int(ms[3].group(1)) <= 0:
+        fail("output and RHS row extents must be positive")
+    return {"rows": rows, "rhs_columns": k}

@@ -1,0 +1,77 @@
+"""Bundles run on the GPU through a stand-in of lrrt's launch(n, args) and
+match the CPU oracle (fp32 bound |y - y_ref| <= 1e-5 sum|a*b|)."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from sparsewavecomp_amd import bundle as B
+from sparsewavecomp_amd import workloads as W
+from tests import gpu_util as G
+from tests._check import assert_within_bound
+from tests.lrrt_stub import Bundle
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("tile", [4, 1, 8])
+def test_spmm_bundle_matches_oracle(dev, orc, tmp_path, tile):
+    csr = W.random_csr(3000, 2000, 20.0, tile, empty_fraction=0.2,
+                       lognormal=True, max_len=2000)
+    rhs = np.random.default_rng(1).uniform(-1, 1, (2000, tile)).astype(
+        np.float32)
+    B.build_spmm_bundle(tmp_path / "b", rows=csr.rows, rhs_columns=tile,
+                        tile_size=tile)
+    B.verify_bundle(tmp_path / "b")
+    bun = Bundle(tmp_path / "b")
+    ro, col, val, b = (G.t(csr.row_offsets), G.t(csr.column_indices),
+                       G.t(csr.values), G.t(rhs))
+    out = torch.full((csr.rows, tile), float("nan"), device=G.DEV)
+    G.say(f"bundle spmm tile={tile}")
+    bun.launch("spmm", csr.rows, {"rowOffsets": ro.data_ptr(),
+                                  "columnIndices": col.data_ptr(),
+                                  "values": val.data_ptr(),
+                                  "rhs": b.data_ptr(),
+                                  "output": out.data_ptr()})
+    torch.cuda.synchronize()
+    bun.close()
+    ref = orc.spmm(csr.row_offsets, csr.column_indices, csr.values, rhs)
+    bound = orc.spmm_abs_bound(csr.row_offsets, csr.column_indices,
+                               csr.values, rhs)
+    assert_within_bound(out.cpu().numpy(), ref, bound)
+
+
+def test_attention_bundle_matches_oracle(dev, orc, tmp_path):
+    mask, q, kt, v, alpha = W.config5(seed=0, seq=512, d=64)
+    v = v[:, :32].copy()
+    B.build_attention_bundle(tmp_path / "b", rows=512, key_rows=512,
+                             head_dim=64, value_cols=32, alpha=alpha)
+    B.verify_bundle(tmp_path / "b")
+    bun = Bundle(tmp_path / "b")
+    bufs = {"rowOffsets": G.t(mask.row_offsets),
+            "columnIndices": G.t(mask.column_indices),
+            "maskValues": G.t(mask.values), "query": G.t(q),
+            "transposedKey": G.t(kt), "value": G.t(v),
+            "scores": torch.empty(mask.nnz, device=G.DEV),
+            "rowMaximum": torch.empty(512, device=G.DEV),
+            "rowSum": torch.empty(512, device=G.DEV),
+            "output": torch.full((512, 32), float("nan"), device=G.DEV)}
+    ptrs = {k: t.data_ptr() for k, t in bufs.items()}
+    # the runtime executor's order (the manifest deliberately has none)
+    order = ["sparse_attention_scores", "sparse_attention_row_max",
+             "sparse_attention_exp", "sparse_attention_row_sum",
+             "sparse_attention_normalize", "sparse_attention_output"]
+    G.say("bundle attention")
+    for name in order:
+        n = 512 * 32 if name == "sparse_attention_output" else 512
+        bun.launch(name, n, ptrs)
+    torch.cuda.synchronize()
+    bun.close()
+    s_ref, m_ref, r_ref, ref = orc.sparse_attention(
+        mask.row_offsets, mask.column_indices, mask.values, q, kt, v, alpha)
+    bound = orc.spmm_abs_bound(mask.row_offsets, mask.column_indices, s_ref, v)
+    assert_within_bound(bufs["output"].cpu().numpy(), ref, bound, rel=2e-5)
+    np.testing.assert_allclose(bufs["rowMaximum"].cpu().numpy(), m_ref,
+                               rtol=1e-5, atol=1e-6)
+    assert math.isfinite(float(bufs["rowSum"].sum()))
