@@ -287,6 +287,39 @@ __global__ __launch_bounds__(256) void rowwise_map_wave(
     out[p] = map_value(kind, val[p], rv);
 }
 
+
+// The four row ops of the attention chain fused (row max, exp(s - max), row
+// sum, s / sum): one wave per row, one read and one write of the row's
+// scores besides the max pass; rowMaximum and rowSum are written as the
+// separate ops would write them.
+__global__ __launch_bounds__(256) void row_softmax_wave(
+    const int32_t *__restrict__ ro, float *scores, float *__restrict__ rmax,
+    float *__restrict__ rsum, int32_t rows) {
+  const int64_t r = (int64_t)blockIdx.x * (blockDim.x / kWave) +
+                    threadIdx.x / kWave;
+  if (r >= rows)
+    return;
+  const int l = lane_id();
+  const int32_t s = ro[r], e = ro[r + 1];
+  float m = -INFINITY;
+  for (int32_t p = s + l; p < e; p += kWave)
+    m = maximumf(m, scores[p]);
+  m = wave_max(m);
+  float sum = 0.0f;
+  for (int32_t p = s + l; p < e; p += kWave) {
+    const float v = expf(scores[p] - m);
+    scores[p] = v;
+    sum += v;
+  }
+  sum = group_sum<kWave>(sum);
+  for (int32_t p = s + l; p < e; p += kWave)
+    scores[p] = scores[p] / sum;
+  if (l == 0) {
+    rmax[r] = m;
+    rsum[r] = sum;
+  }
+}
+
 int grid_for(int64_t work, int64_t per_block, const char *what,
              int64_t *grid) {
   *grid = std::max<int64_t>(sw::ceil_div(work, per_block), 1);
@@ -514,6 +547,23 @@ extern "C" int sw_sparse_attention_f32(
                           SW_SDDMM_AFFINE, alpha, beta, o, st);
     if (rc)
       return rc;
+  }
+  if (o.sddmm_lanes_per_row == 64) {
+    // wave row ops: the four softmax ops run as one kernel
+    int64_t grid = std::max<int64_t>(sw::ceil_div(rows, 4), 1);
+    rc = sw::check_grid(grid, "attention softmax");
+    if (rc)
+      return rc;
+    hipLaunchKernelGGL(row_softmax_wave, dim3((unsigned)grid), dim3(256), 0,
+                       st, row_offsets, scores, row_maximum, row_sum,
+                       (int32_t)rows);
+    rc = sw::launch_check("attention softmax kernel");
+    if (rc)
+      return rc;
+    if (dv == 0)
+      return SW_OK;
+    return sw::launch_spmm(row_offsets, column_indices, scores, value, output,
+                           rows, nnz, dv, o, "attention output SpMM", st);
   }
   rc = sw::launch_row_reduce(row_offsets, scores, row_maximum, rows, true, o, st);
   if (rc)
