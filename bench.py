@@ -48,6 +48,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true",
                     help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-rocsparse", action="store_true",
+                    help="skip the rocSPARSE comparison")
     ap.add_argument("--mappings", default="",
                     help="';'-separated SpMV option strings to measure "
                          "instead of the default list")
@@ -137,6 +139,25 @@ def main():
     workloads["spmv_config2"] = {"bytes": spmv_bytes, "flops": spmv_flops,
                                  "best": best, "mappings": spmv_results}
 
+    # rocSPARSE on the same buffers (compute stage only; its analysis /
+    # preprocess stage runs once, outside the timed region)
+    rocsparse = {}
+    if not args.no_rocsparse:
+        try:
+            from sparsewavecomp_amd.rocsparse_runner import RocSparse
+            rs = RocSparse()
+            for alg in ("default", "csr_adaptive", "csr_lrb",
+                        "csr_rowsplit"):
+                log(f"rocSPARSE SpMV {alg}")
+                run = rs.spmv(ro, col, val, xv, y, alg=alg)
+                ms = time_steps(run, K, Wm)
+                rocsparse[f"spmv_{alg}"] = {"ms": ms,
+                                            "GB/s": spmv_bytes / ms / 1e6}
+                log(f"  {ms * 1e3:.1f} us")
+        except Exception as e:  # the comparison is optional
+            rocsparse["error"] = str(e)
+    workloads["rocsparse_config2"] = rocsparse
+
     if not args.only_headline:
         # ---- configuration 1: the reference's CPU-runnable case ------------
         c1, x1 = W.config1(seed=0)
@@ -170,6 +191,18 @@ def main():
                 "GFLOP/s": 2 * nnz * k / ms / 1e6,
                 "hbm_frac": b / ms / 1e6 / HBM_PEAK_GBS}
             log(f"  {ms * 1e3:.1f} us  {b / ms / 1e6:.0f} GB/s")
+            key = f"spmm_k{k}"
+            if not args.no_rocsparse and key not in rocsparse and \
+                    "error" not in rocsparse:
+                try:
+                    for alg in ("default", "csr_merge"):
+                        run = rs.spmm(ro, col, val, rhs, out, alg=alg)
+                        ms2 = time_steps(run, max(K // 2, 1), Wm)
+                        rocsparse.setdefault(key, {})[alg] = {
+                            "ms": ms2, "GB/s": b / ms2 / 1e6}
+                        log(f"  rocSPARSE SpMM {alg}: {ms2 * 1e3:.1f} us")
+                except Exception as e:
+                    rocsparse[key] = {"error": str(e)}
             del rhs, out
         del ro, col, val, xv, y
         torch.cuda.empty_cache()
@@ -269,6 +302,11 @@ def main():
             "rows": n, "nnz": nnz, "mapping": best,
             "GFLOP/s": round(head["GFLOP/s"], 2),
             "hbm_frac": round(head["hbm_frac"], 4),
+            "vs_rocsparse": (round(min(v["ms"] for k2, v in rocsparse.items()
+                                       if k2.startswith("spmv_"))
+                                   / head["ms"], 3)
+                             if any(k2.startswith("spmv_") for k2 in
+                                    rocsparse) else None),
         },
         "roofline": {
             "bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,

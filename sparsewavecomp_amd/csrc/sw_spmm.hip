@@ -154,7 +154,7 @@ __global__ __launch_bounds__(1024) void spmm_thread_position(
 // over the virtual lanes (stride CL) and the one-atomic-per-segment emission
 // follow the SpMV kernel.  Position balance makes rows of any length cost the
 // same, which the row-tile mapping cannot offer for rows thousands long.
-template <int V, int CL, int P>
+template <int V, int CL, int P, bool SR>
 __global__ __launch_bounds__(1024) void spmm_wave_position(
     const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
     const float *__restrict__ val, const float *__restrict__ rhs,
@@ -335,19 +335,40 @@ __global__ __launch_bounds__(1024) void spmm_wave_position(
   int next_lrow = __shfl_down(active ? lrow : -2, CL, kWave);
   if (lane >= kWave - CL)
     next_lrow = -2;
+  // With SR (output rows of whole cache lines) only the chunk's first and
+  // last rows, which can own positions of other chunks, are accumulated
+  // atomically (position_init zeroed them) and the rest are stored;
+  // otherwise every segment is an atomic add into a zeroed output (narrow
+  // rows: scattered partial-line stores from several XCDs measured slower
+  // than atomics).
+  const bool first_shared = !SR || ro[first_row] < wbeg;
+  const bool last_shared = !SR || ro[last_row + 1] > wend;
   if (active && col_ok) {
     if (closed > 0) {
       float *o = out + (int64_t)lrow * k + cb;
       const bool carry = prev_key == lrow;
+      const bool shared = (lrow == first_row && first_shared) ||
+                          (lrow == last_row && last_shared);
 #pragma unroll
-      for (int i = 0; i < V; ++i)
-        unsafeAtomicAdd(o + i, head[i] + (carry ? prev_sc[i] : 0.0f));
+      for (int i = 0; i < V; ++i) {
+        const float h = head[i] + (carry ? prev_sc[i] : 0.0f);
+        if (shared)
+          unsafeAtomicAdd(o + i, h);
+        else
+          o[i] = h;
+      }
     }
     if (next_lrow != row) {
       float *o = out + (int64_t)row * k + cb;
+      const bool shared = (row == first_row && first_shared) ||
+                          (row == last_row && last_shared);
 #pragma unroll
-      for (int i = 0; i < V; ++i)
-        unsafeAtomicAdd(o + i, sc[i]);
+      for (int i = 0; i < V; ++i) {
+        if (shared)
+          unsafeAtomicAdd(o + i, sc[i]);
+        else
+          o[i] = sc[i];
+      }
     }
   }
 }
@@ -356,10 +377,22 @@ template <int V, int CL, int P>
 void launch_wpos(int64_t grid, int64_t B, hipStream_t st, const int32_t *ro,
                  const int32_t *col, const float *val, const float *rhs,
                  float *out, int32_t rows, int32_t nnz, int64_t k,
-                 int64_t units, int64_t chunks, int64_t tiles, bool vec) {
-  hipLaunchKernelGGL((spmm_wave_position<V, CL, P>), dim3((unsigned)grid),
-                     dim3((unsigned)B), 0, st, ro, col, val, rhs, out, rows,
-                     nnz, k, units, chunks, tiles, vec);
+                 int64_t units, int64_t chunks, int64_t tiles, bool vec,
+                 bool store_rows) {
+  // the store-emission variant exists for 128-bit lanes of >= 8-lane tiles
+  // only (k >= 32)
+  if constexpr (V == 4 && CL >= 8) {
+    if (store_rows) {
+      hipLaunchKernelGGL((spmm_wave_position<V, CL, P, true>),
+                         dim3((unsigned)grid), dim3((unsigned)B), 0, st, ro,
+                         col, val, rhs, out, rows, nnz, k, units, chunks,
+                         tiles, vec);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((spmm_wave_position<V, CL, P, false>),
+                     dim3((unsigned)grid), dim3((unsigned)B), 0, st, ro, col,
+                     val, rhs, out, rows, nnz, k, units, chunks, tiles, vec);
 }
 
 template <int V, int CL>
@@ -367,13 +400,13 @@ bool dispatch_wpos_p(int P, int64_t grid, int64_t B, hipStream_t st,
                      const int32_t *ro, const int32_t *col, const float *val,
                      const float *rhs, float *out, int32_t rows, int32_t nnz,
                      int64_t k, int64_t units, int64_t chunks, int64_t tiles,
-                     bool vec) {
+                     bool vec, bool sr) {
   switch (P) {
-  case 1: launch_wpos<V, CL, 1>(grid, B, st, ro, col, val, rhs, out, rows, nnz, k, units, chunks, tiles, vec); return true;
-  case 2: launch_wpos<V, CL, 2>(grid, B, st, ro, col, val, rhs, out, rows, nnz, k, units, chunks, tiles, vec); return true;
-  case 4: launch_wpos<V, CL, 4>(grid, B, st, ro, col, val, rhs, out, rows, nnz, k, units, chunks, tiles, vec); return true;
-  case 8: launch_wpos<V, CL, 8>(grid, B, st, ro, col, val, rhs, out, rows, nnz, k, units, chunks, tiles, vec); return true;
-  case 16: launch_wpos<V, CL, 16>(grid, B, st, ro, col, val, rhs, out, rows, nnz, k, units, chunks, tiles, vec); return true;
+  case 1: launch_wpos<V, CL, 1>(grid, B, st, ro, col, val, rhs, out, rows, nnz, k, units, chunks, tiles, vec, sr); return true;
+  case 2: launch_wpos<V, CL, 2>(grid, B, st, ro, col, val, rhs, out, rows, nnz, k, units, chunks, tiles, vec, sr); return true;
+  case 4: launch_wpos<V, CL, 4>(grid, B, st, ro, col, val, rhs, out, rows, nnz, k, units, chunks, tiles, vec, sr); return true;
+  case 8: launch_wpos<V, CL, 8>(grid, B, st, ro, col, val, rhs, out, rows, nnz, k, units, chunks, tiles, vec, sr); return true;
+  case 16: launch_wpos<V, CL, 16>(grid, B, st, ro, col, val, rhs, out, rows, nnz, k, units, chunks, tiles, vec, sr); return true;
   }
   return false;
 }
@@ -485,6 +518,95 @@ __global__ __launch_bounds__(256) void spmm_tile_mfma(
   }
 }
 
+
+// Row-owner SpMM for wide rhs (Wave64 extension, k % 4 == 0).
+//
+// The nonzeros are cut into chunks of `chunk` positions; wave w owns the
+// rows whose first position falls in its chunk (rows starting past the last
+// chunk, i.e. trailing empty rows, belong to the last one), so every output
+// row has exactly one writer: plain 128-bit stores, no zero fill, no
+// atomics, and the row assignment is balanced by nonzeros, not by rows.  The
+// wave computes one row at a time: its 64 lanes form PL = 64/CL groups of CL
+// lanes, each lane holding 4 output columns of the CL*4-column tile; the
+// groups take positions s+g, s+g+PL, ... U at a time (U = 16 for rows longer
+// than 512 positions, 4 otherwise), and the groups' partial rows meet in an
+// xor butterfly.
+template <int CL>
+__global__ __launch_bounds__(256) void spmm_row_owner(
+    const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
+    const float *__restrict__ val, const float *__restrict__ rhs,
+    float *__restrict__ out, int32_t rows, int32_t nnz, int64_t k,
+    int64_t chunk, int64_t chunks, int64_t tiles) {
+  constexpr int PL = kWave / CL;
+  const int64_t wave =
+      (int64_t)blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+  if (wave >= chunks * tiles)
+    return;
+  const int64_t c = wave / tiles;
+  const int64_t t = wave - c * tiles;
+  const int lane = lane_id();
+  const int vl = lane / CL, cl = lane % CL;
+  const int64_t cb = t * (CL * 4) + (int64_t)cl * 4;
+  const bool col_ok = cb < k;
+  // owned rows: first r with ro[r] >= c*chunk .. (last chunk: to rows)
+  const int r0 = 1 + row_search_uniform(ro, 0u, (uint32_t)rows + 1u,
+                                         (int32_t)(c * chunk) - 1);
+  const int r1 = c == chunks - 1
+                     ? rows
+                     : 1 + row_search_uniform(ro, (uint32_t)r0,
+                                              (uint32_t)rows + 1u,
+                                              (int32_t)((c + 1) * chunk) - 1);
+  for (int r = r0; r < r1 && r < rows; ++r) {
+    const int32_t s = ro[r], e = ro[r + 1];
+    v4f acc = {0.f, 0.f, 0.f, 0.f};
+    if (col_ok) {
+      if (e - s > 512) {
+        constexpr int U = 16;
+        for (int32_t p = s + vl; p < e; p += PL * U) {
+          v4f b[U];
+          float v[U];
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            const int32_t q = p + u * PL;
+            v[u] = q < e ? ld_stream(val + q) : 0.0f;
+            const int64_t cc = q < e ? ld_stream(col + q) : 0;
+            b[u] = *reinterpret_cast<const v4f *>(rhs + cc * k + cb);
+          }
+#pragma unroll
+          for (int u = 0; u < U; ++u)
+            acc += v[u] * b[u];
+        }
+      } else {
+        constexpr int U = 4;
+        for (int32_t p = s + vl; p < e; p += PL * U) {
+          v4f b[U];
+          float v[U];
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            const int32_t q = p + u * PL;
+            v[u] = q < e ? ld_stream(val + q) : 0.0f;
+            const int64_t cc = q < e ? ld_stream(col + q) : 0;
+            b[u] = *reinterpret_cast<const v4f *>(rhs + cc * k + cb);
+          }
+#pragma unroll
+          for (int u = 0; u < U; ++u)
+            acc += v[u] * b[u];
+        }
+      }
+    }
+#pragma unroll
+    for (int off = CL; off < kWave; off <<= 1) {
+      acc.x += __shfl_xor(acc.x, off, kWave);
+      acc.y += __shfl_xor(acc.y, off, kWave);
+      acc.z += __shfl_xor(acc.z, off, kWave);
+      acc.w += __shfl_xor(acc.w, off, kWave);
+    }
+    if (vl == 0 && col_ok)
+      __builtin_nontemporal_store(acc, reinterpret_cast<v4f *>(
+                                           out + (int64_t)r * k + cb));
+  }
+}
+
 template <int V, int CL, int G>
 void launch_tile(int64_t grid, int64_t B, hipStream_t st, const int32_t *ro,
                  const int32_t *col, const float *val, const float *rhs,
@@ -535,6 +657,9 @@ int next_pow2(int v) {
 namespace sw {
 
 int launch_fill_zero(float *y, int64_t n, int64_t block, hipStream_t st);
+int launch_position_init(const int32_t *ro, float *out, int64_t rows,
+                         int64_t k, int64_t chunk, int64_t P, int64_t units,
+                         int64_t waves, hipStream_t st);
 
 int launch_spmm(const int32_t *ro, const int32_t *col, const float *val,
                 const float *rhs, float *out, int64_t rows, int64_t nnz,
@@ -587,14 +712,33 @@ int launch_spmm(const int32_t *ro, const int32_t *col, const float *val,
                        ro, col, val, rhs, out, (int32_t)rows, k);
     return launch_check("SpMM tile MFMA kernel");
   }
-  // row-tile-mfma with k not a multiple of 16 takes the position schedule
-  if (streq(o.spmm_mapping, "wave-per-position") ||
-      streq(o.spmm_mapping, "row-tile-mfma")) {
-    int rc = launch_fill_zero(out, rows * k, B, st);
+  if (streq(o.spmm_mapping, "wave-per-row-balanced") && k % 4 == 0 &&
+      aligned16(rhs) && aligned16(out)) {
+    const int CL = std::min(16, next_pow2((int)std::min<int64_t>(k / 4, 16)));
+    const int64_t chunk = 64 * o.spmm_positions_per_lane;
+    const int64_t chunks = std::max<int64_t>(ceil_div(nnz, chunk), 1);
+    const int64_t tiles = ceil_div(k, (int64_t)CL * 4);
+    const int64_t grid = ceil_div(chunks * tiles, B / 64);
+    int rc = check_grid(grid, what);
     if (rc)
       return rc;
-    if (nnz == 0)
-      return SW_OK;
+#define SW_OWNER(CC)                                                          \
+  case CC:                                                                    \
+    hipLaunchKernelGGL(spmm_row_owner<CC>, dim3((unsigned)grid),              \
+                       dim3((unsigned)B), 0, st, ro, col, val, rhs, out,      \
+                       (int32_t)rows, (int32_t)nnz, k, chunk, chunks, tiles); \
+    break;
+    switch (CL) {
+      SW_OWNER(1) SW_OWNER(2) SW_OWNER(4) SW_OWNER(8) SW_OWNER(16)
+    }
+#undef SW_OWNER
+    return launch_check("row-owner SpMM kernel");
+  }
+  // row-tile-mfma with k not a multiple of 16 and wave-per-row-balanced
+  // without 128-bit rows take the position schedule
+  if (streq(o.spmm_mapping, "wave-per-position") ||
+      streq(o.spmm_mapping, "row-tile-mfma") ||
+      streq(o.spmm_mapping, "wave-per-row-balanced")) {
     const bool v4 = (k % 4 == 0) && aligned16(rhs) && aligned16(out);
     const int V = v4 ? 4 : 1;
     const int CL = std::min(16, next_pow2((int)std::min<int64_t>(
@@ -605,16 +749,30 @@ int launch_spmm(const int32_t *ro, const int32_t *col, const float *val,
     const int64_t chunks = ceil_div(units, PL);
     const int64_t tiles = ceil_div(k, (int64_t)CL * V);
     const int64_t grid = ceil_div(chunks * tiles, B / 64);
-    rc = check_grid(grid, what);
+    int rc = check_grid(grid, what);
     if (rc)
       return rc;
+    // rows of at least one 128-byte line are stored; narrower rows go
+    // through atomics into a fully zeroed output
+    const bool store_rows = V == 4 && CL >= 8 && k >= 32;
+    if (store_rows)
+      // chunks of PL*P positions: zero the rows that span chunks, and the
+      // empty rows
+      rc = launch_position_init(ro, out, rows, k, PL * P, P, units,
+                                std::max<int64_t>(chunks, 1), st);
+    else
+      rc = launch_fill_zero(out, rows * k, B, st);
+    if (rc)
+      return rc;
+    if (nnz == 0)
+      return SW_OK;
     const bool vec = aligned16(col) && aligned16(val);
     bool ok = false;
 #define SW_WPOS(VV, CC)                                                       \
   if (V == VV && CL == CC)                                                    \
     ok = dispatch_wpos_p<VV, CC>(P, grid, B, st, ro, col, val, rhs, out,      \
                                  (int32_t)rows, (int32_t)nnz, k, units,       \
-                                 chunks, tiles, vec);
+                                 chunks, tiles, vec, store_rows);
     SW_WPOS(4, 1) SW_WPOS(4, 2) SW_WPOS(4, 4) SW_WPOS(4, 8) SW_WPOS(4, 16)
     SW_WPOS(1, 1) SW_WPOS(1, 2) SW_WPOS(1, 4) SW_WPOS(1, 8) SW_WPOS(1, 16)
 #undef SW_WPOS

@@ -114,6 +114,47 @@ __global__ __launch_bounds__(1024) void fill_zero_f32(float *__restrict__ y,
   }
 }
 
+
+// ---------------------------------------------------------------------------
+// Output initialisation of the wide-row SpMM position schedule.  There a row
+// is accumulated atomically only when its positions belong to more than one
+// wave; every other row receives exactly one plain store from the wave that
+// holds it.  So only those rows, and empty rows (which no position reaches),
+// need the zero the reference's init kernel writes
+// (SparsePositionScheduling.cpp:31-47): one thread per row decides.
+// Waves either own aligned chunks of `chunk` positions (chunk > 0) or the
+// balanced partition of `units` units of P positions over `waves` waves.
+__device__ __forceinline__ int64_t wave_of_position(int64_t p, int64_t chunk,
+                                                    int64_t P, int64_t units,
+                                                    int64_t waves) {
+  if (chunk > 0)
+    return p / chunk;
+  const int64_t u = p / P;
+  const int64_t base = units / waves, rem = units % waves;
+  const int64_t big = (base + 1) * rem;
+  return u < big ? u / (base + 1) : rem + (u - big) / base;
+}
+
+__global__ __launch_bounds__(256) void position_init(
+    const int32_t *__restrict__ ro, float *__restrict__ out, int32_t rows,
+    int64_t k, int64_t chunk, int64_t P, int64_t units, int64_t waves) {
+  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows)
+    return;
+  const int32_t s = ro[r], e = ro[r + 1];
+  if (s < e && wave_of_position(s, chunk, P, units, waves) ==
+                   wave_of_position(e - 1, chunk, P, units, waves))
+    return;
+  float *o = out + r * k;
+  if (k % 4 == 0 && (reinterpret_cast<uintptr_t>(o) & 15u) == 0) {
+    for (int64_t c = 0; c < k; c += 4)
+      *reinterpret_cast<v4f *>(o + c) = v4f{0.f, 0.f, 0.f, 0.f};
+  } else {
+    for (int64_t c = 0; c < k; ++c)
+      o[c] = 0.0f;
+  }
+}
+
 // ---------------------------------------------------------------------------
 // thread-per-position, atomic: worker w handles positions
 // [w*chunk, min((w+1)*chunk, nnz)), recovers each position's row by the row
@@ -314,6 +355,10 @@ __global__ __launch_bounds__(1024) void spmv_wave_position(
   const int prev_key = shfl_up1_i(key, INT32_MIN);
   const float prev_scanned = shfl_up1_f(scanned, 0.0f);
   const int next_lrow = shfl_down1_i(active ? lrow : -2, -2);
+  // Segment emissions are fire-and-forget atomic adds into the zeroed
+  // output.  (Plain 4-byte stores of the rows owned by one wave measured
+  // twice as slow: neighbouring rows of a cache line are written from waves
+  // on different XCDs.)
   if (active) {
     if (closed > 0) {
       float h = head + (prev_key == lrow ? prev_scanned : 0.0f);
@@ -369,6 +414,21 @@ int launch_fill_zero(float *y, int64_t n, int64_t block, hipStream_t st) {
   return launch_check("output initialisation kernel");
 }
 
+int launch_position_init(const int32_t *ro, float *out, int64_t rows,
+                         int64_t k, int64_t chunk, int64_t P, int64_t units,
+                         int64_t waves, hipStream_t st) {
+  if (rows <= 0 || k <= 0)
+    return SW_OK;
+  int64_t grid = ceil_div(rows, 256);
+  int rc = check_grid(grid, "output initialisation");
+  if (rc)
+    return rc;
+  hipLaunchKernelGGL(position_init, dim3((unsigned)grid), dim3(256), 0, st,
+                     ro, out, (int32_t)rows, k, chunk, P,
+                     std::max<int64_t>(units, 1), std::max<int64_t>(waves, 1));
+  return launch_check("position output initialisation kernel");
+}
+
 int launch_spmv(const int32_t *ro, const int32_t *col, const float *val,
                 const float *x, float *y, int64_t rows, int64_t nnz,
                 const sw_options &o, hipStream_t st) {
@@ -407,11 +467,12 @@ int launch_spmv(const int32_t *ro, const int32_t *col, const float *val,
                        dim3((unsigned)B), 0, st, ro, col, val, x, y, n);
     return launch_check("block-per-row SpMV kernel");
   }
-  // position mappings: zero the output, then accumulate
-  int rc = launch_fill_zero(y, rows, o.spmv_block_size, st);
-  if (rc)
-    return rc;
+  int rc;
   if (streq(o.spmv_mapping, "thread-per-position")) {
+    // every contribution is atomic: zero the whole output first
+    rc = launch_fill_zero(y, rows, o.spmv_block_size, st);
+    if (rc)
+      return rc;
     if (nnz == 0)
       return SW_OK;
     const int64_t chunk = o.spmv_position_chunk_size;
@@ -431,8 +492,6 @@ int launch_spmv(const int32_t *ro, const int32_t *col, const float *val,
     return launch_check("thread-per-position SpMV kernel");
   }
   // wave-per-position
-  if (nnz == 0)
-    return SW_OK;
   const int64_t P = o.spmv_positions_per_lane;
   const int64_t units = ceil_div(nnz, P);
   const int64_t grid = std::max<int64_t>(ceil_div(units, B), 1);
@@ -440,6 +499,11 @@ int launch_spmv(const int32_t *ro, const int32_t *col, const float *val,
   if (rc)
     return rc;
   const int64_t waves = grid * (B / 64);
+  rc = launch_fill_zero(y, rows, o.spmv_block_size, st);
+  if (rc)
+    return rc;
+  if (nnz == 0)
+    return SW_OK;
   const bool vec = aligned16(col) && aligned16(val);
   dim3 g((unsigned)grid), b((unsigned)B);
   const int32_t z = (int32_t)nnz;

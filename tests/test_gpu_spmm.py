@@ -34,6 +34,9 @@ MAPPINGS = [
     "spmm-mapping=wave-per-position spmm-positions-per-lane=16 "
     "spmm-block-size=128",
     "spmm-mapping=row-tile-mfma",
+    "spmm-mapping=wave-per-row-balanced",
+    "spmm-mapping=wave-per-row-balanced spmm-positions-per-lane=1 "
+    "spmm-block-size=64",
 ]
 
 
@@ -112,6 +115,9 @@ def config3():
         "spmm-block-size=64"),
     (64, "spmm-mapping=wave-per-position spmm-positions-per-lane=8 "
          "spmm-block-size=64"),
+    (64, "spmm-mapping=wave-per-row-balanced spmm-positions-per-lane=4 "
+         "spmm-block-size=64"),
+    (4, "spmm-mapping=wave-per-row-balanced spmm-positions-per-lane=4"),
 ])
 def test_config3_full_size(dev, orc, config3, k, opts):
     csr = config3
