@@ -127,6 +127,22 @@ int sw_spmv_csr_f32(const int32_t *row_offsets, const int32_t *column_indices,
                     const sw_options *opts, void *stream);
 
 /*
+ * sparsewave.coo_spmv: output[rows] = A * vector with A in COO form.
+ * Operands in op order (SparseWaveOps.td:54-88): row_indices[nnz],
+ * column_indices[nnz], values[nnz], vector[cols], output[rows]; entries in
+ * any order, repeated coordinates add up.  The output is zeroed, then
+ * accumulated.  Replaces ThreadPerNonzeroCOOSpMVPattern
+ * (SparseWaveToGPU.cpp:154-214), which reads only spmv-block-size; with
+ * spmv-mapping=wave-per-position a run-segmented kernel (one atomic per run
+ * of equal adjacent rows, spmv-positions-per-lane entries per lane) is used
+ * instead.
+ */
+int sw_spmv_coo_f32(const int32_t *row_indices, const int32_t *column_indices,
+                    const float *values, const float *vector, float *output,
+                    int64_t rows, int64_t cols, int64_t nnz,
+                    const sw_options *opts, void *stream);
+
+/*
  * sparsewave.spmm: output[rows][k] = A * rhs[cols][k], dense matrices
  * row-major.  Operand order and the 5-buffer bundle ABI of
  * SparseWaveOps.td:91-124 / tools/sparsewave-bundle/sparsewave_bundle_ir.py:11-17.
@@ -236,6 +252,89 @@ int sw_sparse_attention_f32(const int32_t *row_offsets,
 int sw_csr_row_at_position(const int32_t *row_offsets, int64_t rows,
                            const int64_t *positions, int32_t *out_rows,
                            int64_t count, void *stream);
+
+/* ---- Host-side matrix files -------------------------------------------- */
+/* These run on the host only and make no HIP call: every pointer below is
+ * host memory, and the readers allocate their results with malloc.  They
+ * load the reference harness's workloads (SuiteSparse Matrix Market files
+ * and the SWCSR001 / SWCOO001 / SWBSR001 binaries it converts them to). */
+
+/*
+ * A sparse matrix in host memory, as the benchmark harness holds it
+ * (benchmark/benchmark_utils.py:56-177 returns the same fields).  The
+ * arrays are malloc'ed by the library when it returns one (free with
+ * sw_host_matrix_free); a caller building one for a writer owns them.
+ * row_indices / column_indices / values are the COO entries (nnz each);
+ * row_offsets (rows + 1) is set, and has_row_offsets = 1, when the entries
+ * are grouped by row in row order (always after a Matrix Market or CSR read,
+ * for a COO read only when the file stores them that way).  Values are kept
+ * in double until written, as the reference writer holds Python floats.
+ */
+typedef struct sw_host_matrix {
+  int64_t rows, columns, nnz;
+  int32_t *row_offsets;
+  int32_t *row_indices;
+  int32_t *column_indices;
+  double *values;
+  int32_t has_row_offsets;
+  char field[16];    /* "real" | "integer" | "pattern" ("" for binaries) */
+  char symmetry[16]; /* "general" | "symmetric" ("" for binaries) */
+  int64_t min_row_nnz, max_row_nnz;
+  double mean_row_nnz;
+} sw_host_matrix;
+
+/*
+ * A padded BSR matrix with the COO entries it was built from
+ * (convert_to_bsr, benchmark/benchmark_utils.py:240-312): rows / columns
+ * padded up to multiples of block_size, blocks row-major [nnzb][b][b],
+ * repeated coordinates added up.
+ */
+typedef struct sw_host_bsr {
+  int64_t rows, columns, nnzb, block_size;
+  int64_t original_rows, original_columns, nnz;
+  int32_t *block_row_offsets;    /* rows / block_size + 1 */
+  int32_t *block_column_indices; /* nnzb */
+  double *block_values;          /* nnzb * block_size^2 */
+  int32_t *input_row_indices;    /* nnz */
+  int32_t *input_column_indices; /* nnz */
+  double *input_values;          /* nnz */
+  double block_density, internal_zero_fraction, storage_overhead;
+} sw_host_bsr;
+
+void sw_host_matrix_free(sw_host_matrix *m);
+void sw_host_bsr_free(sw_host_bsr *b);
+
+/* Matrix Market coordinate reader (benchmark/benchmark_utils.py:56-177):
+ * real / integer / pattern, general / symmetric (off-diagonal entries
+ * mirrored), 1-based indices, finite values that fit f32, entry count as
+ * declared; entries sorted by (row, column), repeated coordinates kept in
+ * file order.  Errors name the file and line. */
+int sw_matrix_market_read(const char *path, sw_host_matrix **out);
+
+/* SWCSR001 / SWCOO001 writers (benchmark/benchmark_utils.py:180-237): the
+ * 8-byte magic, rows, columns, nnz as little-endian u64, then i32 / f32
+ * arrays (CSR: row offsets, column indices, values; COO: row indices,
+ * column indices, values). */
+int sw_csr_binary_write(const char *path, const sw_host_matrix *m);
+int sw_coo_binary_write(const char *path, const sw_host_matrix *m);
+
+/* Readers of the same files (benchmark/SparseBenchmarkUtils.cpp:83-141),
+ * which also check the index structure (offsets 0..nnz, non-decreasing,
+ * indices in range) so the result can go to the GPU as is. */
+int sw_csr_binary_read(const char *path, sw_host_matrix **out);
+int sw_coo_binary_read(const char *path, sw_host_matrix **out);
+
+/* COO -> padded BSR (benchmark/benchmark_utils.py:240-312). */
+int sw_convert_to_bsr(const sw_host_matrix *m, int64_t block_size,
+                      sw_host_bsr **out);
+
+/* SWBSR001 writer / reader (benchmark/benchmark_utils.py:315-379,
+ * benchmark/SparseBenchmarkUtils.cpp:143-185): magic, rows, columns, nnzb,
+ * block size, original rows, original columns, original nnz (u64), then
+ * block-row offsets, block-column indices, block values, and the original
+ * COO row indices, column indices and values. */
+int sw_bsr_binary_write(const char *path, const sw_host_bsr *m);
+int sw_bsr_binary_read(const char *path, sw_host_bsr **out);
 
 #ifdef __cplusplus
 }

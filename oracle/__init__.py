@@ -49,6 +49,7 @@ def _declare(l):
     l.oracle_spmv_csr_f32_mt.argtypes = [_I64, _P, _P, _P, _P, _P]
     l.oracle_num_threads.restype = ctypes.c_int
     l.oracle_spmv_abs_bound.argtypes = [_I64, _P, _P, _P, _P, _P]
+    l.oracle_spmv_coo_f32.argtypes = [_I64, _I64, _P, _P, _P, _P, _P, _P]
     l.oracle_spmm_csr_f32.argtypes = [_I64, _I64, _P, _P, _P, _P, _P]
     l.oracle_spmm_abs_bound.argtypes = [_I64, _I64, _P, _P, _P, _P, _P]
     l.oracle_bsr_spmm_f32.argtypes = [_I64, _I64, _I64, _P, _P, _P, _P, _P]
@@ -105,6 +106,18 @@ def spmv_abs_bound(ro, col, val, x):
     lib().oracle_spmv_abs_bound(rows, _ptr(ro), _ptr(col), _ptr(val), _ptr(x),
                                 _ptr(b))
     return b
+
+
+def spmv_coo(rows, ri, ci, val, x):
+    """COO SpMV in storage order; returns (y, per-row bound sum |val*x|).
+    SparseWaveToGPU.cpp:154-214 / SparseBenchmarkUtils.cpp:231-251."""
+    ri, ci, val, x = (_c(ri, np.int32), _c(ci, np.int32),
+                      _c(val, np.float32), _c(x, np.float32))
+    y = np.empty(rows, np.float32)
+    b = np.empty(rows, np.float64)
+    lib().oracle_spmv_coo_f32(rows, ri.size, _ptr(ri), _ptr(ci), _ptr(val),
+                              _ptr(x), _ptr(y), _ptr(b))
+    return y, b
 
 
 def spmm(ro, col, val, rhs):

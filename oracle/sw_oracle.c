@@ -60,6 +60,29 @@ void oracle_spmv_abs_bound(int64_t rows, const int32_t *ro, const int32_t *col,
   }
 }
 
+/* COO SpMV: output zeroed, then each stored entry adds its product to its
+ * row in storage order (duplicates and any entry order allowed).  Body of
+ * ThreadPerNonzeroCOOSpMVPattern (SparseWaveToGPU.cpp:154-214: zero-fill,
+ * then `atomic addf (val[p] * x[col[p]])` per entry) run sequentially; the
+ * loop order of the expected output in benchmark/SparseBenchmarkUtils.cpp:
+ * 231-251.  Also writes the per-row magnitude bound sum |val * x| (double)
+ * when `bound` is not NULL. */
+void oracle_spmv_coo_f32(int64_t rows, int64_t nnz, const int32_t *ri,
+                         const int32_t *ci, const float *val, const float *x,
+                         float *y, double *bound) {
+  for (int64_t r = 0; r < rows; ++r) {
+    y[r] = 0.0f;
+    if (bound)
+      bound[r] = 0.0;
+  }
+  for (int64_t p = 0; p < nnz; ++p) {
+    const float product = val[p] * x[ci[p]];
+    y[ri[p]] += product;
+    if (bound)
+      bound[ri[p]] += fabs((double)product);
+  }
+}
+
 /* CSR SpMM, row-major rhs[m][k] and out[n][k].
  * Loop order of benchmark/SparseBenchmarkUtils.cpp:277-288 (row, output
  * column, position), which is also the per-thread body of

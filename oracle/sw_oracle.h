@@ -26,6 +26,9 @@ void oracle_spmv_csr_f32_mt(int64_t rows, const int32_t *ro,
 int oracle_num_threads(void);
 void oracle_spmv_abs_bound(int64_t rows, const int32_t *ro, const int32_t *col,
                            const float *val, const float *x, double *bound);
+void oracle_spmv_coo_f32(int64_t rows, int64_t nnz, const int32_t *ri,
+                         const int32_t *ci, const float *val, const float *x,
+                         float *y, double *bound);
 void oracle_spmm_csr_f32(int64_t rows, int64_t k, const int32_t *ro,
                          const int32_t *col, const float *val,
                          const float *rhs, float *out);

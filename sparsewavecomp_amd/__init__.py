@@ -17,6 +17,7 @@ import os
 
 __all__ = [
     "Options", "SparseWaveError", "library_path", "load_library", "spmv",
+    "coo_spmv",
     "spmm", "bsr_spmm", "sddmm", "csr_row_reduce", "csr_rowwise_map",
     "sparse_attention", "csr_row_at_position", "SDDMM_MUL", "SDDMM_AFFINE",
     "SDDMM_DOT", "MAP_EXP_SUB", "MAP_DIV", "MAP_SUB", "MAP_MUL",
@@ -32,9 +33,14 @@ MAP_EXP_SUB, MAP_DIV, MAP_SUB, MAP_MUL = 0, 1, 2, 3
 EXPORTED_SYMBOLS = (
     "sw_options_init", "sw_options_set", "sw_options_parse",
     "sw_validate_options", "sw_last_error", "sw_version", "sw_spmv_csr_f32",
+    "sw_spmv_coo_f32",
     "sw_spmm_csr_f32", "sw_bsr_spmm_f32", "sw_bsr_spmm_bf16",
     "sw_sddmm_csr_f32", "sw_csr_row_reduce_f32", "sw_csr_rowwise_map_f32",
     "sw_sparse_attention_f32", "sw_csr_row_at_position",
+    "sw_host_matrix_free", "sw_host_bsr_free", "sw_matrix_market_read",
+    "sw_csr_binary_write", "sw_coo_binary_write", "sw_csr_binary_read",
+    "sw_coo_binary_read", "sw_convert_to_bsr", "sw_bsr_binary_write",
+    "sw_bsr_binary_read",
 )
 
 
@@ -102,6 +108,8 @@ def load_library():
         "sw_last_error": (C, []),
         "sw_version": (C, []),
         "sw_spmv_csr_f32": (ctypes.c_int, [P, P, P, P, P, I64, I64, I64, OP,
+                                           P]),
+        "sw_spmv_coo_f32": (ctypes.c_int, [P, P, P, P, P, I64, I64, I64, OP,
                                            P]),
         "sw_spmm_csr_f32": (ctypes.c_int, [P, P, P, P, P, I64, I64, I64, I64,
                                            OP, P]),
@@ -220,6 +228,24 @@ def spmv(row_offsets, column_indices, values, vector, output, options=None,
         _dev(values, torch.float32, "values"),
         _dev(vector, torch.float32, "vector"),
         _dev(output, torch.float32, "output"), rows, vector.numel(),
+        values.numel(), _opts(options), _stream(stream)))
+    return output
+
+
+def coo_spmv(row_indices, column_indices, values, vector, output,
+             options=None, stream=None):
+    """sparsewave.coo_spmv (SparseWaveOps.td:54-88): output = A @ vector with
+    A as COO entries (any order, repeated coordinates add up)."""
+    import torch
+    if not (row_indices.numel() == column_indices.numel() == values.numel()):
+        raise SparseWaveError(-2, "COO row indices, column indices and values "
+                                  "must have the same length")
+    _check(load_library().sw_spmv_coo_f32(
+        _dev(row_indices, torch.int32, "row_indices"),
+        _dev(column_indices, torch.int32, "column_indices"),
+        _dev(values, torch.float32, "values"),
+        _dev(vector, torch.float32, "vector"),
+        _dev(output, torch.float32, "output"), output.numel(), vector.numel(),
         values.numel(), _opts(options), _stream(stream)))
     return output
 

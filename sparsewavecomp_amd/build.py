@@ -20,6 +20,7 @@ ARCH = "gfx950"
 
 SOURCES = [
     "sw_options.cpp",
+    "sw_io.cpp",
     "sw_spmv.hip",
     "sw_spmm.hip",
     "sw_bsr.hip",

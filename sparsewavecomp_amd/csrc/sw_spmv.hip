@@ -1,6 +1,6 @@
 // sparsewave.spmv on gfx950: the row mappings (thread, wave, block per row)
 // and the position mappings (thread and wave per position), with their
-// launchers behind sw_spmv_csr_f32.
+// launchers behind sw_spmv_csr_f32; COO SpMV behind sw_spmv_coo_f32.
 //
 // Reference kernels (generated IR, not hand-written code):
 //   thread-per-row     SparseWaveToGPU.cpp:216-274
@@ -9,6 +9,7 @@
 //   thread-per-position SparsePositionScheduling.cpp:135-316
 //   wave-per-position  SparsePositionScheduling.cpp:318-403,
 //                      SparsePositionToSCF.cpp:190-271, SparseGPUUtils.cpp:247-292
+//   COO thread-per-nonzero SparseWaveToGPU.cpp:154-214
 #include "sw_device.h"
 #include "sw_internal.h"
 
@@ -380,6 +381,123 @@ __global__ __launch_bounds__(256) void csr_row_at_position_kernel(
     out[i] = row_search_lane(ro, 1u, (uint32_t)rows + 1u, (int32_t)pos[i]);
 }
 
+// ---------------------------------------------------------------------------
+// sparsewave.coo_spmv (SparseWaveOps.td:54-88): parallel row-index,
+// column-index and value arrays, entries in any order, coordinates may
+// repeat; the output is zeroed first, then accumulated.
+//
+// thread-per-nonzero: the reference's COO lowering
+// (ThreadPerNonzeroCOOSpMVPattern, SparseWaveToGPU.cpp:154-214), one thread
+// and one atomic add of val*x[col] per stored entry.
+__global__ __launch_bounds__(1024) void coo_thread_per_nonzero(
+    const int32_t *__restrict__ ri, const int32_t *__restrict__ col,
+    const float *__restrict__ val, const float *__restrict__ x,
+    float *__restrict__ y, int64_t nnz) {
+  const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (p < nnz)
+    unsafeAtomicAdd(y + ld_stream(ri + p),
+                    ld_stream(val + p) * x[ld_stream(col + p)]);
+}
+
+// Run-segmented COO (Wave64 extension, taken under the position mapping):
+// grid lane u takes entries [u*P, u*P+P).  Runs of equal adjacent row
+// indices are summed in registers; a run that closes inside the lane is added
+// atomically; the lane's last run is carried across lanes by a segmented scan
+// keyed on run numbers (a ballot prefix count of run starts, which is
+// monotone even when row indices are not), so a row-sorted matrix costs about
+// one atomic per row per wave instead of one per entry.  Unsorted input stays
+// correct: a row split over several runs gets one atomic per run.
+template <int P, bool VEC>
+__global__ __launch_bounds__(1024) void coo_run_segmented(
+    const int32_t *__restrict__ ri, const int32_t *__restrict__ col,
+    const float *__restrict__ val, const float *__restrict__ x,
+    float *__restrict__ y, int64_t nnz) {
+  const int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t p0 = u * P;
+  const bool active = p0 < nnz;
+  const int n = active ? (int)(nnz - p0 < P ? nnz - p0 : P) : 0;
+  int32_t rr[P];
+  float prod[P];
+#pragma unroll
+  for (int q = 0; q < P; ++q) {
+    rr[q] = 0;
+    prod[q] = 0.0f;
+  }
+  bool full = false;
+  if constexpr (VEC && P >= 4) {
+    full = n == P;
+    if (full) {
+#pragma unroll
+      for (int q = 0; q < P; q += 4) {
+        v4i r = ld_stream(reinterpret_cast<const v4i *>(ri + p0 + q));
+        v4i c = ld_stream(reinterpret_cast<const v4i *>(col + p0 + q));
+        v4f v = ld_stream(reinterpret_cast<const v4f *>(val + p0 + q));
+        rr[q + 0] = r.x;
+        rr[q + 1] = r.y;
+        rr[q + 2] = r.z;
+        rr[q + 3] = r.w;
+        prod[q + 0] = v.x * x[c.x];
+        prod[q + 1] = v.y * x[c.y];
+        prod[q + 2] = v.z * x[c.z];
+        prod[q + 3] = v.w * x[c.w];
+      }
+    }
+  }
+  if (!full) {
+#pragma unroll
+    for (int q = 0; q < P; ++q)
+      if (q < n) {
+        rr[q] = ld_stream(ri + p0 + q);
+        prod[q] = ld_stream(val + p0 + q) * x[ld_stream(col + p0 + q)];
+      }
+  }
+  int hk = -1, tk = -1, closed = 0;
+  float head = 0.0f, acc = 0.0f;
+  if (active) {
+    hk = tk = rr[0];
+#pragma unroll
+    for (int q = 0; q < P; ++q)
+      if (q < n) {
+        if (rr[q] != tk) {
+          if (closed == 0)
+            head = acc;
+          else
+            unsafeAtomicAdd(y + tk, acc);
+          ++closed;
+          acc = 0.0f;
+          tk = rr[q];
+        }
+        acc += prod[q];
+      }
+  }
+  // A lane's last run continues the previous lane's last run exactly when
+  // the lane holds a single run of the same row.
+  const int prev_tk = shfl_up1_i(active ? tk : -1, -1);
+  const bool starts = !(active && closed == 0 && tk == prev_tk);
+  const uint64_t m = ballot(starts);
+  const int run = (int)__builtin_amdgcn_mbcnt_hi(
+                      (uint32_t)(m >> 32),
+                      __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u)) +
+                  (starts ? 1 : 0);
+  const float scanned = wave_segmented_scan(run, active ? acc : 0.0f);
+  const float prev_scanned = shfl_up1_f(scanned, 0.0f);
+  const int next_hk = shfl_down1_i(active ? hk : -2, -2);
+  if (active) {
+    if (closed > 0)
+      unsafeAtomicAdd(y + hk, head + (prev_tk == hk ? prev_scanned : 0.0f));
+    if (next_hk != tk)
+      unsafeAtomicAdd(y + tk, scanned);
+  }
+}
+
+template <int P, bool VEC>
+void launch_coo_runs(int64_t grid, int64_t B, hipStream_t st,
+                     const int32_t *ri, const int32_t *col, const float *val,
+                     const float *x, float *y, int64_t nnz) {
+  hipLaunchKernelGGL((coo_run_segmented<P, VEC>), dim3((unsigned)grid),
+                     dim3((unsigned)B), 0, st, ri, col, val, x, y, nnz);
+}
+
 template <int G>
 void launch_group(dim3 grid, dim3 block, hipStream_t st, const int32_t *ro,
                   const int32_t *col, const float *val, const float *x,
@@ -526,6 +644,47 @@ int launch_spmv(const int32_t *ro, const int32_t *col, const float *val,
   return launch_check("wave-per-position SpMV kernel");
 }
 
+int launch_spmv_coo(const int32_t *ri, const int32_t *col, const float *val,
+                    const float *x, float *y, int64_t rows, int64_t nnz,
+                    const sw_options &o, hipStream_t st) {
+  const int64_t B = o.spmv_block_size;
+  int rc = launch_fill_zero(y, rows, B, st);
+  if (rc || nnz == 0)
+    return rc;
+  if (streq(o.spmv_mapping, "wave-per-position")) {
+    const int64_t P = o.spmv_positions_per_lane;
+    const int64_t grid = std::max<int64_t>(ceil_div(ceil_div(nnz, P), B), 1);
+    rc = check_grid(grid, "run-segmented COO SpMV");
+    if (rc)
+      return rc;
+    const bool vec = aligned16(ri) && aligned16(col) && aligned16(val);
+    switch (P) {
+    case 1: launch_coo_runs<1, false>(grid, B, st, ri, col, val, x, y, nnz); break;
+    case 2: launch_coo_runs<2, false>(grid, B, st, ri, col, val, x, y, nnz); break;
+    case 4:
+      if (vec) launch_coo_runs<4, true>(grid, B, st, ri, col, val, x, y, nnz);
+      else launch_coo_runs<4, false>(grid, B, st, ri, col, val, x, y, nnz);
+      break;
+    case 8:
+      if (vec) launch_coo_runs<8, true>(grid, B, st, ri, col, val, x, y, nnz);
+      else launch_coo_runs<8, false>(grid, B, st, ri, col, val, x, y, nnz);
+      break;
+    default:
+      if (vec) launch_coo_runs<16, true>(grid, B, st, ri, col, val, x, y, nnz);
+      else launch_coo_runs<16, false>(grid, B, st, ri, col, val, x, y, nnz);
+      break;
+    }
+    return launch_check("run-segmented COO SpMV kernel");
+  }
+  const int64_t grid = std::max<int64_t>(ceil_div(nnz, B), 1);
+  rc = check_grid(grid, "thread-per-nonzero COO SpMV");
+  if (rc)
+    return rc;
+  hipLaunchKernelGGL(coo_thread_per_nonzero, dim3((unsigned)grid),
+                     dim3((unsigned)B), 0, st, ri, col, val, x, y, nnz);
+  return launch_check("thread-per-nonzero COO SpMV kernel");
+}
+
 } // namespace sw
 
 extern "C" int sw_spmv_csr_f32(const int32_t *row_offsets,
@@ -550,6 +709,35 @@ extern "C" int sw_spmv_csr_f32(const int32_t *row_offsets,
     return sw::fail(SW_ERR_INVALID_ARGUMENT, "vector or output pointer is null");
   return sw::launch_spmv(row_offsets, column_indices, values, vector, output,
                          rows, nnz, o, sw::as_stream(stream));
+}
+
+extern "C" int sw_spmv_coo_f32(const int32_t *row_indices,
+                               const int32_t *column_indices,
+                               const float *values, const float *vector,
+                               float *output, int64_t rows, int64_t cols,
+                               int64_t nnz, const sw_options *opts,
+                               void *stream) {
+  sw::clear_error();
+  sw_options o;
+  int rc = sw::resolve_options(opts, &o);
+  if (rc)
+    return rc;
+  if (rows < 0 || cols < 0 || nnz < 0)
+    return sw::fail(SW_ERR_INVALID_SHAPE,
+                    "expected non-negative rows, columns and nnz");
+  if (rows > INT32_MAX)
+    return sw::fail(SW_ERR_INVALID_SHAPE,
+                    "i32 COO row indices cannot address %lld rows",
+                    (long long)rows);
+  if (rows == 0)
+    return SW_OK;
+  if (!output)
+    return sw::fail(SW_ERR_INVALID_ARGUMENT, "output pointer is null");
+  if (nnz > 0 && (!row_indices || !column_indices || !values || !vector))
+    return sw::fail(SW_ERR_INVALID_ARGUMENT,
+                    "row index, column index, value or vector pointer is null");
+  return sw::launch_spmv_coo(row_indices, column_indices, values, vector,
+                             output, rows, nnz, o, sw::as_stream(stream));
 }
 
 extern "C" int sw_csr_row_at_position(const int32_t *row_offsets, int64_t rows,

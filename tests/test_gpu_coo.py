@@ -1,0 +1,117 @@
+"""GPU parity of sparsewave.coo_spmv (thread-per-nonzero and run-segmented)
+against the CPU oracle.
+
+fp32 bar: |y - y_ref| <= 1e-5 * sum |val * x| per row; the golden vector
+must match exactly."""
+import numpy as np
+import pytest
+import torch
+
+import sparsewavecomp_amd as sw
+from sparsewavecomp_amd import workloads as W
+from tests import gpu_util as G
+from tests._check import assert_within_bound
+
+pytestmark = pytest.mark.gpu
+
+MAPPINGS = [
+    "",  # reference lowering: thread per nonzero, spmv-block-size 256
+    "spmv-block-size=64",
+    "spmv-mapping=wave-per-position spmv-positions-per-lane=1",
+    "spmv-mapping=wave-per-position spmv-positions-per-lane=4",
+    "spmv-mapping=wave-per-position spmv-positions-per-lane=8 "
+    "spmv-block-size=64",
+    "spmv-mapping=wave-per-position spmv-positions-per-lane=16 "
+    "spmv-block-size=512",
+]
+
+
+def _run(rows, ri, ci, val, x, opts, offset=0):
+    """offset > 0 starts the COO arrays off a 16-byte boundary."""
+    G.say(f"coo_spmv rows={rows} nnz={len(ri)} opts='{opts}' offset={offset}")
+    t = G.t
+    pad = lambda a: t(np.concatenate([np.zeros(offset, a.dtype), a]))[offset:]
+    y = torch.full((rows,), float("nan"), device=G.DEV)
+    sw.coo_spmv(pad(ri), pad(ci), pad(val), t(x), y, options=opts or None)
+    torch.cuda.synchronize()
+    return y.cpu().numpy()
+
+
+def _check(orc, rows, ri, ci, val, x, opts, offset=0):
+    y = _run(rows, ri, ci, val, x, opts, offset)
+    ref, bound = orc.spmv_coo(rows, ri, ci, val, x)
+    assert_within_bound(y, ref, bound)
+
+
+def _coo(csr):
+    ri = np.repeat(np.arange(csr.rows, dtype=np.int32),
+                   np.diff(csr.row_offsets))
+    return ri, csr.column_indices, csr.values
+
+
+@pytest.mark.parametrize("opts", MAPPINGS)
+def test_golden(dev, golden, opts):
+    g = golden["coo_spmv"]
+    y = _run(g["rows"], np.array(g["row_indices"], np.int32),
+             np.array(g["column_indices"], np.int32),
+             np.array(g["values"], np.float32),
+             np.array(g["vector"], np.float32), opts)
+    np.testing.assert_array_equal(y, np.array(g["expected"], np.float32))
+
+
+@pytest.mark.parametrize("opts", MAPPINGS)
+@pytest.mark.parametrize("order", ["sorted", "shuffled"])
+def test_ragged(dev, orc, opts, order):
+    csr = W.random_csr(3000, 2500, 20.0, 7, empty_fraction=0.3,
+                       max_len=2500, lognormal=True)
+    ri, ci, val = _coo(csr)
+    if order == "shuffled":
+        p = np.random.default_rng(8).permutation(ri.size)
+        ri, ci, val = ri[p], ci[p], val[p]
+    x = np.random.default_rng(9).uniform(-1, 1, 2500).astype(np.float32)
+    _check(orc, csr.rows, ri, ci, val, x, opts)
+
+
+@pytest.mark.parametrize("opts", MAPPINGS)
+def test_duplicates_and_edges(dev, orc, opts):
+    rng = np.random.default_rng(10)
+    x = rng.uniform(-1, 1, 64).astype(np.float32)
+    # one long run of a single coordinate crossing lanes and waves
+    n = 5000
+    ri = np.full(n, 3, np.int32)
+    ci = np.full(n, 5, np.int32)
+    val = rng.uniform(-1, 1, n).astype(np.float32)
+    _check(orc, 10, ri, ci, val, x, opts)
+    # alternating rows (every entry its own run)
+    ri = (np.arange(n) % 2 * 9).astype(np.int32)
+    _check(orc, 10, ri, ci, val, x, opts)
+    # ragged tail lengths and a misaligned start
+    for m in (1, 3, 63, 65, 1023):
+        r = rng.integers(0, 7, m).astype(np.int32)
+        c = rng.integers(0, 64, m).astype(np.int32)
+        v = rng.uniform(-1, 1, m).astype(np.float32)
+        _check(orc, 7, np.sort(r), c, v, x, opts, offset=1)
+    # no entries: the output is zeroed
+    y = _run(5, np.zeros(0, np.int32), np.zeros(0, np.int32),
+             np.zeros(0, np.float32), x, opts)
+    np.testing.assert_array_equal(y, np.zeros(5, np.float32))
+
+
+@pytest.mark.parametrize("opts", [
+    "", "spmv-mapping=wave-per-position spmv-positions-per-lane=8 "
+    "spmv-block-size=64"])
+def test_config2_as_coo(dev, orc, opts):
+    """Config-2 pattern as row-sorted COO: equals the CSR product."""
+    csr, x = W.config2(seed=0)
+    ri, ci, val = _coo(csr)
+    _check(orc, csr.rows, ri, ci, val, x, opts)
+
+
+def test_errors(dev):
+    z = torch.zeros(4, dtype=torch.int32, device=G.DEV)
+    v = torch.zeros(4, device=G.DEV)
+    with pytest.raises(sw.SparseWaveError, match="same length"):
+        sw.coo_spmv(z, z[:3], v, v, v)
+    with pytest.raises(sw.SparseWaveError, match="positions-per-lane"):
+        sw.coo_spmv(z, z, v, v, v, options="spmv-mapping=wave-per-position "
+                                           "spmv-positions-per-lane=3")

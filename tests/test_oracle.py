@@ -40,6 +40,110 @@ def test_golden_spmv(orc, golden):
     np.testing.assert_array_equal(y, np.array(g["expected"], np.float32))
 
 
+def test_golden_coo_spmv(orc, golden):
+    g = golden["coo_spmv"]
+    y, bound = orc.spmv_coo(g["rows"], g["row_indices"], g["column_indices"],
+                            g["values"], np.array(g["vector"], np.float32))
+    np.testing.assert_array_equal(y, np.array(g["expected"], np.float32))
+    # all products are positive here, so the magnitude bound is the sum
+    np.testing.assert_array_equal(bound, np.array(g["expected"]))
+
+
+def _random_coo(rng, rows, cols, nnz, sort):
+    ri = rng.integers(0, rows, nnz).astype(np.int32)
+    ci = rng.integers(0, cols, nnz).astype(np.int32)
+    if sort:
+        o = np.lexsort((ci, ri))
+        ri, ci = ri[o], ci[o]
+    val = rng.uniform(-1, 1, nnz).astype(np.float32)
+    return ri, ci, val
+
+
+@pytest.mark.parametrize("sort", [True, False])
+def test_coo_spmv_matches_scipy(orc, sort):
+    """scipy's coo_matrix adds repeated coordinates, as the op does."""
+    rng = np.random.default_rng(11)
+    rows, cols = 300, 200
+    ri, ci, val = _random_coo(rng, rows, cols, 4000, sort)
+    ri[:50] = ri[50]  # a run of one row with repeated coordinates
+    ci[:50] = 7
+    x = rng.uniform(-1, 1, cols).astype(np.float32)
+    y, bound = orc.spmv_coo(rows, ri, ci, val, x)
+    a = sp.coo_matrix((val.astype(np.float64), (ri, ci)), shape=(rows, cols))
+    ref = a @ x.astype(np.float64)
+    assert_within_bound(y, ref, bound)
+    # mutation: dropping repeated coordinates (keeping the first) fails
+    _, first = np.unique(np.stack([ri, ci], 1), axis=0, return_index=True)
+    keep = np.sort(first)
+    y_bad, _ = orc.spmv_coo(rows, ri[keep], ci[keep], val[keep], x)
+    with pytest.raises(AssertionError):
+        assert_within_bound(y_bad, ref, bound)
+
+
+def _run_segmented_emulation(rows, ri, ci, val, x, P, wave=64):
+    """Lane-by-lane emulation of the run-segmented COO kernel's emission
+    rule (runs in a lane, a scan over the lanes' last runs keyed on run
+    numbers, head/tail hand-off between neighbours); products in float64 so
+    the comparison isolates the emission logic."""
+    y = np.zeros(rows)
+    nnz = ri.size
+    lanes = -(-nnz // P)
+    for w0 in range(0, lanes, wave):
+        L = []
+        for u in range(w0, min(w0 + wave, lanes)):
+            seg = list(range(u * P, min(u * P + P, nnz)))
+            runs = []
+            for p in seg:
+                pr = float(val[p]) * float(x[ci[p]])
+                if runs and runs[-1][0] == ri[p]:
+                    runs[-1][1] += pr
+                else:
+                    runs.append([int(ri[p]), pr])
+            L.append(runs)
+        L += [None] * (wave - len(L))
+        tails, keys = [], []
+        for i, runs in enumerate(L):
+            if runs is None:
+                keys.append(None)
+                tails.append(0.0)
+                continue
+            prev = L[i - 1][-1][0] if i and L[i - 1] else None
+            cont = len(runs) == 1 and runs[0][0] == prev
+            tails.append(runs[-1][1] + (tails[i - 1] if cont else 0.0))
+            keys.append(runs[-1][0])
+        for i, runs in enumerate(L):
+            if runs is None:
+                continue
+            prev_t = keys[i - 1] if i else None
+            if len(runs) > 1:
+                h = runs[0][1] + (tails[i - 1] if prev_t == runs[0][0] else 0)
+                y[runs[0][0]] += h
+                for r, s in runs[1:-1]:
+                    y[r] += s
+            nxt = L[i + 1][0][0] if i + 1 < wave and L[i + 1] else None
+            if nxt != runs[-1][0]:
+                y[runs[-1][0]] += tails[i]
+    return y
+
+
+@pytest.mark.parametrize("sort", [True, False])
+@pytest.mark.parametrize("P", [1, 4, 16])
+def test_run_segmented_emission_rule(orc, sort, P):
+    """The emission rule of the run-segmented COO kernel delivers every
+    entry exactly once, for sorted and unsorted entries, runs that cross
+    lanes and waves, and ragged final lanes."""
+    rng = np.random.default_rng(P + 2 * sort)
+    rows, cols = 40, 30
+    ri, ci, val = _random_coo(rng, rows, cols, 64 * P * 2 + 37, sort)
+    ri[100:100 + 3 * P * 64 // 2] = 5  # one row spanning lanes and waves
+    x = rng.uniform(-1, 1, cols).astype(np.float32)
+    y = _run_segmented_emulation(rows, ri, ci, val, x, P)
+    _, bound = orc.spmv_coo(rows, ri, ci, val, x)
+    ref = np.zeros(rows)
+    np.add.at(ref, ri, val.astype(np.float64) * x[ci])
+    np.testing.assert_allclose(y, ref, rtol=0, atol=1e-9 * (1 + bound.max()))
+
+
 @pytest.mark.parametrize("case", ["spmm", "spmm_torch_example"])
 def test_golden_spmm(orc, golden, case):
     g = golden[case]
