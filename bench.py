@@ -53,7 +53,117 @@ def parse():
     ap.add_argument("--mappings", default="",
                     help="';'-separated SpMV option strings to measure "
                          "instead of the default list")
+    ap.add_argument("--matrix", default="",
+                    help="also measure the SpMV mappings on this Matrix "
+                         "Market / SWCSR001 / SWCOO001 file (the reference "
+                         "harness's SuiteSparse workloads)")
+    ap.add_argument("--profile", default="",
+                    choices=["", "spmv", "coo", "spmm", "bsr", "bsr-bf16",
+                             "attention", "copy"],
+                    help="run one workload --steps times with no timing or "
+                         "JSON (for rocprofv3 kernel-trace / pmc runs)")
+    ap.add_argument("--opts", default="",
+                    help="option string for --profile (default: the "
+                         "headline mapping of that workload)")
+    ap.add_argument("--k", type=int, default=4,
+                    help="rhs columns for --profile spmm")
     return ap.parse_args()
+
+
+HEADLINE_SPMV = ("spmv-mapping=wave-per-position spmv-positions-per-lane=4 "
+                 "spmv-block-size=64")
+COPY_BYTES = 256 << 20
+
+
+def profile(args):
+    """--profile: the workload's kernels only, `--steps` times."""
+    import torch
+    import sparsewavecomp_amd as sw
+    from sparsewavecomp_amd import workloads as W
+
+    sw.load_library()
+    dev = torch.device("cuda:0")
+    T = lambda a, dt=None: (torch.from_numpy(np.ascontiguousarray(a)).to(dt)
+                            if dt else torch.from_numpy(
+                                np.ascontiguousarray(a))).to(dev)
+    w, n = args.profile, max(args.steps, 1)
+    log(f"profile {w} opts='{args.opts}' steps={n}")
+    if w == "copy":
+        # plain device copy of COPY_BYTES: FETCH_SIZE / WRITE_SIZE of this
+        # kernel calibrate the counters' units
+        src = torch.ones(COPY_BYTES // 4, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(n):
+            dst.copy_(src)
+    elif w in ("spmv", "coo", "spmm"):
+        csr, x = W.config2(seed=0)
+        ro, col, val = T(csr.row_offsets), T(csr.column_indices), T(csr.values)
+        if w == "spmv":
+            o = sw.Options.parse(args.opts or HEADLINE_SPMV)
+            xv, y = T(x), torch.empty(csr.rows, device=dev)
+            for _ in range(n):
+                sw.spmv(ro, col, val, xv, y, options=o)
+        elif w == "coo":
+            o = sw.Options.parse(args.opts or HEADLINE_SPMV)
+            ri = T(np.repeat(np.arange(csr.rows, dtype=np.int32),
+                             np.diff(csr.row_offsets)))
+            xv, y = T(x), torch.empty(csr.rows, device=dev)
+            for _ in range(n):
+                sw.coo_spmv(ri, col, val, xv, y, options=o)
+        else:
+            o = sw.Options.parse(args.opts or (
+                "spmm-mapping=wave-per-position spmm-positions-per-lane=16 "
+                "spmm-block-size=64"))
+            rhs = T(W.config3_rhs(csr.cols, args.k, seed=0))
+            out = torch.empty((csr.rows, args.k), device=dev)
+            for _ in range(n):
+                sw.spmm(ro, col, val, rhs, out, options=o)
+    elif w in ("bsr", "bsr-bf16"):
+        bsr, rhs = W.config4(seed=0)
+        dt = torch.bfloat16 if w == "bsr-bf16" else None
+        a4 = (T(bsr.block_row_offsets), T(bsr.block_column_indices),
+              T(bsr.block_values, dt), T(rhs, dt))
+        out = torch.empty((bsr.rows, 128), device=dev)
+        o = sw.Options.parse(args.opts)
+        for _ in range(n):
+            sw.bsr_spmm(*a4, out, 16, options=o)
+    elif w == "attention":
+        mask, q, kt, v, alpha = W.config5(seed=0)
+        att = (T(mask.row_offsets), T(mask.column_indices), T(mask.values),
+               T(q), T(kt), T(v))
+        s = torch.empty(mask.nnz, device=dev)
+        rm = torch.empty(mask.rows, device=dev)
+        rs = torch.empty(mask.rows, device=dev)
+        out = torch.empty((mask.rows, 64), device=dev)
+        o = sw.Options.parse(args.opts or (
+            "sddmm-mapping=row-tile-mfma sddmm-lanes-per-row=64 "
+            "spmm-mapping=row-tile-mfma"))
+        for _ in range(n):
+            sw.sparse_attention(*att, s, rm, rs, out, alpha, 0.0, options=o)
+    torch.cuda.synchronize()
+    log(f"profile {w} done")
+
+
+def traffic_from_profile(mapping):
+    """HBM bytes per SpMV launch (init + compute kernels) from the committed
+    rocprofv3 --pmc summary of the headline mapping, or None when the
+    summary is absent or was taken for another mapping."""
+    path = os.path.join(ROOT, "profiles", "spmv_config2_wave_position_pmc.md")
+    try:
+        text = open(path).read()
+    except OSError:
+        return None
+    fields = {}
+    for line in text.splitlines():
+        if line.startswith("- ") and " = " in line:
+            k, v = line[2:].split(" = ", 1)
+            fields[k.strip()] = v.strip().strip("`")
+    if fields.get("mapping") != mapping:
+        return None
+    try:
+        return int(fields["traffic_bytes_per_launch"])
+    except (KeyError, ValueError):
+        return None
 
 
 def time_steps(fn, steps, warmup):
@@ -80,6 +190,9 @@ def main():
         print(json.dumps({"error": "this build measures one GPU; every GPU "
                           "box has one MI355X, so --gpus must be 1"}))
         sys.exit(2)
+    if args.profile:
+        profile(args)
+        return
     import torch
     import sparsewavecomp_amd as sw
     from sparsewavecomp_amd import workloads as W
@@ -109,8 +222,7 @@ def main():
     spmv_bytes = W.algorithmic_bytes_spmv(n, m, nnz)
     spmv_flops = 2 * nnz
     mappings = [
-        "spmv-mapping=wave-per-position spmv-positions-per-lane=4 "
-        "spmv-block-size=64",
+        HEADLINE_SPMV,
         "spmv-mapping=wave-per-position spmv-positions-per-lane=8 "
         "spmv-block-size=64",
         "spmv-mapping=wave-per-position spmv-positions-per-lane=8 "
@@ -157,6 +269,46 @@ def main():
         except Exception as e:  # the comparison is optional
             rocsparse["error"] = str(e)
     workloads["rocsparse_config2"] = rocsparse
+
+    if not args.only_headline:
+        # the configuration-2 matrix as row-sorted COO (sparsewave.coo_spmv);
+        # bytes count the row-index array in place of the row offsets
+        ri = T(np.repeat(np.arange(n, dtype=np.int32),
+                         np.diff(csr.row_offsets)))
+        coo_bytes = 12 * nnz + 4 * m + 4 * n
+        for opts in ["", HEADLINE_SPMV]:
+            o = sw.Options.parse(opts)
+            log(f"COO SpMV '{opts}'")
+            ms = time_steps(lambda: sw.coo_spmv(ri, col, val, xv, y,
+                                                options=o), K, Wm)
+            workloads.setdefault("coo_spmv_config2", {})[
+                opts or "reference (thread-per-nonzero)"] = {
+                "ms": ms, "GB/s": coo_bytes / ms / 1e6,
+                "hbm_frac": coo_bytes / ms / 1e6 / HBM_PEAK_GBS}
+            log(f"  {ms * 1e3:.1f} us  {coo_bytes / ms / 1e6:.0f} GB/s")
+        del ri
+
+    if args.matrix:
+        from sparsewavecomp_amd import formats as F
+        mat = F.read_matrix(args.matrix)
+        if mat["row_offsets"] is None:
+            raise SystemExit(f"{args.matrix}: entries are not stored by row")
+        mro, mcol = T(mat["row_offsets"]), T(mat["column_indices"])
+        mval = T(mat["values"].astype(np.float32))
+        mx = T(F.benchmark_vector(mat["columns"]))
+        my = torch.empty(mat["rows"], device=dev)
+        mb = W.algorithmic_bytes_spmv(mat["rows"], mat["columns"], mat["nnz"])
+        res = {}
+        for opts in mappings:
+            o = sw.Options.parse(opts)
+            ms = time_steps(lambda: sw.spmv(mro, mcol, mval, mx, my,
+                                            options=o), K, Wm)
+            res[opts] = {"ms": ms, "GB/s": mb / ms / 1e6}
+            log(f"{os.path.basename(args.matrix)} {opts}: {ms * 1e3:.1f} us")
+        workloads["matrix_file"] = {"path": args.matrix, "rows": mat["rows"],
+                                    "nnz": mat["nnz"], "bytes": mb,
+                                    "mappings": res}
+        del mro, mcol, mval, mx, my
 
     if not args.only_headline:
         # ---- configuration 1: the reference's CPU-runnable case ------------
@@ -311,7 +463,7 @@ def main():
         "roofline": {
             "bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic_from_profile(best),
         },
         "cpu_baseline": cpu,
         "workloads": workloads,
