@@ -42,7 +42,10 @@ def test_bsr_golden(dev, golden, opts):
 
 
 @pytest.mark.parametrize("opts", BSR_OPTS)
-@pytest.mark.parametrize("b,k", [(16, 128), (16, 40), (16, 200), (4, 9)])
+# k % 4 == 0 takes the column-interleaved MFMA kernels (partial strips at 40
+# and 200), other k the scalar-load MFMA kernels
+@pytest.mark.parametrize("b,k", [(16, 128), (16, 40), (16, 200), (16, 30),
+                                 (16, 7), (4, 9)])
 def test_bsr_fp32(dev, orc, opts, b, k):
     bsr = W.bsr_banded(seed=b + k, rows=b * 96, block_size=b,
                        blocks_per_row=6, band=3, band_blocks=3,
@@ -58,9 +61,10 @@ def test_bsr_fp32(dev, orc, opts, b, k):
 
 
 @pytest.mark.parametrize("opts", ["bsr-use-mfma=1", "bsr-use-mfma=0"])
-def test_bsr_bf16(dev, orc, opts):
+@pytest.mark.parametrize("k", [128, 36, 30])
+def test_bsr_bf16(dev, orc, opts, k):
     bsr = W.bsr_banded(seed=3, rows=16 * 128, block_size=16)
-    rhs = np.random.default_rng(3).standard_normal((bsr.cols, 128)).astype(
+    rhs = np.random.default_rng(3).standard_normal((bsr.cols, k)).astype(
         np.float32)
     out = _bsr_run(bsr, rhs, opts, bf16=True)
     ref = orc.bsr_spmm(bsr.block_row_offsets, bsr.block_column_indices,
