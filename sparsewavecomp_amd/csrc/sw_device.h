@@ -112,6 +112,17 @@ __device__ __forceinline__ float wave_segmented_scan(int key, float v) {
   return v;
 }
 
+// XCD-contiguous workgroup order.  Workgroups are dispatched to the eight
+// XCDs round-robin (workgroup b to XCD b % 8); this maps b to a position so
+// that each XCD works through one contiguous range of the n workgroups' work,
+// and neighbouring work items share that XCD's L2.  A bijection on [0, n).
+__device__ __forceinline__ int64_t xcd_contiguous(int64_t b, int64_t n) {
+  constexpr int64_t kXcds = 8;
+  const int64_t q = n / kXcds, r = n % kXcds;
+  const int64_t x = b % kXcds, i = b / kXcds;
+  return x * q + (x < r ? x : r) + i;
+}
+
 // Shift by one lane up / down across the whole wave (ds_bpermute).
 __device__ __forceinline__ int shfl_up1_i(int v, int fill) {
   int l = lane_id();

@@ -52,7 +52,8 @@ __global__ __launch_bounds__(1024) void spmm_row_tile(
     int64_t tiles_per_row) {
   constexpr int PL = G / CL;
   const int units_per_block = blockDim.x / G;
-  const int64_t unit = (int64_t)blockIdx.x * units_per_block + threadIdx.x / G;
+  const int64_t unit =
+      xcd_contiguous(blockIdx.x, gridDim.x) * units_per_block + threadIdx.x / G;
   const int gl = threadIdx.x & (G - 1);
   const int pl = gl / CL;
   const int cl = gl % CL;
@@ -103,14 +104,18 @@ __global__ __launch_bounds__(1024) void spmm_row_tile(
   }
   if (unit_ok && pl == 0 && cb < cend) {
     float *o = out + r * k + cb;
+    // non-temporal: the output is not re-read and should not displace RHS
+    // rows from L2
     if (V == 4 && cb + 4 <= cend) {
-      *reinterpret_cast<v4f *>(o) = v4f{acc[0], acc[V > 1 ? 1 : 0],
-                                        acc[V > 2 ? 2 : 0], acc[V > 3 ? 3 : 0]};
+      __builtin_nontemporal_store(
+          v4f{acc[0], acc[V > 1 ? 1 : 0], acc[V > 2 ? 2 : 0],
+              acc[V > 3 ? 3 : 0]},
+          reinterpret_cast<v4f *>(o));
     } else {
 #pragma unroll
       for (int i = 0; i < V; ++i)
         if (cb + i < cend)
-          o[i] = acc[i];
+          __builtin_nontemporal_store(acc[i], o + i);
     }
   }
 }
