@@ -326,7 +326,8 @@ def main():
         # ---- configuration 3: CSR SpMM K = 4 and 64 -------------------------
         for k, opts in [(4, "spmm-mapping=wave-per-position "
                             "spmm-positions-per-lane=8 spmm-block-size=256"),
-                        (4, "spmm-mapping=wave-per-row-tile spmm-tile-size=4"),
+                        (4, "spmm-mapping=wave-per-row-tile spmm-tile-size=4 "
+                            "spmm-block-size=64"),
                         (64, "spmm-mapping=wave-per-position "
                              "spmm-positions-per-lane=16 spmm-block-size=64"),
                         (64, "spmm-mapping=wave-per-row-tile "

@@ -28,6 +28,9 @@ int launch_spmm(const int32_t *ro, const int32_t *col, const float *val,
 
 namespace {
 
+// waves per 16-row SDDMM tile (4: 20.9 us on configuration 5; 8: 24.6 us)
+constexpr int kSddmmTileWaves = 4;
+
 __device__ __forceinline__ float combine_sddmm(int kind, float sample,
                                                float dot, float alpha,
                                                float beta) {
@@ -136,17 +139,21 @@ __global__ __launch_bounds__(256) void sddmm_wave_per_row(
 
 // SDDMM over 16-row tiles on the matrix cores (kdim = 64 * KB).
 //
-// A workgroup of four waves owns rows r0 .. r0+15.  When every row's columns
+// A workgroup of W waves owns rows r0 .. r0+15.  When every row's columns
 // are a prefix of the last row's (tile_prefix_ok_block), the tile's dot products
 // for 16 of the last row's columns at a time are one 16 x 16 x kdim product
 //   D = lhs[r0 .. r0+15][:] * rhs[:][c_t0 .. c_t0+15]
 // computed with v_mfma_f32_16x16x4_f32 (lane (i, g) supplies
 // lhs[r0+i][16g+s] at step s, lane (j, g) supplies rhs[16g+s][c_j]); wave w
-// takes the column chunks w, w+4, ...  Each result lands at its CSR position
+// takes the column chunks w, w+W, ...  Each result lands at its CSR position
 // ro[row] + t when t is inside that row.  Tiles without the shared structure
 // are computed row by row on the vector ALUs.
-template <int KB>
-__global__ __launch_bounds__(256) void sddmm_tile_mfma(
+//
+// Latency: the row bounds and lhs rows are requested before the structure
+// check waits, and a chunk pair's sampled values before its rhs loads wait
+// (checking the structure inside the chunk loop instead measured slower).
+template <int KB, int W>
+__global__ __launch_bounds__(64 * W) void sddmm_tile_mfma(
     const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
     const float *__restrict__ val, const float *__restrict__ lhs,
     const float *__restrict__ rhs, float *__restrict__ out, int32_t rows,
@@ -154,17 +161,7 @@ __global__ __launch_bounds__(256) void sddmm_tile_mfma(
   const int r0 = blockIdx.x * 16;
   const int nt = std::min(16, rows - r0);
   const int wave = threadIdx.x / kWave;
-  __shared__ int verdict;
-  if (!tile_prefix_ok_block(ro, col, r0, nt, &verdict)) {
-    for (int r = r0 + wave; r < r0 + nt; r += 4)
-      sddmm_row_wave(ro, col, val, lhs, rhs, out, r, cols, kdim, kind, alpha,
-                     beta);
-    return;
-  }
   const int l = lane_id(), i = l & 15, g = l >> 4;
-  const int last = r0 + nt - 1;
-  const int32_t bl = ro[last];
-  const int32_t len_last = ro[last + 1] - bl;
   int32_t rb[4], rl[4];
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
@@ -180,13 +177,30 @@ __global__ __launch_bounds__(256) void sddmm_tile_mfma(
       qa[kb * 16 + st] = i < nt ? lhs[(int64_t)(r0 + i) * kdim + kb * 64 +
                                       16 * g + st]
                                 : 0.0f;
-  // two column chunks per iteration (waves w and w+4 apart): two
-  // independent accumulators and 32 outstanding rhs loads per lane
-  for (int32_t t0 = wave * 16; t0 < len_last; t0 += 128) {
-    const int32_t t1 = t0 + 64;
+  __shared__ int verdict;
+  if (!tile_prefix_ok_block(ro, col, r0, nt, &verdict)) {
+    for (int r = r0 + wave; r < r0 + nt; r += W)
+      sddmm_row_wave(ro, col, val, lhs, rhs, out, r, cols, kdim, kind, alpha,
+                     beta);
+    return;
+  }
+  const int last = r0 + nt - 1;
+  const int32_t bl = ro[last];
+  const int32_t len_last = ro[last + 1] - bl;
+  // two column chunks per iteration (W chunks apart): two independent
+  // accumulators and 32 outstanding rhs loads per lane
+  for (int32_t t0 = wave * 16; t0 < len_last; t0 += 32 * W) {
+    const int32_t t1 = t0 + 16 * W;
     const bool two = t1 < len_last; // wave-uniform
-    const int64_t cj0 = t0 + i < len_last ? (int64_t)col[bl + t0 + i] : 0;
-    const int64_t cj1 = two && t1 + i < len_last ? (int64_t)col[bl + t1 + i] : 0;
+    const int32_t ta = t0 + i, tb = t1 + i;
+    const int64_t cj0 = ta < len_last ? (int64_t)col[bl + ta] : 0;
+    const int64_t cj1 = two && tb < len_last ? (int64_t)col[bl + tb] : 0;
+    float s0[4], s1[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      s0[v] = val != nullptr && ta < rl[v] ? val[rb[v] + ta] : 0.0f;
+      s1[v] = val != nullptr && two && tb < rl[v] ? val[rb[v] + tb] : 0.0f;
+    }
     v4f acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
@@ -208,17 +222,10 @@ __global__ __launch_bounds__(256) void sddmm_tile_mfma(
     }
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-      const int32_t ta = t0 + i, tb = t1 + i;
-      if (ta < rl[v]) {
-        const int32_t p = rb[v] + ta;
-        out[p] = combine_sddmm(kind, val != nullptr ? val[p] : 0.0f, acc0[v],
-                               alpha, beta);
-      }
-      if (two && tb < rl[v]) {
-        const int32_t p = rb[v] + tb;
-        out[p] = combine_sddmm(kind, val != nullptr ? val[p] : 0.0f, acc1[v],
-                               alpha, beta);
-      }
+      if (ta < rl[v])
+        out[rb[v] + ta] = combine_sddmm(kind, s0[v], acc0[v], alpha, beta);
+      if (two && tb < rl[v])
+        out[rb[v] + tb] = combine_sddmm(kind, s1[v], acc1[v], alpha, beta);
     }
   }
 }
@@ -289,9 +296,12 @@ __global__ __launch_bounds__(256) void rowwise_map_wave(
 
 
 // The four row ops of the attention chain fused (row max, exp(s - max), row
-// sum, s / sum): one wave per row, one read and one write of the row's
-// scores besides the max pass; rowMaximum and rowSum are written as the
-// separate ops would write them.
+// sum, s / sum): one wave per row.  Rows of up to 64 * kSoftmaxRegs entries
+// stay in registers between the ops (one read and one write of the scores);
+// longer rows take a max pass and two read/write passes.  rowMaximum and
+// rowSum are written as the separate ops would write them.
+constexpr int kSoftmaxRegs = 8;
+
 __global__ __launch_bounds__(256) void row_softmax_wave(
     const int32_t *__restrict__ ro, float *scores, float *__restrict__ rmax,
     float *__restrict__ rsum, int32_t rows) {
@@ -302,18 +312,42 @@ __global__ __launch_bounds__(256) void row_softmax_wave(
   const int l = lane_id();
   const int32_t s = ro[r], e = ro[r + 1];
   float m = -INFINITY;
-  for (int32_t p = s + l; p < e; p += kWave)
-    m = maximumf(m, scores[p]);
-  m = wave_max(m);
   float sum = 0.0f;
-  for (int32_t p = s + l; p < e; p += kWave) {
-    const float v = expf(scores[p] - m);
-    scores[p] = v;
-    sum += v;
+  if (e - s <= kWave * kSoftmaxRegs) { // wave-uniform
+    float v[kSoftmaxRegs];
+#pragma unroll
+    for (int j = 0; j < kSoftmaxRegs; ++j) {
+      const int32_t p = s + l + j * kWave;
+      v[j] = p < e ? scores[p] : -INFINITY;
+      m = maximumf(m, v[j]);
+    }
+    m = wave_max(m);
+#pragma unroll
+    for (int j = 0; j < kSoftmaxRegs; ++j)
+      if (s + l + j * kWave < e) {
+        v[j] = expf(v[j] - m);
+        sum += v[j];
+      }
+    sum = group_sum<kWave>(sum);
+#pragma unroll
+    for (int j = 0; j < kSoftmaxRegs; ++j) {
+      const int32_t p = s + l + j * kWave;
+      if (p < e)
+        scores[p] = v[j] / sum;
+    }
+  } else {
+    for (int32_t p = s + l; p < e; p += kWave)
+      m = maximumf(m, scores[p]);
+    m = wave_max(m);
+    for (int32_t p = s + l; p < e; p += kWave) {
+      const float v = expf(scores[p] - m);
+      scores[p] = v;
+      sum += v;
+    }
+    sum = group_sum<kWave>(sum);
+    for (int32_t p = s + l; p < e; p += kWave)
+      scores[p] = scores[p] / sum;
   }
-  sum = group_sum<kWave>(sum);
-  for (int32_t p = s + l; p < e; p += kWave)
-    scores[p] = scores[p] / sum;
   if (l == 0) {
     rmax[r] = m;
     rsum[r] = sum;
@@ -342,8 +376,9 @@ int launch_sddmm(const int32_t *ro, const int32_t *col, const float *val,
       return rc;
     const int kb = (int)(kdim / 64);
 #define SW_SDDMM_TILE(KB)                                                     \
-  hipLaunchKernelGGL(sddmm_tile_mfma<KB>, dim3((unsigned)grid), dim3(256), 0, \
-                     st, ro, col, val, lhs, rhs, out, (int32_t)rows, cols,    \
+  hipLaunchKernelGGL((sddmm_tile_mfma<KB, kSddmmTileWaves>),                  \
+                     dim3((unsigned)grid), dim3(64 * kSddmmTileWaves), 0, st, \
+                     ro, col, val, lhs, rhs, out, (int32_t)rows, cols,        \
                      (int32_t)kdim, kind, alpha, beta)
     if (kb == 1)
       SW_SDDMM_TILE(1);

@@ -213,14 +213,15 @@ __device__ __forceinline__ int row_search_gallop(const int32_t *__restrict__ ro,
 // tile's dense products over the last row's columns give every stored entry.
 // The check reads every column index of the tile once.
 //
-// tile_prefix_ok_block splits the rows over the four waves of a 256-thread
-// workgroup (wave w checks rows w, w+4, ...) and combines their verdicts in
-// LDS; every thread of the workgroup must call it (it has a barrier).
+// tile_prefix_ok_block splits the rows over the W waves of the workgroup
+// (wave w checks rows w, w+W, ...) and combines their verdicts in LDS; every
+// thread of the workgroup must call it (it has a barrier).
 __device__ __forceinline__ bool tile_prefix_ok_block(
     const int32_t *__restrict__ ro, const int32_t *__restrict__ col, int r0,
     int nt, int *verdict /* __shared__ int[1] */) {
   const int lane = lane_id();
   const int wave = threadIdx.x / kWave;
+  const int waves = blockDim.x / kWave;
   if (threadIdx.x == 0)
     *verdict = 1;
   __syncthreads();
@@ -229,7 +230,7 @@ __device__ __forceinline__ bool tile_prefix_ok_block(
   const int32_t base_last = __builtin_amdgcn_readlane(my_ro, nt - 1);
   const int32_t len_last = __builtin_amdgcn_readlane(my_ro, nt) - base_last;
   bool ok = true;
-  for (int i = wave; i < nt - 1; i += 4) {
+  for (int i = wave; i < nt - 1; i += waves) {
     const int32_t b = __builtin_amdgcn_readlane(my_ro, i);
     const int32_t len = __builtin_amdgcn_readlane(my_ro, i + 1) - b;
     if (len > len_last) {
@@ -245,6 +246,7 @@ __device__ __forceinline__ bool tile_prefix_ok_block(
   __syncthreads();
   return *verdict != 0;
 }
+
 
 // Wave-cooperative 64-ary search for a wave-uniform position: every round
 // each lane probes one offset and a ballot narrows the range 64-fold, so a

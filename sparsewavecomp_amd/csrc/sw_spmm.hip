@@ -441,38 +441,42 @@ __device__ __forceinline__ void spmm_row_wave(const int32_t *__restrict__ ro,
 // the tile's values (zero past each row's end) with the rhs rows of the last
 // row's columns, 16 stored entries (four v_mfma_f32_16x16x4_f32 steps) at a
 // time: lane (i, g) supplies val[ro[r0+i] + t0+4g+s], lane (j, g) supplies
-// rhs[c_{t0+4g+s}][n0+j].  The four waves split the stored entries (wave w
-// takes the 32-entry chunks w, w+4, ...), each accumulates four 16-column
+// rhs[c_{t0+4g+s}][n0+j].  The W waves split the stored entries (wave w
+// takes the 32-entry chunks w, w+W, ...), each accumulates four 16-column
 // output tiles, and the partial tiles are summed through LDS.  Tiles without
-// the shared structure are computed row by row.
-__global__ __launch_bounds__(256) void spmm_tile_mfma(
+// the shared structure are computed row by row.  Eight waves per tile
+// (17.6 us on configuration 5, four: 21.9 us) give the chip enough waves:
+// 8192 rows are only 512 tiles.
+template <int W>
+__global__ __launch_bounds__(64 * W) void spmm_tile_mfma(
     const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
     const float *__restrict__ val, const float *__restrict__ rhs,
     float *__restrict__ out, int32_t rows, int64_t k) {
   constexpr int CH = 2; // 16-entry chunks per step
-  __shared__ float part[4][4][4][kWave]; // [wave][n tile][v][lane]
+  __shared__ float part[W][4][4][kWave]; // [wave][n tile][v][lane]
   const int r0 = blockIdx.x * 16;
   const int nt = std::min(16, rows - r0);
   const int wave = threadIdx.x / kWave;
-  __shared__ int verdict;
-  if (!tile_prefix_ok_block(ro, col, r0, nt, &verdict)) {
-    for (int r = r0 + wave; r < r0 + nt; r += 4)
-      spmm_row_wave(ro, col, val, rhs, out, r, k);
-    return;
-  }
   const int l = lane_id(), i = l & 15, g = l >> 4;
+  // the row bounds are requested before the structure check waits
   const int last = r0 + nt - 1;
   const int32_t bl = ro[last];
   const int32_t len_last = ro[last + 1] - bl;
   const int32_t ra = i < nt ? ro[r0 + i] : 0;
   const int32_t la = i < nt ? ro[r0 + i + 1] - ra : 0;
+  __shared__ int verdict;
+  if (!tile_prefix_ok_block(ro, col, r0, nt, &verdict)) {
+    for (int r = r0 + wave; r < r0 + nt; r += W)
+      spmm_row_wave(ro, col, val, rhs, out, r, k);
+    return;
+  }
   for (int64_t nb = 0; nb < k; nb += 64) {
     const int ntiles = (int)std::min<int64_t>(4, (k - nb) / 16);
     v4f acc[4];
 #pragma unroll
     for (int n = 0; n < 4; ++n)
       acc[n] = v4f{0.f, 0.f, 0.f, 0.f};
-    for (int32_t t0 = wave * 16 * CH; t0 < len_last; t0 += 4 * 16 * CH) {
+    for (int32_t t0 = wave * 16 * CH; t0 < len_last; t0 += W * 16 * CH) {
       float a[CH][4];
       int64_t c[CH][4];
 #pragma unroll
@@ -512,8 +516,10 @@ __global__ __launch_bounds__(256) void spmm_tile_mfma(
     if (wave < ntiles) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const float sum = part[0][wave][v][l] + part[1][wave][v][l] +
-                          part[2][wave][v][l] + part[3][wave][v][l];
+        float sum = 0.0f;
+#pragma unroll
+        for (int w = 0; w < W; ++w)
+          sum += part[w][wave][v][l];
         const int rr = 4 * g + v;
         if (rr < nt)
           out[(int64_t)(r0 + rr) * k + nb + 16 * wave + i] = sum;
@@ -713,8 +719,8 @@ int launch_spmm(const int32_t *ro, const int32_t *col, const float *val,
     int rc = check_grid(grid, what);
     if (rc)
       return rc;
-    hipLaunchKernelGGL(spmm_tile_mfma, dim3((unsigned)grid), dim3(256), 0, st,
-                       ro, col, val, rhs, out, (int32_t)rows, k);
+    hipLaunchKernelGGL(spmm_tile_mfma<8>, dim3((unsigned)grid), dim3(512), 0,
+                       st, ro, col, val, rhs, out, (int32_t)rows, k);
     return launch_check("SpMM tile MFMA kernel");
   }
   if (streq(o.spmm_mapping, "wave-per-row-balanced") && k % 4 == 0 &&

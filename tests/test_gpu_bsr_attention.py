@@ -144,6 +144,81 @@ def test_sddmm_golden_and_random(dev, orc, golden, opts):
             assert_within_bound(out.cpu().numpy(), ref, bound + 1e-30)
 
 
+def _tile_structure_csr():
+    """87 rows in 16-row tiles exercising each path of the MFMA tile
+    kernels: prefix-structured tiles (the MFMA path), a row with the last
+    row's length but one different column (recomputed after the shared
+    check), a row longer than the tile's last row (row path from the start),
+    empty rows, a mismatch deep in the row (a later wave's chunk), and a
+    partial last tile."""
+    rng = np.random.default_rng(31)
+    cols = 300
+    rows_cols = []
+    for tile in range(6):
+        nt = 16 if tile < 5 else 7
+        base = np.sort(rng.choice(cols, 200, replace=False))
+        lens = np.sort(rng.integers(1, 201, nt))
+        lens[-1] = 200
+        if tile == 3:
+            lens[:5] = 0
+        tile_rows = [base[:n].copy() for n in lens]
+        if tile == 1:                       # same length, one column differs
+            tile_rows[5] = tile_rows[-1][:lens[5]].copy()
+            spare = np.setdiff1d(np.arange(cols), base)[0]
+            tile_rows[5][min(10, lens[5] - 1)] = spare
+            tile_rows[5] = np.sort(tile_rows[5])
+        if tile == 2:                       # a row longer than the last
+            extra = np.setdiff1d(np.arange(cols), base)[:5]
+            tile_rows[3] = np.sort(np.concatenate([base, extra]))
+        if tile == 4:                       # mismatch at position 150
+            tile_rows[9] = base[:200].copy()
+            tile_rows[9][150] = np.setdiff1d(np.arange(cols), base)[1]
+            tile_rows[9] = np.sort(tile_rows[9])
+            tile_rows[-1] = base.copy()
+        rows_cols += tile_rows
+    lengths = np.array([len(c) for c in rows_cols])
+    ro = np.zeros(len(rows_cols) + 1, np.int32)
+    np.cumsum(lengths, out=ro[1:])
+    col = np.concatenate(rows_cols).astype(np.int32)
+    val = rng.uniform(-1, 1, col.size).astype(np.float32)
+    return W.CSR(len(rows_cols), cols, ro, col, val)
+
+
+@pytest.mark.parametrize("kind", ["mul", "affine"])
+def test_sddmm_tile_structure_paths(dev, orc, kind):
+    csr = _tile_structure_csr()
+    rng = np.random.default_rng(5)
+    lhs = rng.standard_normal((csr.rows, 64)).astype(np.float32)
+    rhs = rng.standard_normal((64, csr.cols)).astype(np.float32)
+    k = sw.SDDMM_MUL if kind == "mul" else sw.SDDMM_AFFINE
+    out = torch.full((csr.nnz,), float("nan"), device=G.DEV)
+    G.say(f"sddmm tile structure paths kind={kind}")
+    sw.sddmm(G.t(csr.row_offsets), G.t(csr.column_indices), G.t(csr.values),
+             G.t(lhs), G.t(rhs), out, k, 0.3, 0.7,
+             options="sddmm-mapping=row-tile-mfma")
+    torch.cuda.synchronize()
+    ref = orc.sddmm(csr.row_offsets, csr.column_indices, csr.values, lhs, rhs,
+                    k, 0.3, 0.7)
+    rows = np.repeat(np.arange(csr.rows), np.diff(csr.row_offsets))
+    b = (np.abs(lhs.astype(np.float64)) @ np.abs(rhs.astype(np.float64)))[
+        rows, csr.column_indices]
+    v = np.abs(csr.values.astype(np.float64))
+    bound = v * b if kind == "mul" else 0.7 * v + 0.3 * b
+    assert_within_bound(out.cpu().numpy(), ref, bound + 1e-30)
+
+
+@pytest.mark.parametrize("k", [16, 64, 80])
+def test_spmm_tile_structure_paths(dev, orc, k):
+    csr = _tile_structure_csr()
+    rhs = np.random.default_rng(k).standard_normal((csr.cols, k)).astype(
+        np.float32)
+    out = G.spmm(csr, rhs, "spmm-mapping=row-tile-mfma")
+    ref = orc.spmm(csr.row_offsets, csr.column_indices, csr.values, rhs)
+    bound = orc.spmm_abs_bound(csr.row_offsets, csr.column_indices,
+                               csr.values, rhs)
+    assert_within_bound(out, ref, bound)
+
+
 @pytest.mark.parametrize("opts", ROW_OPTS)
 def test_row_reduce_and_map(dev, orc, golden, opts):
     g = golden["row_reduce"]
