@@ -162,21 +162,30 @@ __global__ __launch_bounds__(64 * W) void sddmm_tile_mfma(
   const int nt = std::min(16, rows - r0);
   const int wave = threadIdx.x / kWave;
   const int l = lane_id(), i = l & 15, g = l >> 4;
+  // loads are unconditional from clamped, valid addresses, their values
+  // selected afterwards (a guarded load becomes a branch that waits for it
+  // on the spot)
   int32_t rb[4], rl[4];
+  {
+    int32_t b[5];
 #pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    const int rr = r0 + 4 * g + v;
-    rb[v] = rr < r0 + nt ? ro[rr] : 0;
-    rl[v] = rr < r0 + nt ? ro[rr + 1] - rb[v] : 0;
+    for (int v = 0; v < 5; ++v)
+      b[v] = ro[std::min(r0 + 4 * g + v, rows)];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      rb[v] = b[v];
+      rl[v] = 4 * g + v < nt ? b[v + 1] - b[v] : 0;
+    }
   }
   float qa[16 * KB];
+  const int64_t qrow = (int64_t)std::min(r0 + i, rows - 1) * kdim;
 #pragma unroll
   for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-    for (int st = 0; st < 16; ++st)
-      qa[kb * 16 + st] = i < nt ? lhs[(int64_t)(r0 + i) * kdim + kb * 64 +
-                                      16 * g + st]
-                                : 0.0f;
+    for (int st = 0; st < 16; ++st) {
+      const float x = lhs[qrow + kb * 64 + 16 * g + st];
+      qa[kb * 16 + st] = i < nt ? x : 0.0f;
+    }
   __shared__ int verdict;
   if (!tile_prefix_ok_block(ro, col, r0, nt, &verdict)) {
     for (int r = r0 + wave; r < r0 + nt; r += W)
@@ -198,8 +207,13 @@ __global__ __launch_bounds__(64 * W) void sddmm_tile_mfma(
     float s0[4], s1[4];
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-      s0[v] = val != nullptr && ta < rl[v] ? val[rb[v] + ta] : 0.0f;
-      s1[v] = val != nullptr && two && tb < rl[v] ? val[rb[v] + tb] : 0.0f;
+      // position bl is inside the last row, always a valid index
+      const bool in0 = val != nullptr && ta < rl[v];
+      const bool in1 = val != nullptr && two && tb < rl[v];
+      const float x0 = val != nullptr ? val[in0 ? rb[v] + ta : bl] : 0.0f;
+      const float x1 = val != nullptr ? val[in1 ? rb[v] + tb : bl] : 0.0f;
+      s0[v] = in0 ? x0 : 0.0f;
+      s1[v] = in1 ? x1 : 0.0f;
     }
     v4f acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -313,12 +327,15 @@ __global__ __launch_bounds__(256) void row_softmax_wave(
   const int32_t s = ro[r], e = ro[r + 1];
   float m = -INFINITY;
   float sum = 0.0f;
-  if (e - s <= kWave * kSoftmaxRegs) { // wave-uniform
+  if (e > s && e - s <= kWave * kSoftmaxRegs) { // wave-uniform
     float v[kSoftmaxRegs];
 #pragma unroll
     for (int j = 0; j < kSoftmaxRegs; ++j) {
+      // unconditional load from a clamped index, then select (a guarded
+      // load would wait on the spot)
       const int32_t p = s + l + j * kWave;
-      v[j] = p < e ? scores[p] : -INFINITY;
+      const float x = scores[p < e ? p : e - 1];
+      v[j] = p < e ? x : -INFINITY;
       m = maximumf(m, v[j]);
     }
     m = wave_max(m);

@@ -8,6 +8,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
 
 namespace swd {
@@ -225,8 +226,10 @@ __device__ __forceinline__ bool tile_prefix_ok_block(
   if (threadIdx.x == 0)
     *verdict = 1;
   __syncthreads();
-  // lanes 0..nt hold ro[r0 .. r0+nt]: one load instead of a chain
-  const int32_t my_ro = lane <= nt ? ro[r0 + lane] : 0;
+  // lanes 0..nt hold ro[r0 .. r0+nt]: one load instead of a chain (loads
+  // here are unconditional from clamped, valid addresses: a guarded load
+  // becomes a branch that waits for it on the spot)
+  const int32_t my_ro = ro[r0 + (lane < nt ? lane : nt)];
   const int32_t base_last = __builtin_amdgcn_readlane(my_ro, nt - 1);
   const int32_t len_last = __builtin_amdgcn_readlane(my_ro, nt) - base_last;
   bool ok = true;
@@ -237,9 +240,18 @@ __device__ __forceinline__ bool tile_prefix_ok_block(
       ok = false;
       break; // wave-uniform
     }
-#pragma unroll 4
-    for (int32_t t = lane; t < len; t += kWave)
-      ok &= col[b + t] == col[base_last + t];
+    for (int32_t t0 = 0; t0 < len; t0 += 4 * kWave) { // wave-uniform
+      int32_t x[4], y[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int32_t t = std::min(t0 + u * kWave + lane, len - 1);
+        x[u] = col[b + t];
+        y[u] = col[base_last + t];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        ok &= x[u] == y[u]; // clamped lanes compare the last entry again
+    }
   }
   if (__builtin_amdgcn_ballot_w64(!ok) != 0 && lane == 0)
     *verdict = 0;

@@ -458,12 +458,15 @@ __global__ __launch_bounds__(64 * W) void spmm_tile_mfma(
   const int nt = std::min(16, rows - r0);
   const int wave = threadIdx.x / kWave;
   const int l = lane_id(), i = l & 15, g = l >> 4;
-  // the row bounds are requested before the structure check waits
+  // the row bounds are requested before the structure check waits; loads
+  // are unconditional from clamped, valid addresses (a guarded load becomes
+  // a branch that waits for it on the spot)
   const int last = r0 + nt - 1;
   const int32_t bl = ro[last];
   const int32_t len_last = ro[last + 1] - bl;
-  const int32_t ra = i < nt ? ro[r0 + i] : 0;
-  const int32_t la = i < nt ? ro[r0 + i + 1] - ra : 0;
+  const int ic = i < nt ? i : nt - 1;
+  const int32_t ra = ro[r0 + ic];
+  const int32_t la = i < nt ? ro[r0 + ic + 1] - ra : 0;
   __shared__ int verdict;
   if (!tile_prefix_ok_block(ro, col, r0, nt, &verdict)) {
     for (int r = r0 + wave; r < r0 + nt; r += W)
@@ -484,8 +487,12 @@ __global__ __launch_bounds__(64 * W) void spmm_tile_mfma(
 #pragma unroll
         for (int st = 0; st < 4; ++st) {
           const int32_t t = t0 + 16 * h + 4 * g + st;
-          a[h][st] = t < la ? val[ra + t] : 0.0f;
-          c[h][st] = t < len_last ? (int64_t)col[bl + t] : -1;
+          const int32_t tc = std::min(t, len_last - 1); // len_last > 0 here
+          // rows shorter than t read the last row's entry, then drop it
+          const float x = val[t < la ? ra + t : bl + tc];
+          const int32_t cx = col[bl + tc];
+          a[h][st] = t < la ? x : 0.0f;
+          c[h][st] = t < len_last ? (int64_t)cx : -1;
         }
       float bv[CH][4][4];
 #pragma unroll
@@ -493,10 +500,15 @@ __global__ __launch_bounds__(64 * W) void spmm_tile_mfma(
 #pragma unroll
         for (int n = 0; n < 4; ++n)
 #pragma unroll
-          for (int st = 0; st < 4; ++st)
-            bv[h][n][st] = (n < ntiles && c[h][st] >= 0)
-                               ? rhs[c[h][st] * k + nb + 16 * n + i]
-                               : 0.0f;
+          for (int st = 0; st < 4; ++st) {
+            const bool in = n < ntiles && c[h][st] >= 0;
+            const float x =
+                rhs[(in ? c[h][st] : 0) * k + nb + 16 * (in ? n : 0) + i];
+            bv[h][n][st] = in ? x : 0.0f;
+          }
+      // keep the step's loads ahead of its MFMAs (left alone, the compiler
+      // interleaves load, wait, MFMA)
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int h = 0; h < CH; ++h)
 #pragma unroll
