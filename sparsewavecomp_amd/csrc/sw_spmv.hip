@@ -18,6 +18,38 @@ using namespace swd;
 namespace {
 
 // ---------------------------------------------------------------------------
+// sum of val[p] * x[col[p]] over p = p0, p0+stride, ... < e, added to acc in
+// position order, with kRowUnroll positions' loads and gathers in flight per
+// step (a loop that loads, gathers and multiplies one position at a time
+// waits a full memory trip per position).
+constexpr int kRowUnroll = 4;
+
+__device__ __forceinline__ float strided_dot(const int32_t *__restrict__ col,
+                                             const float *__restrict__ val,
+                                             const float *__restrict__ x,
+                                             int32_t p, int32_t e,
+                                             int32_t stride, float acc) {
+  for (; p + (kRowUnroll - 1) * stride < e; p += kRowUnroll * stride) {
+    int32_t c[kRowUnroll];
+    float v[kRowUnroll], xv[kRowUnroll];
+#pragma unroll
+    for (int u = 0; u < kRowUnroll; ++u) {
+      c[u] = ld_stream(col + p + u * stride);
+      v[u] = ld_stream(val + p + u * stride);
+    }
+#pragma unroll
+    for (int u = 0; u < kRowUnroll; ++u)
+      xv[u] = x[c[u]];
+#pragma unroll
+    for (int u = 0; u < kRowUnroll; ++u)
+      acc = __builtin_fmaf(v[u], xv[u], acc);
+  }
+  for (; p < e; p += stride)
+    acc = __builtin_fmaf(ld_stream(val + p), x[ld_stream(col + p)], acc);
+  return acc;
+}
+
+// ---------------------------------------------------------------------------
 // thread-per-row: one thread accumulates one row sequentially from zero.
 __global__ __launch_bounds__(1024) void spmv_thread_per_row(
     const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
@@ -27,10 +59,7 @@ __global__ __launch_bounds__(1024) void spmv_thread_per_row(
   if (r >= rows)
     return;
   int32_t s = ro[r], e = ro[r + 1];
-  float acc = 0.0f;
-  for (int32_t p = s; p < e; ++p)
-    acc = __builtin_fmaf(ld_stream(val + p), x[ld_stream(col + p)], acc);
-  y[r] = acc;
+  y[r] = strided_dot(col, val, x, s, e, 1, 0.0f);
 }
 
 // ---------------------------------------------------------------------------
@@ -48,18 +77,7 @@ __global__ __launch_bounds__(1024) void spmv_group_per_row(
   float acc = 0.0f;
   if (r < rows) {
     int32_t s = ro[r], e = ro[r + 1];
-    int32_t p = s + gl;
-    // two independent accumulators keep two gathers in flight per lane
-    float acc2 = 0.0f;
-    for (; p + G < e; p += 2 * G) {
-      int32_t c0 = ld_stream(col + p), c1 = ld_stream(col + p + G);
-      float v0 = ld_stream(val + p), v1 = ld_stream(val + p + G);
-      acc = __builtin_fmaf(v0, x[c0], acc);
-      acc2 = __builtin_fmaf(v1, x[c1], acc2);
-    }
-    if (p < e)
-      acc = __builtin_fmaf(ld_stream(val + p), x[ld_stream(col + p)], acc);
-    acc += acc2;
+    acc = strided_dot(col, val, x, s + gl, e, G, 0.0f);
   }
   // every lane of the wave takes part in the butterfly
   acc = group_sum<G>(acc);
@@ -81,8 +99,7 @@ __global__ __launch_bounds__(1024) void spmv_block_per_row(
   float acc = 0.0f;
   if (r < rows) {
     int32_t s = ro[r], e = ro[r + 1];
-    for (int32_t p = s + t; p < e; p += B)
-      acc = __builtin_fmaf(ld_stream(val + p), x[ld_stream(col + p)], acc);
+    acc = strided_dot(col, val, x, s + t, e, B, 0.0f);
   }
   // blockDim.x is a multiple of 64 (validated), so every wave is full
   float w = wave_sum(acc);
