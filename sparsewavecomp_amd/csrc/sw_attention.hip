@@ -76,7 +76,20 @@ __global__ __launch_bounds__(1024) void sddmm_thread_per_row(
   for (int32_t p = ro[r]; p < ro[r + 1]; ++p) {
     int64_t c = col[p];
     float dot = 0.0f;
-    for (int32_t i = 0; i < kdim; ++i)
+    int32_t i = 0;
+    // four terms' loads in flight, added in order
+    for (; i + 3 < kdim; i += 4) {
+      float av[4], bv[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        av[u] = a[i + u];
+        bv[u] = rhs[(int64_t)(i + u) * cols + c];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        dot = __builtin_fmaf(av[u], bv[u], dot);
+    }
+    for (; i < kdim; ++i)
       dot = __builtin_fmaf(a[i], rhs[(int64_t)i * cols + c], dot);
     out[p] = combine_sddmm(kind, val != nullptr ? val[p] : 0.0f, dot, alpha,
                            beta);
@@ -252,7 +265,19 @@ __global__ __launch_bounds__(1024) void row_reduce_thread(
   if (r >= rows)
     return;
   float acc = MAX ? -INFINITY : 0.0f;
-  for (int32_t p = ro[r]; p < ro[r + 1]; ++p)
+  const int32_t e = ro[r + 1];
+  int32_t p = ro[r];
+  // four loads in flight, combined in position order
+  for (; p + 3 < e; p += 4) {
+    float v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      v[u] = val[p + u];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      acc = MAX ? maximumf(acc, v[u]) : acc + v[u];
+  }
+  for (; p < e; ++p)
     acc = MAX ? maximumf(acc, val[p]) : acc + val[p];
   out[r] = acc;
 }

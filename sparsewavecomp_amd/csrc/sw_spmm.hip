@@ -28,7 +28,25 @@ __global__ __launch_bounds__(1024) void spmm_thread_per_output(
   int64_t r = e / k, c = e - r * k;
   int32_t s = ro[r], t = ro[r + 1];
   float acc = 0.0f;
-  for (int32_t p = s; p < t; ++p)
+  int32_t p = s;
+  // four positions' loads and rhs gathers in flight, products added in
+  // position order
+  for (; p + 3 < t; p += 4) {
+    float v[4], b[4];
+    int64_t cc[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      v[u] = val[p + u];
+      cc[u] = col[p + u];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      b[u] = rhs[cc[u] * k + c];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      acc = __builtin_fmaf(v[u], b[u], acc);
+  }
+  for (; p < t; ++p)
     acc = __builtin_fmaf(val[p], rhs[(int64_t)col[p] * k + c], acc);
   out[e] = acc;
 }
