@@ -412,8 +412,8 @@ __global__ __launch_bounds__(1024) void coo_thread_per_nonzero(
     float *__restrict__ y, int64_t nnz) {
   const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (p < nnz)
-    unsafeAtomicAdd(y + ld_stream(ri + p),
-                    ld_stream(val + p) * x[ld_stream(col + p)]);
+    unsafeAtomicAdd(y + ld_nontemporal(ri + p),
+                    ld_nontemporal(val + p) * x[ld_nontemporal(col + p)]);
 }
 
 // Run-segmented COO (Wave64 extension, taken under the position mapping):
@@ -446,9 +446,9 @@ __global__ __launch_bounds__(1024) void coo_run_segmented(
     if (full) {
 #pragma unroll
       for (int q = 0; q < P; q += 4) {
-        v4i r = ld_stream(reinterpret_cast<const v4i *>(ri + p0 + q));
-        v4i c = ld_stream(reinterpret_cast<const v4i *>(col + p0 + q));
-        v4f v = ld_stream(reinterpret_cast<const v4f *>(val + p0 + q));
+        v4i r = ld_nontemporal(reinterpret_cast<const v4i *>(ri + p0 + q));
+        v4i c = ld_nontemporal(reinterpret_cast<const v4i *>(col + p0 + q));
+        v4f v = ld_nontemporal(reinterpret_cast<const v4f *>(val + p0 + q));
         rr[q + 0] = r.x;
         rr[q + 1] = r.y;
         rr[q + 2] = r.z;
@@ -464,8 +464,9 @@ __global__ __launch_bounds__(1024) void coo_run_segmented(
 #pragma unroll
     for (int q = 0; q < P; ++q)
       if (q < n) {
-        rr[q] = ld_stream(ri + p0 + q);
-        prod[q] = ld_stream(val + p0 + q) * x[ld_stream(col + p0 + q)];
+        rr[q] = ld_nontemporal(ri + p0 + q);
+        prod[q] =
+            ld_nontemporal(val + p0 + q) * x[ld_nontemporal(col + p0 + q)];
       }
   }
   int hk = -1, tk = -1, closed = 0;
