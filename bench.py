@@ -70,8 +70,10 @@ def parse():
     return ap.parse_args()
 
 
-HEADLINE_SPMV = ("spmv-mapping=wave-per-position spmv-positions-per-lane=4 "
+HEADLINE_SPMV = ("spmv-mapping=wave-per-position spmv-positions-per-lane=8 "
                  "spmv-block-size=64")
+HEADLINE_COO = ("spmv-mapping=wave-per-position spmv-positions-per-lane=4 "
+                "spmv-block-size=64")
 COPY_BYTES = 256 << 20
 
 
@@ -104,7 +106,7 @@ def profile(args):
             for _ in range(n):
                 sw.spmv(ro, col, val, xv, y, options=o)
         elif w == "coo":
-            o = sw.Options.parse(args.opts or HEADLINE_SPMV)
+            o = sw.Options.parse(args.opts or HEADLINE_COO)
             ri = T(np.repeat(np.arange(csr.rows, dtype=np.int32),
                              np.diff(csr.row_offsets)))
             xv, y = T(x), torch.empty(csr.rows, device=dev)
@@ -223,7 +225,7 @@ def main():
     spmv_flops = 2 * nnz
     mappings = [
         HEADLINE_SPMV,
-        "spmv-mapping=wave-per-position spmv-positions-per-lane=8 "
+        "spmv-mapping=wave-per-position spmv-positions-per-lane=4 "
         "spmv-block-size=64",
         "spmv-mapping=wave-per-position spmv-positions-per-lane=8 "
         "spmv-block-size=128",
@@ -276,7 +278,7 @@ def main():
         ri = T(np.repeat(np.arange(n, dtype=np.int32),
                          np.diff(csr.row_offsets)))
         coo_bytes = 12 * nnz + 4 * m + 4 * n
-        for opts in ["", HEADLINE_SPMV]:
+        for opts in ["", HEADLINE_COO]:
             o = sw.Options.parse(opts)
             log(f"COO SpMV '{opts}'")
             ms = time_steps(lambda: sw.coo_spmv(ri, col, val, xv, y,

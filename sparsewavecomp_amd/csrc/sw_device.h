@@ -2,8 +2,9 @@
 //
 // Cross-lane work uses DPP (row_shr, quad_perm, row_mirror, row_bcast) and
 // ds_swizzle, which move data through the VALU without LDS memory, and
-// v_readlane for wave-uniform results.  Streaming CSR arrays are read with
-// non-temporal loads so they do not evict the gathered vector from L2.
+// v_readlane for wave-uniform results.  Streaming CSR and BSR arrays are
+// read with plain loads (ld_stream); only COO SpMV uses the non-temporal
+// hint, the one kernel it measured faster for.
 #pragma once
 
 #include <hip/hip_runtime.h>

@@ -236,7 +236,7 @@ __global__ __launch_bounds__(1024) void spmv_thread_position_segmented(
 // and lane l the unit begin+l.  The wave finds the rows of its first and last
 // position with wave-uniform searches (scalar loads), each lane then finds the row of
 // its first position inside that narrow range, walks its P positions
-// (col/val read with 128-bit non-temporal loads when P >= 4) and
+// (col/val read with 128-bit loads when P >= 4) and
 //   - stores rows that start and end inside the lane directly,
 //   - keeps the partial of its first row (head) and of its last row (tail).
 // One segmented scan over the tails joins rows that continue across lanes;
