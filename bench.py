@@ -58,8 +58,8 @@ def parse():
                          "Market / SWCSR001 / SWCOO001 file (the reference "
                          "harness's SuiteSparse workloads)")
     ap.add_argument("--profile", default="",
-                    choices=["", "spmv", "coo", "spmm", "bsr", "bsr-bf16",
-                             "attention", "copy"],
+                    choices=["", "spmv", "floor", "coo", "spmm", "bsr",
+                             "bsr-bf16", "attention", "copy"],
                     help="run one workload --steps times with no timing or "
                          "JSON (for rocprofv3 kernel-trace / pmc runs)")
     ap.add_argument("--opts", default="",
@@ -100,7 +100,7 @@ def profile(args):
         dst = torch.empty_like(src)
         for _ in range(n):
             dst.copy_(src)
-    elif w in ("spmv", "coo", "spmm"):
+    elif w in ("spmv", "floor", "coo", "spmm"):
         csr, x = W.config2(seed=0)
         ro, col, val = T(csr.row_offsets), T(csr.column_indices), T(csr.values)
         if w == "spmv":
@@ -108,6 +108,11 @@ def profile(args):
             xv, y = T(x), torch.empty(csr.rows, device=dev)
             for _ in range(n):
                 sw.spmv(ro, col, val, xv, y, options=o)
+        elif w == "floor":
+            xv = T(x)
+            part = torch.empty((csr.nnz + 511) // 512, device=dev)
+            for _ in range(n):
+                sw.spmv_gather_floor(col, val, xv, part)
         elif w == "coo":
             o = sw.Options.parse(args.opts or HEADLINE_COO)
             ri = T(np.repeat(np.arange(csr.rows, dtype=np.int32),
@@ -261,8 +266,20 @@ def main():
             "hbm_frac": spmv_bytes / ms / 1e6 / HBM_PEAK_GBS}
         log(f"  {ms * 1e3:.1f} us  {spmv_bytes / ms / 1e6:.0f} GB/s")
     best = min(spmv_results, key=lambda k: spmv_results[k]["ms"])
-    workloads["spmv_config2"] = {"bytes": spmv_bytes, "flops": spmv_flops,
-                                 "best": best, "mappings": spmv_results}
+    # the gather floor on the same buffers: column/value reads and x gathers
+    # with no row structure, the part no SpMV schedule avoids
+    part = torch.empty((nnz + 511) // 512, device=dev)
+    log("gather floor")
+    floor_ms = time_steps(lambda: sw.spmv_gather_floor(col, val, xv, part),
+                          K, Wm)
+    log(f"  {floor_ms * 1e3:.1f} us")
+    del part
+    workloads["spmv_config2"] = {
+        "bytes": spmv_bytes, "flops": spmv_flops, "best": best,
+        "mappings": spmv_results,
+        "gather_floor": {"ms": floor_ms,
+                         "best_mapping_frac": floor_ms /
+                         spmv_results[best]["ms"]}}
 
     # rocSPARSE on the same buffers (compute stage only; its analysis /
     # preprocess stage runs once, outside the timed region)
@@ -470,6 +487,9 @@ def main():
             "rows": n, "nnz": nnz, "mapping": best,
             "GFLOP/s": round(head["GFLOP/s"], 2),
             "hbm_frac": round(head["hbm_frac"], 4),
+            "gather_floor_frac": round(
+                workloads["spmv_config2"]["gather_floor"]["best_mapping_frac"],
+                3),
             "vs_rocsparse": (round(min(v["ms"] for k2, v in rocsparse.items()
                                        if k2.startswith("spmv_"))
                                    / head["ms"], 3)

@@ -143,6 +143,19 @@ int sw_spmv_coo_f32(const int32_t *row_indices, const int32_t *column_indices,
                     const sw_options *opts, void *stream);
 
 /*
+ * Gather floor, a diagnostic with no counterpart in the reference: reads
+ * column_indices[nnz] and values[nnz] once and gathers vector[col] once per
+ * entry, with no row structure, and writes
+ * partial[w] = sum of values[p] * vector[column_indices[p]] over
+ * p in [512 w, 512 w + 512) for w < ceil(nnz / 512).  Its time is the floor
+ * under any CSR SpMV schedule that reads each nonzero and gathers x once;
+ * bench.py reports the headline SpMV against it.
+ */
+int sw_spmv_gather_floor_f32(const int32_t *column_indices,
+                             const float *values, const float *vector,
+                             float *partial, int64_t nnz, void *stream);
+
+/*
  * sparsewave.spmm: output[rows][k] = A * rhs[cols][k], dense matrices
  * row-major.  Operand order and the 5-buffer bundle ABI of
  * SparseWaveOps.td:91-124 / tools/sparsewave-bundle/sparsewave_bundle_ir.py:11-17.

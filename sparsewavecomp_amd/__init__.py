@@ -17,7 +17,7 @@ import os
 
 __all__ = [
     "Options", "SparseWaveError", "library_path", "load_library", "spmv",
-    "coo_spmv",
+    "coo_spmv", "spmv_gather_floor",
     "spmm", "bsr_spmm", "sddmm", "csr_row_reduce", "csr_rowwise_map",
     "sparse_attention", "csr_row_at_position", "SDDMM_MUL", "SDDMM_AFFINE",
     "SDDMM_DOT", "MAP_EXP_SUB", "MAP_DIV", "MAP_SUB", "MAP_MUL",
@@ -33,7 +33,7 @@ MAP_EXP_SUB, MAP_DIV, MAP_SUB, MAP_MUL = 0, 1, 2, 3
 EXPORTED_SYMBOLS = (
     "sw_options_init", "sw_options_set", "sw_options_parse",
     "sw_validate_options", "sw_last_error", "sw_version", "sw_spmv_csr_f32",
-    "sw_spmv_coo_f32",
+    "sw_spmv_coo_f32", "sw_spmv_gather_floor_f32",
     "sw_spmm_csr_f32", "sw_bsr_spmm_f32", "sw_bsr_spmm_bf16",
     "sw_sddmm_csr_f32", "sw_csr_row_reduce_f32", "sw_csr_rowwise_map_f32",
     "sw_sparse_attention_f32", "sw_csr_row_at_position",
@@ -111,6 +111,7 @@ def load_library():
                                            P]),
         "sw_spmv_coo_f32": (ctypes.c_int, [P, P, P, P, P, I64, I64, I64, OP,
                                            P]),
+        "sw_spmv_gather_floor_f32": (ctypes.c_int, [P, P, P, P, I64, P]),
         "sw_spmm_csr_f32": (ctypes.c_int, [P, P, P, P, P, I64, I64, I64, I64,
                                            OP, P]),
         "sw_bsr_spmm_f32": (ctypes.c_int, [P, P, P, P, P, I64, I64, I64, I64,
@@ -248,6 +249,25 @@ def coo_spmv(row_indices, column_indices, values, vector, output,
         _dev(output, torch.float32, "output"), output.numel(), vector.numel(),
         values.numel(), _opts(options), _stream(stream)))
     return output
+
+
+def spmv_gather_floor(column_indices, values, vector, partial, stream=None):
+    """Diagnostic (no reference counterpart): partial[w] = sum of
+    values[p] * vector[column_indices[p]] over p in [512 w, 512 w + 512),
+    i.e. a CSR SpMV's column/value reads and x gathers without its rows."""
+    import torch
+    nnz = values.numel()
+    if column_indices.numel() != nnz:
+        raise SparseWaveError(-2, "column indices and values must have the "
+                                  "same length")
+    if partial.numel() < (nnz + 511) // 512:
+        raise SparseWaveError(-2, "partial needs ceil(nnz / 512) entries")
+    _check(load_library().sw_spmv_gather_floor_f32(
+        _dev(column_indices, torch.int32, "column_indices"),
+        _dev(values, torch.float32, "values"),
+        _dev(vector, torch.float32, "vector"),
+        _dev(partial, torch.float32, "partial"), nnz, _stream(stream)))
+    return partial
 
 
 def spmm(row_offsets, column_indices, values, rhs, output, options=None,

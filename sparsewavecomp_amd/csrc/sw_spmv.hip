@@ -388,6 +388,41 @@ __global__ __launch_bounds__(1024) void spmv_wave_position(
 }
 
 // ---------------------------------------------------------------------------
+// Gather floor (a diagnostic with no reference counterpart): the part of a
+// CSR SpMV that no row schedule avoids -- every column index and value read
+// once with 128-bit loads and every x[col] gathered once -- without the row
+// structure.  Lane l of wave w owns positions [8u, 8u + 8), u = 64w + l, and
+// each wave writes the sum of its products to partial[w].  Its time bounds
+// any SpMV schedule that reads col/val and gathers x once per nonzero.
+constexpr int kFloorUnit = 8;
+
+__global__ __launch_bounds__(64) void spmv_gather_floor(
+    const int32_t *__restrict__ col, const float *__restrict__ val,
+    const float *__restrict__ x, float *__restrict__ partial, int64_t nnz,
+    bool vec) {
+  const int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t p0 = u * kFloorUnit;
+  float acc = 0.0f;
+  if (vec && p0 + kFloorUnit <= nnz) {
+#pragma unroll
+    for (int q = 0; q < kFloorUnit; q += 4) {
+      const v4i c = ld_stream(reinterpret_cast<const v4i *>(col + p0 + q));
+      const v4f v = ld_stream(reinterpret_cast<const v4f *>(val + p0 + q));
+      acc = __builtin_fmaf(v.x, x[c.x], acc);
+      acc = __builtin_fmaf(v.y, x[c.y], acc);
+      acc = __builtin_fmaf(v.z, x[c.z], acc);
+      acc = __builtin_fmaf(v.w, x[c.w], acc);
+    }
+  } else {
+    for (int64_t p = p0; p < p0 + kFloorUnit && p < nnz; ++p)
+      acc = __builtin_fmaf(val[p], x[col[p]], acc);
+  }
+  acc = group_sum<kWave>(acc);
+  if (threadIdx.x == 0)
+    partial[blockIdx.x] = acc;
+}
+
+// ---------------------------------------------------------------------------
 // batch row recovery (sw_csr_row_at_position)
 __global__ __launch_bounds__(256) void csr_row_at_position_kernel(
     const int32_t *__restrict__ ro, int32_t rows,
@@ -730,6 +765,29 @@ extern "C" int sw_spmv_csr_f32(const int32_t *row_offsets,
     return sw::fail(SW_ERR_INVALID_ARGUMENT, "vector or output pointer is null");
   return sw::launch_spmv(row_offsets, column_indices, values, vector, output,
                          rows, nnz, o, sw::as_stream(stream));
+}
+
+extern "C" int sw_spmv_gather_floor_f32(const int32_t *column_indices,
+                                        const float *values,
+                                        const float *vector, float *partial,
+                                        int64_t nnz, void *stream) {
+  sw::clear_error();
+  if (nnz < 0)
+    return sw::fail(SW_ERR_INVALID_SHAPE, "expected non-negative nnz");
+  if (nnz == 0)
+    return SW_OK;
+  if (!column_indices || !values || !vector || !partial)
+    return sw::fail(SW_ERR_INVALID_ARGUMENT,
+                    "column index, value, vector or partial pointer is null");
+  const int64_t grid = sw::ceil_div(sw::ceil_div(nnz, kFloorUnit), kWave);
+  int rc = sw::check_grid(grid, "gather floor");
+  if (rc)
+    return rc;
+  const bool vec = sw::aligned16(column_indices) && sw::aligned16(values);
+  hipLaunchKernelGGL(spmv_gather_floor, dim3((unsigned)grid), dim3(kWave), 0,
+                     sw::as_stream(stream), column_indices, values, vector,
+                     partial, nnz, vec);
+  return sw::launch_check("gather floor kernel");
 }
 
 extern "C" int sw_spmv_coo_f32(const int32_t *row_indices,
