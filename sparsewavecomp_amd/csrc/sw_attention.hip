@@ -396,6 +396,322 @@ __global__ __launch_bounds__(256) void row_softmax_wave(
   }
 }
 
+// Row r of the attention output computed by one wave from the row's
+// normalised scores (the fused kernel's per-row path): lanes over the output
+// columns, sequential over the row's positions.
+__device__ __forceinline__ void attention_row_output(
+    const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
+    const float *scores, const float *__restrict__ value,
+    float *__restrict__ out, int64_t r, int64_t dv) {
+  const int32_t s = ro[r], e = ro[r + 1];
+  for (int64_t c = lane_id(); c < dv; c += kWave) {
+    float acc = 0.0f;
+    for (int32_t p = s; p < e; ++p)
+      acc = __builtin_fmaf(scores[p], value[(int64_t)col[p] * dv + c], acc);
+    out[r * dv + c] = acc;
+  }
+}
+
+// One row's softmax in global memory by one wave (the fused kernel's
+// per-row path): the long-row branch of row_softmax_wave.
+__device__ __forceinline__ void attention_row_softmax(
+    const int32_t *__restrict__ ro, float *scores, float *__restrict__ rmax,
+    float *__restrict__ rsum, int64_t r) {
+  const int l = lane_id();
+  const int32_t s = ro[r], e = ro[r + 1];
+  float m = -INFINITY, sum = 0.0f;
+  for (int32_t p = s + l; p < e; p += kWave)
+    m = maximumf(m, scores[p]);
+  m = wave_max(m);
+  for (int32_t p = s + l; p < e; p += kWave) {
+    const float v = expf(scores[p] - m);
+    scores[p] = v;
+    sum += v;
+  }
+  sum = group_sum<kWave>(sum);
+  for (int32_t p = s + l; p < e; p += kWave)
+    scores[p] = scores[p] / sum;
+  if (l == 0) {
+    rmax[r] = m;
+    rsum[r] = sum;
+  }
+}
+
+// The attention chain fused over 16-row tiles (d = 64 * KB, dv % 16 == 0):
+// scores = alpha * Q K^T + beta * mask on the mask's positions, the row
+// softmax (rowMaximum, rowSum and the normalised scores written as the
+// separate ops write them), and output = P V, in one kernel.  A tile whose
+// rows share the last row's column structure (tile_prefix_ok_block) and
+// whose last row holds at most kFusedCols entries keeps its scores in LDS:
+//   A. the SDDMM of sddmm_tile_mfma (16 x 16 x d MFMA products, wave w
+//      taking the column chunks w, w+W, ...) writes raw scores to LDS;
+//   B. wave w normalises rows w, w+W, ... in LDS and writes each final
+//      score, its row maximum and its row sum once;
+//   C. the SpMM of spmm_tile_mfma reads the tile's probabilities from LDS
+//      (lane (i, g) takes P[i][t0+4g+s]) against the gathered V rows, and
+//      the waves' partial output tiles are summed through LDS.
+// The scores thus cross HBM once (written) instead of five times, and the
+// chain is one launch.  Other tiles run row by row: each wave computes a row's
+// scores, softmax and output in global memory.
+constexpr int kFusedCols = 512;
+constexpr int kFusedStride = kFusedCols + 4; // LDS row pitch (bank spread)
+constexpr int kFusedWaves = 8;
+
+template <int KB, int W>
+__global__ __launch_bounds__(64 * W) void attention_tile_fused(
+    const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
+    const float *__restrict__ mask, const float *__restrict__ q,
+    const float *__restrict__ kt, const float *__restrict__ value,
+    float *scores, float *__restrict__ rmax, float *__restrict__ rsum,
+    float *__restrict__ out, int32_t rows, int64_t cols, int32_t kdim,
+    int64_t dv, float alpha, float beta) {
+  __shared__ float sc[16 * kFusedStride];
+  __shared__ float part[W][4][4][kWave]; // [wave][n tile][v][lane]
+  __shared__ int32_t lcol[kFusedCols];   // the last row's columns
+  __shared__ int verdict;
+  const int r0 = blockIdx.x * 16;
+  const int nt = std::min(16, rows - r0);
+  const int wave = threadIdx.x / kWave;
+  const int l = lane_id(), i = l & 15, g = l >> 4;
+  // loads are unconditional from clamped, valid addresses, their values
+  // selected afterwards (a guarded load becomes a branch that waits for it
+  // on the spot)
+  int32_t rb[4], rl[4];
+  {
+    int32_t b[5];
+#pragma unroll
+    for (int v = 0; v < 5; ++v)
+      b[v] = ro[std::min(r0 + 4 * g + v, rows)];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      rb[v] = b[v];
+      rl[v] = 4 * g + v < nt ? b[v + 1] - b[v] : 0;
+    }
+  }
+  const int ic = i < nt ? i : nt - 1;
+  const int32_t la = i < nt ? ro[r0 + ic + 1] - ro[r0 + ic] : 0;
+  float qa[16 * KB];
+  const int64_t qrow = (int64_t)std::min(r0 + i, rows - 1) * kdim;
+#pragma unroll
+  for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+    for (int st = 0; st < 16; ++st) {
+      const float x = q[qrow + kb * 64 + 16 * g + st];
+      qa[kb * 16 + st] = i < nt ? x : 0.0f;
+    }
+  const int last = r0 + nt - 1;
+  const int32_t bl = ro[last];
+  const int32_t len_last = ro[last + 1] - bl;
+  // The last row's column indices are staged once in LDS: the structure
+  // check compares against them, and both products gather their K / V rows
+  // without waiting for a column load first.  The check itself: wave w
+  // compares rows w and w + W (at most two, nt <= 16 = 2W) with one batch of
+  // loads, since a row of at most kFusedCols entries is 8 loads per lane.
+  static_assert(2 * W >= 16 && kFusedCols == 8 * kWave, "check layout");
+  bool ok = len_last <= kFusedCols; // workgroup-uniform
+  if (ok) {
+    for (int t = threadIdx.x; t < len_last; t += 64 * W)
+      lcol[t] = col[bl + t];
+    if (threadIdx.x == 0)
+      verdict = 1;
+    __syncthreads();
+    const int32_t my_ro = ro[r0 + (l < nt ? l : nt)];
+    bool mine = true;
+    int32_t x[2][8];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int rr = wave + h * W;
+      const int rc = rr < nt - 1 ? rr : 0; // rows past nt-2 are not checked
+      const int32_t b = __builtin_amdgcn_readlane(my_ro, rc);
+      const int32_t len = __builtin_amdgcn_readlane(my_ro, rc + 1) - b;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int32_t t = l + u * kWave;
+        // unconditional loads from clamped, valid positions (nnz > 0)
+        x[h][u] = col[len > 0 ? b + std::min(t, len - 1) : 0];
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int rr = wave + h * W;
+      if (rr < nt - 1) { // wave-uniform
+        const int32_t b = __builtin_amdgcn_readlane(my_ro, rr);
+        const int32_t len = __builtin_amdgcn_readlane(my_ro, rr + 1) - b;
+        mine &= len <= len_last;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int32_t t = l + u * kWave;
+          if (t < len && t < len_last)
+            mine &= x[h][u] == lcol[t];
+        }
+      }
+    }
+    if (__builtin_amdgcn_ballot_w64(!mine) != 0 && l == 0)
+      verdict = 0;
+    __syncthreads();
+    ok = verdict != 0;
+  }
+  if (!ok) { // workgroup-uniform
+    for (int r = r0 + wave; r < r0 + nt; r += W) {
+      sddmm_row_wave(ro, col, mask, q, kt, scores, r, cols, kdim,
+                     SW_SDDMM_AFFINE, alpha, beta);
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+      attention_row_softmax(ro, scores, rmax, rsum, r);
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+      attention_row_output(ro, col, scores, value, out, r, dv);
+    }
+    return;
+  }
+  // A. raw scores into LDS, two column chunks per iteration (W chunks apart)
+  for (int32_t t0 = wave * 16; t0 < len_last; t0 += 32 * W) {
+    const int32_t t1 = t0 + 16 * W;
+    const bool two = t1 < len_last; // wave-uniform
+    const int32_t ta = t0 + i, tb = t1 + i;
+    const int64_t cj0 = lcol[std::min(ta, len_last - 1)];
+    const int64_t cj1 = lcol[std::min(two ? tb : ta, len_last - 1)];
+    float s0[4], s1[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      // position bl is inside the last row, always a valid index
+      const bool in0 = mask != nullptr && ta < rl[v];
+      const bool in1 = mask != nullptr && two && tb < rl[v];
+      const float x0 = mask != nullptr ? mask[in0 ? rb[v] + ta : bl] : 0.0f;
+      const float x1 = mask != nullptr ? mask[in1 ? rb[v] + tb : bl] : 0.0f;
+      s0[v] = in0 ? x0 : 0.0f;
+      s1[v] = in1 ? x1 : 0.0f;
+    }
+    v4f acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+      float bv0[16], bv1[16];
+#pragma unroll
+      for (int st = 0; st < 16; ++st) {
+        const float *krow = kt + (int64_t)(kb * 64 + 16 * g + st) * cols;
+        bv0[st] = krow[cj0];
+        bv1[st] = krow[cj1];
+      }
+#pragma unroll
+      for (int st = 0; st < 16; ++st) {
+        acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[kb * 16 + st], bv0[st],
+                                                    acc0, 0, 0, 0);
+        if (two)
+          acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[kb * 16 + st],
+                                                      bv1[st], acc1, 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      float *srow = sc + (4 * g + v) * kFusedStride;
+      if (ta < rl[v])
+        srow[ta] = combine_sddmm(SW_SDDMM_AFFINE, s0[v], acc0[v], alpha, beta);
+      if (two && tb < rl[v])
+        srow[tb] = combine_sddmm(SW_SDDMM_AFFINE, s1[v], acc1[v], alpha, beta);
+    }
+  }
+  __syncthreads();
+  // C's V rows, 16 stored entries (four MFMA steps) per chunk and two chunks
+  // per step: lane (j, g) takes V[c_t][nb + 16n + j], t = t0 + 16h + 4g + s
+  constexpr int CH = 2;
+  auto load_v = [&](int32_t t0, int64_t nb, float (&bv)[CH][4][4])
+      __attribute__((always_inline)) {
+    const int ntiles = (int)std::min<int64_t>(4, (dv - nb) / 16);
+#pragma unroll
+    for (int h = 0; h < CH; ++h)
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        const int32_t t = t0 + 16 * h + 4 * g + st;
+        const int64_t c = lcol[std::min(t, len_last - 1)];
+#pragma unroll
+        for (int n = 0; n < 4; ++n) {
+          const bool in = n < ntiles && t < len_last;
+          const float x = value[(in ? c : 0) * dv + nb + 16 * (in ? n : 0) + i];
+          bv[h][n][st] = in ? x : 0.0f;
+        }
+      }
+  };
+  // B. row softmax in LDS; each final score is written to HBM once
+  for (int rr = wave; rr < nt; rr += W) {
+    const int32_t s = ro[r0 + rr], len = ro[r0 + rr + 1] - s;
+    float *srow = sc + rr * kFusedStride;
+    float m = -INFINITY, sum = 0.0f;
+    for (int t = l; t < len; t += kWave)
+      m = maximumf(m, srow[t]);
+    m = wave_max(m);
+    for (int t = l; t < len; t += kWave) {
+      const float e = expf(srow[t] - m);
+      srow[t] = e;
+      sum += e;
+    }
+    sum = group_sum<kWave>(sum);
+    for (int t = l; t < len; t += kWave) {
+      const float p = srow[t] / sum;
+      srow[t] = p;
+      scores[s + t] = p;
+    }
+    if (l == 0) {
+      rmax[r0 + rr] = m;
+      rsum[r0 + rr] = sum;
+    }
+  }
+  __syncthreads();
+  // C. output = P V, P from LDS (lane (i, g) takes P[i][t]); the waves'
+  // partial output tiles are summed through LDS
+  const float *prow = sc + i * kFusedStride;
+  auto mfma_step = [&](int32_t t0, const float (&bv)[CH][4][4], v4f (&acc)[4])
+      __attribute__((always_inline)) {
+    float a[CH][4];
+#pragma unroll
+    for (int h = 0; h < CH; ++h)
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        const int32_t t = t0 + 16 * h + 4 * g + st;
+        const float x = prow[std::min(t, kFusedCols - 1)];
+        a[h][st] = t < la ? x : 0.0f;
+      }
+#pragma unroll
+    for (int h = 0; h < CH; ++h)
+#pragma unroll
+      for (int n = 0; n < 4; ++n)
+#pragma unroll
+        for (int st = 0; st < 4; ++st)
+          acc[n] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[h][st], bv[h][n][st],
+                                                        acc[n], 0, 0, 0);
+  };
+  for (int64_t nb = 0; nb < dv; nb += 64) {
+    const int ntiles = (int)std::min<int64_t>(4, (dv - nb) / 16);
+    v4f acc[4];
+#pragma unroll
+    for (int n = 0; n < 4; ++n)
+      acc[n] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int32_t t0 = wave * 16 * CH; t0 < len_last; t0 += W * 16 * CH) {
+      float bv[CH][4][4];
+      load_v(t0, nb, bv);
+      // keep the step's loads ahead of its MFMAs
+      __builtin_amdgcn_sched_barrier(0);
+      mfma_step(t0, bv, acc);
+    }
+#pragma unroll
+    for (int n = 0; n < 4; ++n)
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        part[wave][n][v][l] = acc[n][v];
+    __syncthreads();
+    if (wave < ntiles) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int w = 0; w < W; ++w)
+          sum += part[w][wave][v][l];
+        const int rr = 4 * g + v;
+        if (rr < nt)
+          out[(int64_t)(r0 + rr) * dv + nb + 16 * wave + i] = sum;
+      }
+    }
+    __syncthreads();
+  }
+}
+
 int grid_for(int64_t work, int64_t per_block, const char *what,
              int64_t *grid) {
   *grid = std::max<int64_t>(sw::ceil_div(work, per_block), 1);
@@ -618,6 +934,28 @@ extern "C" int sw_sparse_attention_f32(
       (nnz > 0 && (!scores || !query || !transposed_key || (dv > 0 && !value))))
     return sw::fail(SW_ERR_INVALID_ARGUMENT, "attention buffer pointer is null");
   hipStream_t st = sw::as_stream(stream);
+  if (nnz > 0 && o.sddmm_lanes_per_row == 64 &&
+      sw::streq(o.sddmm_mapping, "row-tile-mfma") &&
+      sw::streq(o.spmm_mapping, "row-tile-mfma") && (d == 64 || d == 128) &&
+      dv > 0 && dv % 16 == 0) {
+    // the whole chain in one kernel per 16-row tile
+    int64_t grid;
+    rc = grid_for(rows, 16, "fused attention", &grid);
+    if (rc)
+      return rc;
+#define SW_FUSED(KB)                                                          \
+  hipLaunchKernelGGL((attention_tile_fused<KB, kFusedWaves>),                 \
+                     dim3((unsigned)grid), dim3(64 * kFusedWaves), 0, st,     \
+                     row_offsets, column_indices, mask_values, query,         \
+                     transposed_key, value, scores, row_maximum, row_sum,     \
+                     output, (int32_t)rows, cols, (int32_t)d, dv, alpha, beta)
+    if (d == 64)
+      SW_FUSED(1);
+    else
+      SW_FUSED(2);
+#undef SW_FUSED
+    return sw::launch_check("fused attention kernel");
+  }
   if (nnz > 0) {
     rc = sw::launch_sddmm(row_offsets, column_indices, mask_values, query,
                           transposed_key, scores, rows, cols, d,

@@ -324,6 +324,66 @@ def test_attention_config5(dev, orc, opts, seq):
     assert math.isfinite(float(out.sum()))
 
 
+FUSED = ("sddmm-mapping=row-tile-mfma sddmm-lanes-per-row=64 "
+         "spmm-mapping=row-tile-mfma")
+
+
+def _long_prefix_csr():
+    """Tiles with the shared (prefix) column structure whose last rows hold
+    700, 512 and 513 entries: the fused kernel keeps at most 512 scores per
+    row in LDS and computes longer tiles row by row."""
+    rng = np.random.default_rng(41)
+    cols = 900
+    rows_cols = []
+    for last in (700, 512, 513):
+        base = np.sort(rng.choice(cols, last, replace=False))
+        lens = np.sort(rng.integers(1, last + 1, 16))
+        lens[-1] = last
+        rows_cols += [base[:n].copy() for n in lens]
+    lengths = np.array([len(c) for c in rows_cols])
+    ro = np.zeros(len(rows_cols) + 1, np.int32)
+    np.cumsum(lengths, out=ro[1:])
+    col = np.concatenate(rows_cols).astype(np.int32)
+    val = rng.uniform(-1, 1, col.size).astype(np.float32)
+    return W.CSR(len(rows_cols), cols, ro, col, val)
+
+
+@pytest.mark.parametrize("shape", ["structure", "long"])
+@pytest.mark.parametrize("d,dv", [(64, 64), (128, 16), (64, 80), (128, 128)])
+def test_attention_fused_paths(dev, orc, shape, d, dv):
+    """The one-kernel attention chain: LDS tiles, the row-by-row path
+    (columns not shared, a row longer than the last, a deep mismatch, rows
+    over 512 entries), empty rows, a partial last tile, d of 64 and 128, dv
+    of one to eight 16-column tiles, and a non-zero mask weight."""
+    csr = _tile_structure_csr() if shape == "structure" else _long_prefix_csr()
+    rng = np.random.default_rng(d + dv)
+    q = rng.standard_normal((csr.rows, d)).astype(np.float32)
+    kt = rng.standard_normal((d, csr.cols)).astype(np.float32)
+    v = rng.standard_normal((csr.cols, dv)).astype(np.float32)
+    alpha, beta = 0.125, 0.5
+    G.say(f"fused attention {shape} rows={csr.rows} nnz={csr.nnz} d={d} "
+          f"dv={dv}")
+    nan = float("nan")
+    scores = torch.full((csr.nnz,), nan, device=G.DEV)
+    rmax = torch.full((csr.rows,), nan, device=G.DEV)
+    rsum = torch.full((csr.rows,), nan, device=G.DEV)
+    out = torch.full((csr.rows, dv), nan, device=G.DEV)
+    sw.sparse_attention(G.t(csr.row_offsets), G.t(csr.column_indices),
+                        G.t(csr.values), G.t(q), G.t(kt), G.t(v), scores,
+                        rmax, rsum, out, alpha, beta, options=FUSED)
+    torch.cuda.synchronize()
+    s_ref, m_ref, sum_ref, ref = orc.sparse_attention(
+        csr.row_offsets, csr.column_indices, csr.values, q, kt, v, alpha,
+        beta)
+    bound = orc.spmm_abs_bound(csr.row_offsets, csr.column_indices, s_ref, v)
+    assert_within_bound(out.cpu().numpy(), ref, bound, rel=2e-5)
+    np.testing.assert_allclose(scores.cpu().numpy(), s_ref, rtol=1e-4,
+                               atol=1e-6)
+    np.testing.assert_allclose(rmax.cpu().numpy(), m_ref, rtol=1e-5,
+                               atol=1e-5)
+    np.testing.assert_allclose(rsum.cpu().numpy(), sum_ref, rtol=1e-4)
+
+
 @pytest.mark.parametrize("kdim", [64, 128, 32])
 def test_sddmm_tile_mfma_block_mask(dev, orc, kdim):
     """Block-structured masks take the 16-row MFMA tiles."""
