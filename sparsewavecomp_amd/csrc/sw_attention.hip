@@ -64,6 +64,8 @@ __device__ __forceinline__ float map_value(int kind, float v, float rv) {
 }
 
 // ---- SDDMM -----------------------------------------------------------------
+constexpr int kSddmmRowPos = 4;
+
 __global__ __launch_bounds__(1024) void sddmm_thread_per_row(
     const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
     const float *__restrict__ val, const float *__restrict__ lhs,
@@ -73,26 +75,47 @@ __global__ __launch_bounds__(1024) void sddmm_thread_per_row(
   if (r >= rows)
     return;
   const float *a = lhs + r * kdim;
-  for (int32_t p = ro[r]; p < ro[r + 1]; ++p) {
-    int64_t c = col[p];
-    float dot = 0.0f;
-    int32_t i = 0;
-    // four terms' loads in flight, added in order
-    for (; i + 3 < kdim; i += 4) {
-      float av[4], bv[4];
+  // kSddmmRowPos positions at a time, sixteen terms of each in flight: the
+  // launch has one thread per row (8192 rows are 128 waves), so a row is a
+  // chain of memory trips and registers are plentiful.  Each position's dot
+  // is still added term by term in order.
+  const int32_t e = ro[r + 1];
+  for (int32_t p = ro[r]; p < e; p += kSddmmRowPos) {
+    int64_t c[kSddmmRowPos];
+    float dot[kSddmmRowPos];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        av[u] = a[i + u];
-        bv[u] = rhs[(int64_t)(i + u) * cols + c];
-      }
-#pragma unroll
-      for (int u = 0; u < 4; ++u)
-        dot = __builtin_fmaf(av[u], bv[u], dot);
+    for (int j = 0; j < kSddmmRowPos; ++j) {
+      c[j] = col[std::min(p + j, e - 1)];
+      dot[j] = 0.0f;
     }
-    for (; i < kdim; ++i)
-      dot = __builtin_fmaf(a[i], rhs[(int64_t)i * cols + c], dot);
-    out[p] = combine_sddmm(kind, val != nullptr ? val[p] : 0.0f, dot, alpha,
-                           beta);
+    int32_t i = 0;
+    for (; i + 15 < kdim; i += 16) {
+      float av[16], bv[kSddmmRowPos][16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u)
+        av[u] = a[i + u];
+#pragma unroll
+      for (int j = 0; j < kSddmmRowPos; ++j)
+#pragma unroll
+        for (int u = 0; u < 16; ++u)
+          bv[j][u] = rhs[(int64_t)(i + u) * cols + c[j]];
+#pragma unroll
+      for (int j = 0; j < kSddmmRowPos; ++j)
+#pragma unroll
+        for (int u = 0; u < 16; ++u)
+          dot[j] = __builtin_fmaf(av[u], bv[j][u], dot[j]);
+    }
+    for (; i < kdim; ++i) {
+      const float av = a[i];
+#pragma unroll
+      for (int j = 0; j < kSddmmRowPos; ++j)
+        dot[j] = __builtin_fmaf(av, rhs[(int64_t)i * cols + c[j]], dot[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < kSddmmRowPos; ++j)
+      if (p + j < e)
+        out[p + j] = combine_sddmm(kind, val != nullptr ? val[p + j] : 0.0f,
+                                   dot[j], alpha, beta);
   }
 }
 

@@ -18,6 +18,11 @@ using namespace swd;
 namespace {
 
 // thread-per-output: one thread per C[r, c], sequential over the row.
+// Products are added in position order with kOutputDeep positions' loads
+// and rhs gathers in flight while that many remain, then four: the kernel's
+// time is the longest rows' chain of memory trips.
+constexpr int kOutputDeep = 16;
+
 __global__ __launch_bounds__(1024) void spmm_thread_per_output(
     const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
     const float *__restrict__ val, const float *__restrict__ rhs,
@@ -29,8 +34,21 @@ __global__ __launch_bounds__(1024) void spmm_thread_per_output(
   int32_t s = ro[r], t = ro[r + 1];
   float acc = 0.0f;
   int32_t p = s;
-  // four positions' loads and rhs gathers in flight, products added in
-  // position order
+  for (; p + kOutputDeep - 1 < t; p += kOutputDeep) {
+    float v[kOutputDeep], b[kOutputDeep];
+    int32_t cc[kOutputDeep];
+#pragma unroll
+    for (int u = 0; u < kOutputDeep; ++u) {
+      v[u] = val[p + u];
+      cc[u] = col[p + u];
+    }
+#pragma unroll
+    for (int u = 0; u < kOutputDeep; ++u)
+      b[u] = rhs[(int64_t)cc[u] * k + c];
+#pragma unroll
+    for (int u = 0; u < kOutputDeep; ++u)
+      acc = __builtin_fmaf(v[u], b[u], acc);
+  }
   for (; p + 3 < t; p += 4) {
     float v[4], b[4];
     int64_t cc[4];

@@ -21,14 +21,34 @@ namespace {
 // sum of val[p] * x[col[p]] over p = p0, p0+stride, ... < e, added to acc in
 // position order, with kRowUnroll positions' loads and gathers in flight per
 // step (a loop that loads, gathers and multiplies one position at a time
-// waits a full memory trip per position).
+// waits a full memory trip per position).  DEEP > 0 first takes steps of
+// DEEP positions while that many remain: a long row handled by one thread
+// then needs DEEP times fewer memory trips.
 constexpr int kRowUnroll = 4;
 
+template <int DEEP = 0>
 __device__ __forceinline__ float strided_dot(const int32_t *__restrict__ col,
                                              const float *__restrict__ val,
                                              const float *__restrict__ x,
                                              int32_t p, int32_t e,
                                              int32_t stride, float acc) {
+  if constexpr (DEEP > 0) {
+    for (; p + (DEEP - 1) * stride < e; p += DEEP * stride) {
+      int32_t c[DEEP];
+      float v[DEEP], xv[DEEP];
+#pragma unroll
+      for (int u = 0; u < DEEP; ++u) {
+        c[u] = ld_stream(col + p + u * stride);
+        v[u] = ld_stream(val + p + u * stride);
+      }
+#pragma unroll
+      for (int u = 0; u < DEEP; ++u)
+        xv[u] = x[c[u]];
+#pragma unroll
+      for (int u = 0; u < DEEP; ++u)
+        acc = __builtin_fmaf(v[u], xv[u], acc);
+    }
+  }
   for (; p + (kRowUnroll - 1) * stride < e; p += kRowUnroll * stride) {
     int32_t c[kRowUnroll];
     float v[kRowUnroll], xv[kRowUnroll];
@@ -51,6 +71,9 @@ __device__ __forceinline__ float strided_dot(const int32_t *__restrict__ col,
 
 // ---------------------------------------------------------------------------
 // thread-per-row: one thread accumulates one row sequentially from zero.
+// Long rows take steps of kThreadRowDeep positions: the kernel's time is the
+// longest rows' chain of memory trips (config 2 has rows of 4096).
+constexpr int kThreadRowDeep = 16;
 __global__ __launch_bounds__(1024) void spmv_thread_per_row(
     const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
     const float *__restrict__ val, const float *__restrict__ x,
@@ -59,7 +82,7 @@ __global__ __launch_bounds__(1024) void spmv_thread_per_row(
   if (r >= rows)
     return;
   int32_t s = ro[r], e = ro[r + 1];
-  y[r] = strided_dot(col, val, x, s, e, 1, 0.0f);
+  y[r] = strided_dot<kThreadRowDeep>(col, val, x, s, e, 1, 0.0f);
 }
 
 // ---------------------------------------------------------------------------
