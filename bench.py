@@ -245,6 +245,7 @@ def main():
         "spmv-block-size=64",
         "spmv-mapping=wave-per-position spmv-positions-per-lane=8 "
         "spmv-block-size=128",
+        "spmv-mapping=wave-per-row spmv-lanes-per-row=16",
         "spmv-mapping=wave-per-row spmv-lanes-per-row=32",
         "spmv-mapping=wave-per-row",
         "spmv-mapping=block-per-row spmv-block-size=128",
