@@ -290,7 +290,17 @@ __global__ __launch_bounds__(1024) void row_reduce_thread(
   float acc = MAX ? -INFINITY : 0.0f;
   const int32_t e = ro[r + 1];
   int32_t p = ro[r];
-  // four loads in flight, combined in position order
+  // sixteen loads in flight while that many remain, then four, combined in
+  // position order (a thread's row is a chain of memory trips)
+  for (; p + 15 < e; p += 16) {
+    float v[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u)
+      v[u] = val[p + u];
+#pragma unroll
+    for (int u = 0; u < 16; ++u)
+      acc = MAX ? maximumf(acc, v[u]) : acc + v[u];
+  }
   for (; p + 3 < e; p += 4) {
     float v[4];
 #pragma unroll
@@ -340,7 +350,20 @@ __global__ __launch_bounds__(1024) void rowwise_map_thread(
   if (r >= rows)
     return;
   const float rv = rowv[r];
-  for (int32_t p = ro[r]; p < ro[r + 1]; ++p)
+  const int32_t e = ro[r + 1];
+  int32_t p = ro[r];
+  // sixteen entries loaded before they are written back: out may be val
+  // itself (in place), and each entry is read before its own write
+  for (; p + 15 < e; p += 16) {
+    float v[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u)
+      v[u] = val[p + u];
+#pragma unroll
+    for (int u = 0; u < 16; ++u)
+      out[p + u] = map_value(kind, v[u], rv);
+  }
+  for (; p < e; ++p)
     out[p] = map_value(kind, val[p], rv);
 }
 
