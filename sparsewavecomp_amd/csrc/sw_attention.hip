@@ -545,25 +545,27 @@ __global__ __launch_bounds__(64 * W) void attention_tile_fused(
       const float x = q[qrow + kb * 64 + 16 * g + st];
       qa[kb * 16 + st] = i < nt ? x : 0.0f;
     }
-  const int last = r0 + nt - 1;
-  const int32_t bl = ro[last];
-  const int32_t len_last = ro[last + 1] - bl;
-  // The last row's column indices are staged once in LDS: the structure
-  // check compares against them, and both products gather their K / V rows
-  // without waiting for a column load first.  The check itself: wave w
-  // compares rows w and w + W (at most two, nt <= 16 = 2W) with one batch of
-  // loads, since a row of at most kFusedCols entries is 8 loads per lane.
-  static_assert(2 * W >= 16 && kFusedCols == 8 * kWave, "check layout");
+  // lanes 0..nt of every wave hold ro[r0 .. r0+nt]
+  const int32_t my_ro = ro[r0 + (l < nt ? l : nt)];
+  const int32_t bl = __builtin_amdgcn_readlane(my_ro, nt - 1);
+  const int32_t len_last = __builtin_amdgcn_readlane(my_ro, nt) - bl;
+  // The structure check and the LDS copy of the last row's column indices
+  // share one batch of loads: wave w compares rows w and w + W (at most two,
+  // nt <= 16 = 2W) against the last row, a row of at most kFusedCols entries
+  // being 8 loads per lane, and stores entries [64w, 64w + 64) of the last
+  // row to LDS, where both products read their K / V row indices.
+  static_assert(W == 8 && kFusedCols == 8 * kWave, "check layout");
   bool ok = len_last <= kFusedCols; // workgroup-uniform
   if (ok) {
-    for (int t = threadIdx.x; t < len_last; t += 64 * W)
-      lcol[t] = col[bl + t];
     if (threadIdx.x == 0)
       verdict = 1;
-    __syncthreads();
-    const int32_t my_ro = ro[r0 + (l < nt ? l : nt)];
-    bool mine = true;
-    int32_t x[2][8];
+    int32_t x[2][8], yl[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int32_t t = l + u * kWave;
+      // unconditional loads from clamped, valid positions (nnz > 0)
+      yl[u] = col[len_last > 0 ? bl + std::min(t, len_last - 1) : 0];
+    }
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int rr = wave + h * W;
@@ -573,10 +575,10 @@ __global__ __launch_bounds__(64 * W) void attention_tile_fused(
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
         const int32_t t = l + u * kWave;
-        // unconditional loads from clamped, valid positions (nnz > 0)
         x[h][u] = col[len > 0 ? b + std::min(t, len - 1) : 0];
       }
     }
+    bool mine = true;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int rr = wave + h * W;
@@ -585,13 +587,17 @@ __global__ __launch_bounds__(64 * W) void attention_tile_fused(
         const int32_t len = __builtin_amdgcn_readlane(my_ro, rr + 1) - b;
         mine &= len <= len_last;
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          const int32_t t = l + u * kWave;
-          if (t < len && t < len_last)
-            mine &= x[h][u] == lcol[t];
-        }
+        for (int u = 0; u < 8; ++u)
+          if (l + u * kWave < len)
+            mine &= x[h][u] == yl[u];
       }
     }
+    // wave w stores the last row's entries 64w .. 64w + 63
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (u == wave && l + u * kWave < len_last)
+        lcol[l + u * kWave] = yl[u];
+    __syncthreads(); // verdict initialised before any wave clears it
     if (__builtin_amdgcn_ballot_w64(!mine) != 0 && l == 0)
       verdict = 0;
     __syncthreads();
