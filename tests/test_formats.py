@@ -334,3 +334,27 @@ def test_binary_errors(tmp_path):
         F.write_csr_binary(tmp_path / "big.csr", big)
     assert math.isfinite(F.read_matrix_market(
         os.path.join(GOLDEN, "tiny.mtx"))["mean_row_nnz"])
+
+
+@pytest.mark.parametrize("kind", ["csr", "coo", "bsr"])
+def test_every_truncation_is_rejected(tmp_path, kind):
+    """A binary cut short at any byte is an error, never a shorter matrix:
+    the native readers check the length of every section they read."""
+    m = F.read_matrix_market(os.path.join(GOLDEN, "tiny.mtx"))
+    p = tmp_path / f"full.{kind}"
+    if kind == "csr":
+        F.write_csr_binary(p, m)
+        read = F.read_csr_binary
+    elif kind == "coo":
+        F.write_coo_binary(p, m)
+        read = F.read_coo_binary
+    else:
+        F.write_bsr_binary(p, F.convert_to_bsr(m, 2))
+        read = F.read_bsr_binary
+    data = p.read_bytes()
+    read(p)
+    q = tmp_path / f"cut.{kind}"
+    for n in range(len(data)):
+        q.write_bytes(data[:n])
+        with pytest.raises(ValueError):
+            read(q)
