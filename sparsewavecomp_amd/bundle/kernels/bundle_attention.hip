@@ -16,7 +16,9 @@
 // Baked shapes: SW_ROWS (query rows), SW_KEY_ROWS, SW_HEAD_DIM,
 // SW_VALUE_COLS; SW_ALPHA / SW_BETA scale the scores.  Kernels 1-5 launch one
 // work-item per row, kernel 6 one per output element (n = rows * value
-// columns), both with the linear grid ceil_div(n, 64) * 64.
+// columns), both with the linear grid ceil_div(n, 64) * 64.  A work-item
+// keeps kDeep of its row's entries (the scores kernel: four positions of
+// sixteen terms) in flight per step.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -31,6 +33,11 @@
 __device__ __forceinline__ int work_item() {
   return blockIdx.x * 64 + __builtin_amdgcn_workitem_id_x();
 }
+
+// Entries a work-item keeps in flight on its row (a row handled by one
+// work-item is a chain of memory trips; values are still combined in
+// position order).
+constexpr int kDeep = 16;
 
 __device__ __forceinline__ float maximumf(float a, float b) {
   if (a != a || b != b)
@@ -51,13 +58,46 @@ SW_KERNEL sparse_attention_scores(const int32_t *__restrict__ rowOffsets,
   if (r >= SW_ROWS)
     return;
   const float *q = query + (int64_t)r * SW_HEAD_DIM;
-  for (int32_t p = rowOffsets[r]; p < rowOffsets[r + 1]; ++p) {
-    const int64_t c = columnIndices[p];
-    float dot = 0.0f;
-    for (int i = 0; i < SW_HEAD_DIM; ++i)
-      dot = __builtin_fmaf(q[i], transposedKey[(int64_t)i * SW_KEY_ROWS + c],
-                           dot);
-    scores[p] = maskValues[p] * (float)SW_BETA + dot * (float)SW_ALPHA;
+  // four positions per step, sixteen terms of each dot in flight; every dot
+  // is still added term by term in order
+  constexpr int NP = 4;
+  const int32_t e = rowOffsets[r + 1];
+  for (int32_t p = rowOffsets[r]; p < e; p += NP) {
+    int64_t c[NP];
+    float dot[NP];
+#pragma unroll
+    for (int j = 0; j < NP; ++j) {
+      c[j] = columnIndices[p + j < e ? p + j : e - 1];
+      dot[j] = 0.0f;
+    }
+    int i = 0;
+    for (; i + kDeep <= SW_HEAD_DIM; i += kDeep) {
+      float qv[kDeep], kv[NP][kDeep];
+#pragma unroll
+      for (int u = 0; u < kDeep; ++u)
+        qv[u] = q[i + u];
+#pragma unroll
+      for (int j = 0; j < NP; ++j)
+#pragma unroll
+        for (int u = 0; u < kDeep; ++u)
+          kv[j][u] = transposedKey[(int64_t)(i + u) * SW_KEY_ROWS + c[j]];
+#pragma unroll
+      for (int j = 0; j < NP; ++j)
+#pragma unroll
+        for (int u = 0; u < kDeep; ++u)
+          dot[j] = __builtin_fmaf(qv[u], kv[j][u], dot[j]);
+    }
+    for (; i < SW_HEAD_DIM; ++i) {
+#pragma unroll
+      for (int j = 0; j < NP; ++j)
+        dot[j] = __builtin_fmaf(
+            q[i], transposedKey[(int64_t)i * SW_KEY_ROWS + c[j]], dot[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < NP; ++j)
+      if (p + j < e)
+        scores[p + j] =
+            maskValues[p + j] * (float)SW_BETA + dot[j] * (float)SW_ALPHA;
   }
 }
 #elif SW_ATTENTION_ROLE == 2
@@ -68,7 +108,18 @@ SW_KERNEL sparse_attention_row_max(const int32_t *__restrict__ rowOffsets,
   if (r >= SW_ROWS)
     return;
   float m = -INFINITY;
-  for (int32_t p = rowOffsets[r]; p < rowOffsets[r + 1]; ++p)
+  const int32_t e = rowOffsets[r + 1];
+  int32_t p = rowOffsets[r];
+  for (; p + kDeep <= e; p += kDeep) {
+    float v[kDeep];
+#pragma unroll
+    for (int u = 0; u < kDeep; ++u)
+      v[u] = scores[p + u];
+#pragma unroll
+    for (int u = 0; u < kDeep; ++u)
+      m = maximumf(m, v[u]);
+  }
+  for (; p < e; ++p)
     m = maximumf(m, scores[p]);
   rowMaximum[r] = m;
 }
@@ -80,7 +131,18 @@ SW_KERNEL sparse_attention_exp(const int32_t *__restrict__ rowOffsets,
   if (r >= SW_ROWS)
     return;
   const float m = rowMaximum[r];
-  for (int32_t p = rowOffsets[r]; p < rowOffsets[r + 1]; ++p)
+  const int32_t e = rowOffsets[r + 1];
+  int32_t p = rowOffsets[r];
+  for (; p + kDeep <= e; p += kDeep) {
+    float v[kDeep];
+#pragma unroll
+    for (int u = 0; u < kDeep; ++u)
+      v[u] = scores[p + u];
+#pragma unroll
+    for (int u = 0; u < kDeep; ++u)
+      scores[p + u] = expf(v[u] - m);
+  }
+  for (; p < e; ++p)
     scores[p] = expf(scores[p] - m);
 }
 #elif SW_ATTENTION_ROLE == 4
@@ -91,7 +153,18 @@ SW_KERNEL sparse_attention_row_sum(const int32_t *__restrict__ rowOffsets,
   if (r >= SW_ROWS)
     return;
   float s = 0.0f;
-  for (int32_t p = rowOffsets[r]; p < rowOffsets[r + 1]; ++p)
+  const int32_t e = rowOffsets[r + 1];
+  int32_t p = rowOffsets[r];
+  for (; p + kDeep <= e; p += kDeep) {
+    float v[kDeep];
+#pragma unroll
+    for (int u = 0; u < kDeep; ++u)
+      v[u] = scores[p + u];
+#pragma unroll
+    for (int u = 0; u < kDeep; ++u)
+      s += v[u];
+  }
+  for (; p < e; ++p)
     s += scores[p];
   rowSum[r] = s;
 }
@@ -103,7 +176,18 @@ SW_KERNEL sparse_attention_normalize(const int32_t *__restrict__ rowOffsets,
   if (r >= SW_ROWS)
     return;
   const float s = rowSum[r];
-  for (int32_t p = rowOffsets[r]; p < rowOffsets[r + 1]; ++p)
+  const int32_t e = rowOffsets[r + 1];
+  int32_t p = rowOffsets[r];
+  for (; p + kDeep <= e; p += kDeep) {
+    float v[kDeep];
+#pragma unroll
+    for (int u = 0; u < kDeep; ++u)
+      v[u] = scores[p + u];
+#pragma unroll
+    for (int u = 0; u < kDeep; ++u)
+      scores[p + u] = v[u] / s;
+  }
+  for (; p < e; ++p)
     scores[p] = scores[p] / s;
 }
 #elif SW_ATTENTION_ROLE == 6
@@ -117,7 +201,24 @@ SW_KERNEL sparse_attention_output(const int32_t *__restrict__ rowOffsets,
     return;
   const int r = e / SW_VALUE_COLS, c = e - r * SW_VALUE_COLS;
   float acc = 0.0f;
-  for (int32_t p = rowOffsets[r]; p < rowOffsets[r + 1]; ++p)
+  const int32_t pe = rowOffsets[r + 1];
+  int32_t p = rowOffsets[r];
+  for (; p + kDeep <= pe; p += kDeep) {
+    float sv[kDeep], vv[kDeep];
+    int32_t cc[kDeep];
+#pragma unroll
+    for (int u = 0; u < kDeep; ++u) {
+      sv[u] = scores[p + u];
+      cc[u] = columnIndices[p + u];
+    }
+#pragma unroll
+    for (int u = 0; u < kDeep; ++u)
+      vv[u] = value[(int64_t)cc[u] * SW_VALUE_COLS + c];
+#pragma unroll
+    for (int u = 0; u < kDeep; ++u)
+      acc = __builtin_fmaf(sv[u], vv[u], acc);
+  }
+  for (; p < pe; ++p)
     acc = __builtin_fmaf(scores[p],
                          value[(int64_t)columnIndices[p] * SW_VALUE_COLS + c],
                          acc);

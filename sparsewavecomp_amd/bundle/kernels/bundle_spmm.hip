@@ -8,9 +8,10 @@
 //   SW_K     rhs / output columns (= the tile size: one tile per row)
 // Mapping wave-per-row-tile with 64-thread blocks: the runtime launches
 // ceil_div(n, 64/64) * 64 work-items, so block b is row b.  Lanes stride the
-// row's positions, each reads the value once and SW_K rhs columns (128-bit
-// loads when SW_K is a multiple of 4), the 64 partial sums of every column
-// meet in a DPP/swizzle butterfly and lane 0 stores the row.
+// row's positions (four in flight per step), each reads the value once and
+// SW_K rhs columns (128-bit loads when SW_K is a multiple of 4), the 64
+// partial sums of every column meet in a DPP/swizzle butterfly and lane 0
+// stores the row.
 #include "../../csrc/sw_device.h"
 
 #ifndef SW_ROWS
@@ -37,9 +38,8 @@ extern "C" __global__ __launch_bounds__(64) void sparsewave_spmm_wave_per_row_ti
   for (int c = 0; c < K; ++c)
     acc[c] = 0.0f;
   const int32_t s = rowOffsets[row], e = rowOffsets[row + 1];
-  for (int32_t p = s + l; p < e; p += kWave) {
-    const float v = ld_stream(values + p);
-    const float *b = rhs + (int64_t)ld_stream(columnIndices + p) * K;
+  // one position's value and rhs row, added to the lane's partials
+  auto add = [&](float v, const float *b) __attribute__((always_inline)) {
     if constexpr (K % 4 == 0) {
 #pragma unroll
       for (int c = 0; c < K; c += 4) {
@@ -54,7 +54,25 @@ extern "C" __global__ __launch_bounds__(64) void sparsewave_spmm_wave_per_row_ti
       for (int c = 0; c < K; ++c)
         acc[c] = __builtin_fmaf(v, b[c], acc[c]);
     }
+  };
+  // four of the lane's positions in flight per step, added in order
+  constexpr int U = 4;
+  int32_t p = s + l;
+  for (; p + (U - 1) * kWave < e; p += U * kWave) {
+    float v[U];
+    const float *b[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      v[u] = ld_stream(values + p + u * kWave);
+      b[u] = rhs + (int64_t)ld_stream(columnIndices + p + u * kWave) * K;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      add(v[u], b[u]);
   }
+  for (; p < e; p += kWave)
+    add(ld_stream(values + p),
+        rhs + (int64_t)ld_stream(columnIndices + p) * K);
 #pragma unroll
   for (int c = 0; c < K; ++c)
     acc[c] = group_sum<kWave>(acc[c]);
