@@ -3,8 +3,8 @@
 // Cross-lane work uses DPP (row_shr, quad_perm, row_mirror, row_bcast) and
 // ds_swizzle, which move data through the VALU without LDS memory, and
 // v_readlane for wave-uniform results.  Streaming CSR and BSR arrays are
-// read with plain loads (ld_stream); only COO SpMV uses the non-temporal
-// hint, the one kernel it measured faster for.
+// read with plain loads (ld_stream); the non-temporal hint is kept where it
+// measured no slower: COO SpMV, and the values of the position SpMV.
 #pragma once
 
 #include <hip/hip_runtime.h>
