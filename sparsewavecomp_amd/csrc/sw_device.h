@@ -4,7 +4,7 @@
 // ds_swizzle, which move data through the VALU without LDS memory, and
 // v_readlane for wave-uniform results.  Streaming CSR and BSR arrays are
 // read with plain loads (ld_stream); the non-temporal hint is kept where it
-// measured no slower: COO SpMV, and the values of the position SpMV.
+// measured no slower: the values of the position and COO SpMV kernels.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -154,7 +154,8 @@ __device__ __forceinline__ T ld_stream(const T *p) {
   return *p;
 }
 
-// Non-temporal load: COO SpMV measured 4% faster with it (237 vs 247 us).
+// Non-temporal load: used for the values of the position SpMV and the COO
+// SpMV, where it measured no slower and keeps x longer in L2.
 template <typename T>
 __device__ __forceinline__ T ld_nontemporal(const T *p) {
   return __builtin_nontemporal_load(p);

@@ -511,8 +511,11 @@ __global__ __launch_bounds__(1024) void coo_run_segmented(
     if (full) {
 #pragma unroll
       for (int q = 0; q < P; q += 4) {
-        v4i r = ld_nontemporal(reinterpret_cast<const v4i *>(ri + p0 + q));
-        v4i c = ld_nontemporal(reinterpret_cast<const v4i *>(col + p0 + q));
+        // row and column indices plain, values non-temporal: 222 us on
+        // configuration 2 as COO, against 233 us with all three
+        // non-temporal and 247 us with all three plain
+        v4i r = ld_stream(reinterpret_cast<const v4i *>(ri + p0 + q));
+        v4i c = ld_stream(reinterpret_cast<const v4i *>(col + p0 + q));
         v4f v = ld_nontemporal(reinterpret_cast<const v4f *>(val + p0 + q));
         rr[q + 0] = r.x;
         rr[q + 1] = r.y;
@@ -529,9 +532,8 @@ __global__ __launch_bounds__(1024) void coo_run_segmented(
 #pragma unroll
     for (int q = 0; q < P; ++q)
       if (q < n) {
-        rr[q] = ld_nontemporal(ri + p0 + q);
-        prod[q] =
-            ld_nontemporal(val + p0 + q) * x[ld_nontemporal(col + p0 + q)];
+        rr[q] = ld_stream(ri + p0 + q);
+        prod[q] = ld_nontemporal(val + p0 + q) * x[ld_stream(col + p0 + q)];
       }
   }
   int hk = -1, tk = -1, closed = 0;
