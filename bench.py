@@ -3,8 +3,9 @@
 
 Headline: CSR SpMV fp32/i32 on the 1,048,576-row lognormal matrix
 (configuration 2), reported as achieved HBM GB/s of algorithmic bytes
-(4(n+1) + 8 nnz + 4 m + 4 n per SpMV) and GFLOP/s (2 nnz), for the fastest
-mapping.  Every mapping, CSR SpMM (K = 4, 64), BSR SpMM (fp32, bf16) and the
+(4(n+1) + 8 nnz + 4 m + 4 n per SpMV) and GFLOP/s (2 nnz), for the tuned
+headline mapping; the run's fastest mapping is named beside it.  Every
+mapping, CSR SpMM (K = 4, 64), BSR SpMM (fp32, bf16) and the
 sparse-attention chain are measured on the same run and reported under
 "workloads".  A step is one call of the C ABI over one resident batch.
 
@@ -266,7 +267,11 @@ def main():
             "GFLOP/s": spmv_flops / ms / 1e6,
             "hbm_frac": spmv_bytes / ms / 1e6 / HBM_PEAK_GBS}
         log(f"  {ms * 1e3:.1f} us  {spmv_bytes / ms / 1e6:.0f} GB/s")
-    best = min(spmv_results, key=lambda k: spmv_results[k]["ms"])
+    # the headline is the tuned default mapping (the one the committed
+    # rocprofv3 summaries are taken for); the fastest measured mapping is
+    # reported beside it
+    fastest = min(spmv_results, key=lambda k: spmv_results[k]["ms"])
+    best = HEADLINE_SPMV if HEADLINE_SPMV in spmv_results else fastest
     # the gather floor on the same buffers: column/value reads and x gathers
     # with no row structure, the part no SpMV schedule avoids
     part = torch.empty((nnz + 511) // 512, device=dev)
@@ -277,7 +282,7 @@ def main():
     del part
     workloads["spmv_config2"] = {
         "bytes": spmv_bytes, "flops": spmv_flops, "best": best,
-        "mappings": spmv_results,
+        "fastest": fastest, "mappings": spmv_results,
         "gather_floor": {"ms": floor_ms,
                          "best_mapping_frac": floor_ms /
                          spmv_results[best]["ms"]}}
