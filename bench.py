@@ -71,7 +71,7 @@ def parse():
     return ap.parse_args()
 
 
-HEADLINE_SPMV = ("spmv-mapping=wave-per-position spmv-positions-per-lane=8 "
+HEADLINE_SPMV = ("spmv-mapping=wave-per-position spmv-positions-per-lane=4 "
                  "spmv-block-size=64")
 HEADLINE_COO = ("spmv-mapping=wave-per-position spmv-positions-per-lane=4 "
                 "spmv-block-size=64")
@@ -242,7 +242,7 @@ def main():
     spmv_flops = 2 * nnz
     mappings = [
         HEADLINE_SPMV,
-        "spmv-mapping=wave-per-position spmv-positions-per-lane=4 "
+        "spmv-mapping=wave-per-position spmv-positions-per-lane=8 "
         "spmv-block-size=64",
         "spmv-mapping=wave-per-position spmv-positions-per-lane=8 "
         "spmv-block-size=128",
