@@ -325,6 +325,17 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// Maximum over aligned groups of 32 lanes, every lane of a group receiving
+// it (the 32-lane half of wave_max).
+__device__ __forceinline__ float group_max32(float v) {
+  v = maximumf(v, dpp_f<kQuadXor1>(-INFINITY, v));
+  v = maximumf(v, dpp_f<kQuadXor2>(-INFINITY, v));
+  v = maximumf(v, dpp_f<kRowHalfMirror>(-INFINITY, v));
+  v = maximumf(v, dpp_f<kRowMirror>(-INFINITY, v));
+  v = maximumf(v, swizzle_xor16(v));
+  return v;
+}
+
 template <bool MAX>
 __global__ __launch_bounds__(256) void row_reduce_wave(
     const int32_t *__restrict__ ro, const float *__restrict__ val,
@@ -491,8 +502,8 @@ __device__ __forceinline__ void attention_row_softmax(
 // whose last row holds at most kFusedCols entries keeps its scores in LDS:
 //   A. the SDDMM of sddmm_tile_mfma (16 x 16 x d MFMA products, wave w
 //      taking the column chunks w, w+W, ...) writes raw scores to LDS;
-//   B. wave w normalises rows w, w+W, ... in LDS and writes each final
-//      score, its row maximum and its row sum once;
+//   B. the two halves of wave w normalise rows w and w+W at once in LDS
+//      and write each final score, its row maximum and its row sum once;
 //   C. the SpMM of spmm_tile_mfma reads the tile's probabilities from LDS
 //      (lane (i, g) takes P[i][t0+4g+s]) against the gathered V rows, and
 //      the waves' partial output tiles are summed through LDS.
@@ -681,26 +692,33 @@ __global__ __launch_bounds__(64 * W) void attention_tile_fused(
         }
       }
   };
-  // B. row softmax in LDS; each final score is written to HBM once
-  for (int rr = wave; rr < nt; rr += W) {
-    const int32_t s = ro[r0 + rr], len = ro[r0 + rr + 1] - s;
-    float *srow = sc + rr * kFusedStride;
+  // B. row softmax in LDS, one row per half-wave (wave w: rows w and w + W,
+  // the two at once); each final score is written to HBM once
+  {
+    constexpr int H = kWave / 2;
+    const int hl = l & (H - 1);
+    const int rr = wave + (l >= H ? W : 0);
+    const bool live = rr < nt;
+    const int rc = live ? rr : 0;
+    const int32_t s = ro[r0 + rc];
+    const int32_t len = live ? ro[r0 + rc + 1] - s : 0;
+    float *srow = sc + rc * kFusedStride;
     float m = -INFINITY, sum = 0.0f;
-    for (int t = l; t < len; t += kWave)
+    for (int t = hl; t < len; t += H)
       m = maximumf(m, srow[t]);
-    m = wave_max(m);
-    for (int t = l; t < len; t += kWave) {
+    m = group_max32(m);
+    for (int t = hl; t < len; t += H) {
       const float e = expf(srow[t] - m);
       srow[t] = e;
       sum += e;
     }
-    sum = group_sum<kWave>(sum);
-    for (int t = l; t < len; t += kWave) {
+    sum = group_sum<H>(sum);
+    for (int t = hl; t < len; t += H) {
       const float p = srow[t] / sum;
       srow[t] = p;
       scores[s + t] = p;
     }
-    if (l == 0) {
+    if (hl == 0 && live) {
       rmax[r0 + rr] = m;
       rsum[r0 + rr] = sum;
     }
