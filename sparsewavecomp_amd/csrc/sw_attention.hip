@@ -499,21 +499,29 @@ __device__ __forceinline__ void attention_row_softmax(
 // softmax (rowMaximum, rowSum and the normalised scores written as the
 // separate ops write them), and output = P V, in one kernel.  A tile whose
 // rows share the last row's column structure (tile_prefix_ok_block) and
-// whose last row holds at most kFusedCols entries keeps its scores in LDS:
-//   A. the SDDMM of sddmm_tile_mfma (16 x 16 x d MFMA products, wave w
-//      taking the column chunks w, w+W, ...) writes raw scores to LDS;
-//   B. the two halves of wave w normalise rows w and w+W at once in LDS
-//      and write each final score, its row maximum and its row sum once;
-//   C. the SpMM of spmm_tile_mfma reads the tile's probabilities from LDS
-//      (lane (i, g) takes P[i][t0+4g+s]) against the gathered V rows, and
-//      the waves' partial output tiles are summed through LDS.
+// whose last row holds at most kFusedCols entries keeps its scores in
+// registers.  Wave w takes the 16-entry chunks k = 0..3 at entries
+// t0(k) = 16 (w + W k) of the last row:
+//   A. S^T = K_chunk Q^T with 16 x 16 x 4 MFMAs (the gathered K rows as the
+//      A operand, Q as the B operand), so that lane (i, g) holds the scores
+//      of row i at entries t0 + 4g .. t0 + 4g + 3, which is the A operand
+//      the P V product takes;
+//   B. the row maxima, then the row sums, are reduced over the four lanes of
+//      a row in each wave and over the waves through LDS (two barriers);
+//      every final score, row maximum and row sum is written once.  The V
+//      rows of each wave's first two chunks are loaded before the first
+//      barrier, so their latency overlaps the softmax;
+//   C. output = P V from those registers against the gathered V rows, the
+//      waves' partial output tiles summed through LDS.
 // The scores thus cross HBM once (written) instead of five times, and the
 // chain is one launch.  Other tiles run row by row: each wave computes a row's
 // scores, softmax and output in global memory.
 constexpr int kFusedCols = 512;
-constexpr int kFusedStride = kFusedCols + 4; // LDS row pitch (bank spread)
 constexpr int kFusedWaves = 8;
+constexpr int kFusedChunks = kFusedCols / (16 * kFusedWaves);
 
+// The host guarantees that the byte offsets into mask / scores (positions),
+// K^T (kdim * cols) and V (cols * dv) fit 32 bits.
 template <int KB, int W>
 __global__ __launch_bounds__(64 * W) void attention_tile_fused(
     const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
@@ -522,8 +530,10 @@ __global__ __launch_bounds__(64 * W) void attention_tile_fused(
     float *scores, float *__restrict__ rmax, float *__restrict__ rsum,
     float *__restrict__ out, int32_t rows, int64_t cols, int32_t kdim,
     int64_t dv, float alpha, float beta) {
-  __shared__ float sc[16 * kFusedStride];
+  static_assert(W == 8 && kFusedCols == 8 * kWave && kFusedChunks == 4,
+                "check layout");
   __shared__ float part[W][4][4][kWave]; // [wave][n tile][v][lane]
+  __shared__ float wred[2][W][16];       // [max, sum][wave][row]
   __shared__ int32_t lcol[kFusedCols];   // the last row's columns
   __shared__ int verdict;
   const int r0 = blockIdx.x * 16;
@@ -533,20 +543,10 @@ __global__ __launch_bounds__(64 * W) void attention_tile_fused(
   // loads are unconditional from clamped, valid addresses, their values
   // selected afterwards (a guarded load becomes a branch that waits for it
   // on the spot)
-  int32_t rb[4], rl[4];
-  {
-    int32_t b[5];
-#pragma unroll
-    for (int v = 0; v < 5; ++v)
-      b[v] = ro[std::min(r0 + 4 * g + v, rows)];
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      rb[v] = b[v];
-      rl[v] = 4 * g + v < nt ? b[v + 1] - b[v] : 0;
-    }
-  }
   const int ic = i < nt ? i : nt - 1;
-  const int32_t la = i < nt ? ro[r0 + ic + 1] - ro[r0 + ic] : 0;
+  // row i of the tile: its first position and its length (0 past nt)
+  const int32_t rbase = ro[r0 + ic];
+  const int32_t la = i < nt ? ro[r0 + ic + 1] - rbase : 0;
   float qa[16 * KB];
   const int64_t qrow = (int64_t)std::min(r0 + i, rows - 1) * kdim;
 #pragma unroll
@@ -565,7 +565,6 @@ __global__ __launch_bounds__(64 * W) void attention_tile_fused(
   // nt <= 16 = 2W) against the last row, a row of at most kFusedCols entries
   // being 8 loads per lane, and stores entries [64w, 64w + 64) of the last
   // row to LDS, where both products read their K / V row indices.
-  static_assert(W == 8 && kFusedCols == 8 * kWave, "check layout");
   bool ok = len_last <= kFusedCols; // workgroup-uniform
   if (ok) {
     if (threadIdx.x == 0)
@@ -625,127 +624,162 @@ __global__ __launch_bounds__(64 * W) void attention_tile_fused(
     }
     return;
   }
-  // A. raw scores into LDS, two column chunks per iteration (W chunks apart)
-  for (int32_t t0 = wave * 16; t0 < len_last; t0 += 32 * W) {
-    const int32_t t1 = t0 + 16 * W;
-    const bool two = t1 < len_last; // wave-uniform
-    const int32_t ta = t0 + i, tb = t1 + i;
-    const int64_t cj0 = lcol[std::min(ta, len_last - 1)];
-    const int64_t cj1 = lcol[std::min(two ? tb : ta, len_last - 1)];
-    float s0[4], s1[4];
+  // first entry of this wave's chunk k (entries past len_last: no chunk)
+  auto chunk_t0 = [&](int k) __attribute__((always_inline)) {
+    return 16 * (wave + W * k);
+  };
+  // entry (k, v) of lane (i, g): row i, entry chunk_t0(k) + 4g + v
+  auto valid = [&](int k, int v) __attribute__((always_inline)) {
+    return chunk_t0(k) + 4 * g + v < la;
+  };
+  // A. S^T per chunk, two chunks per step: sv[k][v] = score (i, t0(k)+4g+v)
+  float sv[kFusedChunks][4];
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      // position bl is inside the last row, always a valid index
-      const bool in0 = mask != nullptr && ta < rl[v];
-      const bool in1 = mask != nullptr && two && tb < rl[v];
-      const float x0 = mask != nullptr ? mask[in0 ? rb[v] + ta : bl] : 0.0f;
-      const float x1 = mask != nullptr ? mask[in1 ? rb[v] + tb : bl] : 0.0f;
-      s0[v] = in0 ? x0 : 0.0f;
-      s1[v] = in1 ? x1 : 0.0f;
-    }
+  for (int it = 0; it < kFusedChunks / 2; ++it) {
+    const int32_t t0 = chunk_t0(2 * it), t1 = chunk_t0(2 * it + 1);
+    const bool one = t0 < len_last, two = t1 < len_last; // wave-uniform
+    const int32_t last = std::max(len_last - 1, 0);
+    const uint32_t cj0 = lcol[std::min(t0 + i, last)];
+    const uint32_t cj1 = lcol[std::min(two ? t1 + i : t0 + i, last)];
+    float s0[4] = {0.f, 0.f, 0.f, 0.f}, s1[4] = {0.f, 0.f, 0.f, 0.f};
     v4f acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+    if (one) {
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb) {
-      float bv0[16], bv1[16];
-#pragma unroll
-      for (int st = 0; st < 16; ++st) {
-        const float *krow = kt + (int64_t)(kb * 64 + 16 * g + st) * cols;
-        bv0[st] = krow[cj0];
-        bv1[st] = krow[cj1];
+      for (int v = 0; v < 4; ++v) {
+        // a chunk exists, so the last row is not empty and its first
+        // position bl is a valid index
+        const bool in0 = valid(2 * it, v), in1 = valid(2 * it + 1, v);
+        const float x0 =
+            *at_bytes(mask, 4u * (in0 ? rbase + t0 + 4 * g + v : bl));
+        const float x1 =
+            *at_bytes(mask, 4u * (in1 ? rbase + t1 + 4 * g + v : bl));
+        s0[v] = in0 ? x0 : 0.0f;
+        s1[v] = in1 ? x1 : 0.0f;
       }
+      // K^T[kb 64 + 16g + st][cj]: the wave-uniform row kb 64 + st plus the
+      // lane's byte offset (16g rows and cj columns on)
+      const uint32_t ko0 = 4u * (16u * g * (uint32_t)cols + cj0);
+      const uint32_t ko1 = 4u * (16u * g * (uint32_t)cols + cj1);
 #pragma unroll
-      for (int st = 0; st < 16; ++st) {
-        acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[kb * 16 + st], bv0[st],
-                                                    acc0, 0, 0, 0);
-        if (two)
-          acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[kb * 16 + st],
-                                                      bv1[st], acc1, 0, 0, 0);
+      for (int kb = 0; kb < KB; ++kb) {
+        float bv0[16], bv1[16];
+#pragma unroll
+        for (int st = 0; st < 16; ++st) {
+          const float *krow = kt + (int64_t)(kb * 64 + st) * cols;
+          bv0[st] = *at_bytes(krow, ko0);
+          bv1[st] = *at_bytes(krow, ko1);
+        }
+#pragma unroll
+        for (int st = 0; st < 16; ++st) {
+          acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(
+              bv0[st], qa[kb * 16 + st], acc0, 0, 0, 0);
+          if (two)
+            acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                bv1[st], qa[kb * 16 + st], acc1, 0, 0, 0);
+        }
       }
     }
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-      float *srow = sc + (4 * g + v) * kFusedStride;
-      if (ta < rl[v])
-        srow[ta] = combine_sddmm(SW_SDDMM_AFFINE, s0[v], acc0[v], alpha, beta);
-      if (two && tb < rl[v])
-        srow[tb] = combine_sddmm(SW_SDDMM_AFFINE, s1[v], acc1[v], alpha, beta);
+      sv[2 * it][v] =
+          combine_sddmm(SW_SDDMM_AFFINE, s0[v], acc0[v], alpha, beta);
+      sv[2 * it + 1][v] =
+          combine_sddmm(SW_SDDMM_AFFINE, s1[v], acc1[v], alpha, beta);
     }
   }
-  __syncthreads();
-  // C's V rows, 16 stored entries (four MFMA steps) per chunk and two chunks
-  // per step: lane (j, g) takes V[c_t][nb + 16n + j], t = t0 + 16h + 4g + s
-  constexpr int CH = 2;
-  auto load_v = [&](int32_t t0, int64_t nb, float (&bv)[CH][4][4])
+  // C's V rows for chunks 2 it and 2 it + 1: lane (j, g) takes
+  // V[c_t][nb + 16n + j] for t = t0(k) + 4g + st (chunks past len_last and
+  // output tiles past dv read a valid address and hold zeros)
+  auto load_v = [&](int it, int64_t nb, float (&bv)[2][4][4])
       __attribute__((always_inline)) {
     const int ntiles = (int)std::min<int64_t>(4, (dv - nb) / 16);
 #pragma unroll
-    for (int h = 0; h < CH; ++h)
+    for (int h = 0; h < 2; ++h)
 #pragma unroll
       for (int st = 0; st < 4; ++st) {
-        const int32_t t = t0 + 16 * h + 4 * g + st;
-        const int64_t c = lcol[std::min(t, len_last - 1)];
+        const int32_t t = chunk_t0(2 * it + h) + 4 * g + st;
+        const uint32_t c = lcol[std::max(std::min(t, len_last - 1), 0)];
+        // V[c][nb + 16n + j]: the wave-uniform column nb + 16n plus the
+        // lane's byte offset (row c, column j; row 0 past len_last).  Tiles
+        // n >= ntiles read tile 0 again: their outputs are never stored, so
+        // their values need no select (a select on the wave-uniform n <
+        // ntiles would become a branch around each load).
+        const uint32_t vo =
+            4u * ((t < len_last ? c * (uint32_t)dv : 0u) + (uint32_t)i);
 #pragma unroll
         for (int n = 0; n < 4; ++n) {
-          const bool in = n < ntiles && t < len_last;
-          const float x = value[(in ? c : 0) * dv + nb + 16 * (in ? n : 0) + i];
-          bv[h][n][st] = in ? x : 0.0f;
+          const int nn = n < ntiles ? n : 0; // wave-uniform
+          const float x = *at_bytes(value + nb + 16 * nn, vo);
+          bv[h][n][st] = t < len_last ? x : 0.0f;
         }
       }
   };
-  // B. row softmax in LDS, one row per half-wave (wave w: rows w and w + W,
-  // the two at once); each final score is written to HBM once
+  float bv[2][4][4];
+  load_v(0, 0, bv); // in flight over the softmax
+  // B. row softmax: lanes (i, 0..3) of every wave hold row i's entries
   {
-    constexpr int H = kWave / 2;
-    const int hl = l & (H - 1);
-    const int rr = wave + (l >= H ? W : 0);
-    const bool live = rr < nt;
-    const int rc = live ? rr : 0;
-    const int32_t s = ro[r0 + rc];
-    const int32_t len = live ? ro[r0 + rc + 1] - s : 0;
-    float *srow = sc + rc * kFusedStride;
-    float m = -INFINITY, sum = 0.0f;
-    for (int t = hl; t < len; t += H)
-      m = maximumf(m, srow[t]);
-    m = group_max32(m);
-    for (int t = hl; t < len; t += H) {
-      const float e = expf(srow[t] - m);
-      srow[t] = e;
-      sum += e;
-    }
-    sum = group_sum<H>(sum);
-    for (int t = hl; t < len; t += H) {
-      const float p = srow[t] / sum;
-      srow[t] = p;
-      scores[s + t] = p;
-    }
-    if (hl == 0 && live) {
-      rmax[r0 + rr] = m;
-      rsum[r0 + rr] = sum;
+    float m = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < kFusedChunks; ++k)
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        if (valid(k, v))
+          m = maximumf(m, sv[k][v]);
+    m = maximumf(m, swizzle_xor16(m));
+    m = maximumf(m, shfl_xor32(m));
+    if (g == 0)
+      wred[0][wave][i] = m;
+    __syncthreads();
+    m = wred[0][0][i];
+#pragma unroll
+    for (int w = 1; w < W; ++w)
+      m = maximumf(m, wred[0][w][i]);
+    float sum = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kFusedChunks; ++k)
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        if (valid(k, v)) {
+          sv[k][v] = expf(sv[k][v] - m);
+          sum += sv[k][v];
+        }
+    sum += swizzle_xor16(sum);
+    sum += shfl_xor32(sum);
+    if (g == 0)
+      wred[1][wave][i] = sum;
+    __syncthreads();
+    sum = wred[1][0][i];
+#pragma unroll
+    for (int w = 1; w < W; ++w)
+      sum += wred[1][w][i];
+#pragma unroll
+    for (int k = 0; k < kFusedChunks; ++k)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const bool in = valid(k, v);
+        const float p = in ? sv[k][v] / sum : 0.0f;
+        if (in) // the wave-uniform entry t0(k) + v, lane offset rbase + 4g
+          *at_bytes(scores + chunk_t0(k) + v, 4u * (rbase + 4 * g)) = p;
+        sv[k][v] = p; // zero past the row: the P V product adds nothing
+      }
+    if (wave == 0 && g == 0 && i < nt) {
+      rmax[r0 + i] = m;
+      rsum[r0 + i] = sum;
     }
   }
-  __syncthreads();
-  // C. output = P V, P from LDS (lane (i, g) takes P[i][t]); the waves'
-  // partial output tiles are summed through LDS
-  const float *prow = sc + i * kFusedStride;
-  auto mfma_step = [&](int32_t t0, const float (&bv)[CH][4][4], v4f (&acc)[4])
+  // C. output = P V with P from sv (lane (i, g) holds P[i][t0(k)+4g+st],
+  // the A operand of step st); the waves' partial tiles are summed in LDS
+  auto mfma_pair = [&](int it, const float (&b)[2][4][4], v4f (&acc)[4])
       __attribute__((always_inline)) {
-    float a[CH][4];
 #pragma unroll
-    for (int h = 0; h < CH; ++h)
+    for (int h = 0; h < 2; ++h)
+      if (chunk_t0(2 * it + h) < len_last) // wave-uniform
 #pragma unroll
-      for (int st = 0; st < 4; ++st) {
-        const int32_t t = t0 + 16 * h + 4 * g + st;
-        const float x = prow[std::min(t, kFusedCols - 1)];
-        a[h][st] = t < la ? x : 0.0f;
-      }
+        for (int n = 0; n < 4; ++n)
 #pragma unroll
-    for (int h = 0; h < CH; ++h)
-#pragma unroll
-      for (int n = 0; n < 4; ++n)
-#pragma unroll
-        for (int st = 0; st < 4; ++st)
-          acc[n] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[h][st], bv[h][n][st],
-                                                        acc[n], 0, 0, 0);
+          for (int st = 0; st < 4; ++st)
+            acc[n] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                sv[2 * it + h][st], b[h][n][st], acc[n], 0, 0, 0);
   };
   for (int64_t nb = 0; nb < dv; nb += 64) {
     const int ntiles = (int)std::min<int64_t>(4, (dv - nb) / 16);
@@ -753,12 +787,15 @@ __global__ __launch_bounds__(64 * W) void attention_tile_fused(
 #pragma unroll
     for (int n = 0; n < 4; ++n)
       acc[n] = v4f{0.f, 0.f, 0.f, 0.f};
-    for (int32_t t0 = wave * 16 * CH; t0 < len_last; t0 += W * 16 * CH) {
-      float bv[CH][4][4];
-      load_v(t0, nb, bv);
-      // keep the step's loads ahead of its MFMAs
+    if (nb > 0)
+      load_v(0, nb, bv);
+    // keep the loads ahead of the MFMAs that take them
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_pair(0, bv, acc);
+    if (chunk_t0(2) < len_last) { // wave-uniform
+      load_v(1, nb, bv);
       __builtin_amdgcn_sched_barrier(0);
-      mfma_step(t0, bv, acc);
+      mfma_pair(1, bv, acc);
     }
 #pragma unroll
     for (int n = 0; n < 4; ++n)
@@ -1007,8 +1044,11 @@ extern "C" int sw_sparse_attention_f32(
   if (nnz > 0 && o.sddmm_lanes_per_row == 64 &&
       sw::streq(o.sddmm_mapping, "row-tile-mfma") &&
       sw::streq(o.spmm_mapping, "row-tile-mfma") && (d == 64 || d == 128) &&
-      dv > 0 && dv % 16 == 0) {
-    // the whole chain in one kernel per 16-row tile
+      dv > 0 && dv % 16 == 0 && 4 * nnz <= (int64_t)UINT32_MAX &&
+      4 * d * cols <= (int64_t)UINT32_MAX &&
+      4 * dv * cols <= (int64_t)UINT32_MAX) {
+    // the whole chain in one kernel per 16-row tile (its loads and stores
+    // take 32-bit byte offsets from wave-uniform bases)
     int64_t grid;
     rc = grid_for(rows, 16, "fused attention", &grid);
     if (rc)

@@ -11,6 +11,7 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <type_traits>
 
 namespace swd {
 
@@ -159,6 +160,16 @@ __device__ __forceinline__ T ld_stream(const T *p) {
 template <typename T>
 __device__ __forceinline__ T ld_nontemporal(const T *p) {
   return __builtin_nontemporal_load(p);
+}
+
+// p advanced by b bytes.  With p wave-uniform this is the form the global
+// memory instructions take directly (base in SGPRs, one 32-bit VGPR offset),
+// so a lane's address costs no 64-bit arithmetic; the caller guarantees that
+// the byte offset fits 32 bits.
+template <typename T>
+__device__ __forceinline__ T *at_bytes(T *p, uint32_t b) {
+  using B = std::conditional_t<std::is_const_v<T>, const char, char>;
+  return reinterpret_cast<T *>(reinterpret_cast<B *>(p) + b);
 }
 
 // ---- CSR row recovery -------------------------------------------------------

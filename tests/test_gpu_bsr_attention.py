@@ -348,21 +348,12 @@ def _long_prefix_csr():
     return W.CSR(len(rows_cols), cols, ro, col, val)
 
 
-@pytest.mark.parametrize("shape", ["structure", "long"])
-@pytest.mark.parametrize("d,dv", [(64, 64), (128, 16), (64, 80), (128, 128)])
-def test_attention_fused_paths(dev, orc, shape, d, dv):
-    """The one-kernel attention chain: LDS tiles, the row-by-row path
-    (columns not shared, a row longer than the last, a deep mismatch, rows
-    over 512 entries), empty rows, a partial last tile, d of 64 and 128, dv
-    of one to eight 16-column tiles, and a non-zero mask weight."""
-    csr = _tile_structure_csr() if shape == "structure" else _long_prefix_csr()
+def _attention_case(orc, csr, d, dv, options):
     rng = np.random.default_rng(d + dv)
     q = rng.standard_normal((csr.rows, d)).astype(np.float32)
     kt = rng.standard_normal((d, csr.cols)).astype(np.float32)
     v = rng.standard_normal((csr.cols, dv)).astype(np.float32)
     alpha, beta = 0.125, 0.5
-    G.say(f"fused attention {shape} rows={csr.rows} nnz={csr.nnz} d={d} "
-          f"dv={dv}")
     nan = float("nan")
     scores = torch.full((csr.nnz,), nan, device=G.DEV)
     rmax = torch.full((csr.rows,), nan, device=G.DEV)
@@ -370,11 +361,29 @@ def test_attention_fused_paths(dev, orc, shape, d, dv):
     out = torch.full((csr.rows, dv), nan, device=G.DEV)
     sw.sparse_attention(G.t(csr.row_offsets), G.t(csr.column_indices),
                         G.t(csr.values), G.t(q), G.t(kt), G.t(v), scores,
-                        rmax, rsum, out, alpha, beta, options=FUSED)
+                        rmax, rsum, out, alpha, beta, options=options)
     torch.cuda.synchronize()
     s_ref, m_ref, sum_ref, ref = orc.sparse_attention(
         csr.row_offsets, csr.column_indices, csr.values, q, kt, v, alpha,
         beta)
+    return scores, rmax, rsum, out, (s_ref, m_ref, sum_ref, ref), v
+
+
+@pytest.mark.parametrize("shape", ["structure", "long"])
+@pytest.mark.parametrize("d,dv", [(64, 64), (128, 16), (64, 80), (128, 128)])
+def test_attention_fused_paths(dev, orc, shape, d, dv):
+    """The one-kernel attention chain: register tiles, the row-by-row path
+    (columns not shared, a row longer than the last, a deep mismatch, rows
+    over 512 entries), empty rows, a partial last tile, d of 64 and 128, dv
+    of one to eight 16-column tiles, and a non-zero mask weight."""
+    csr = _tile_structure_csr() if shape == "structure" else _long_prefix_csr()
+    G.say(f"fused attention {shape} rows={csr.rows} nnz={csr.nnz} d={d} "
+          f"dv={dv}")
+    _check_attention(orc, csr, *_attention_case(orc, csr, d, dv, FUSED))
+
+
+def _check_attention(orc, csr, scores, rmax, rsum, out, refs, v):
+    s_ref, m_ref, sum_ref, ref = refs
     bound = orc.spmm_abs_bound(csr.row_offsets, csr.column_indices, s_ref, v)
     assert_within_bound(out.cpu().numpy(), ref, bound, rel=2e-5)
     np.testing.assert_allclose(scores.cpu().numpy(), s_ref, rtol=1e-4,
