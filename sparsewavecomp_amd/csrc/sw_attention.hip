@@ -1044,9 +1044,8 @@ extern "C" int sw_sparse_attention_f32(
   if (nnz > 0 && o.sddmm_lanes_per_row == 64 &&
       sw::streq(o.sddmm_mapping, "row-tile-mfma") &&
       sw::streq(o.spmm_mapping, "row-tile-mfma") && (d == 64 || d == 128) &&
-      dv > 0 && dv % 16 == 0 && 4 * nnz <= (int64_t)UINT32_MAX &&
-      4 * d * cols <= (int64_t)UINT32_MAX &&
-      4 * dv * cols <= (int64_t)UINT32_MAX) {
+      dv > 0 && dv % 16 == 0 && sw::narrow_offsets(nnz, 1) &&
+      sw::narrow_offsets(cols, d) && sw::narrow_offsets(cols, dv)) {
     // the whole chain in one kernel per 16-row tile (its loads and stores
     // take 32-bit byte offsets from wave-uniform bases)
     int64_t grid;

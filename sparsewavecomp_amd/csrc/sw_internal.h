@@ -33,6 +33,13 @@ inline bool aligned16(const void *p) {
   return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
 }
 
+// True when every byte offset into a dense operand of n rows of w floats
+// fits 32 bits, so that kernels may address it as a wave-uniform base plus a
+// 32-bit lane offset.
+inline bool narrow_offsets(int64_t n, int64_t w) {
+  return n >= 0 && w >= 0 && (w == 0 || n <= (int64_t)(UINT32_MAX / 4) / w);
+}
+
 // Largest grid dimension x we launch in one go.
 constexpr int64_t kMaxGridX = 2147483647;
 

@@ -106,6 +106,41 @@ def test_unaligned_operands(dev, orc):
         _check(orc, csr, x, y.cpu().numpy())
 
 
+def test_vector_past_four_gib(dev):
+    """Columns at and past 2^30: the 128-bit position and COO kernels address
+    x with 32-bit byte offsets only when every offset fits, so a 4 GiB+ x must
+    take the scalar-load path and still gather the right entries."""
+    cols = (1 << 30) + 64
+    rng = np.random.default_rng(5)
+    rows, per_row = 64, 8
+    pool = np.concatenate([rng.choice(1 << 20, 32, replace=False),
+                           (1 << 30) - 8 + np.arange(72)])
+    rc = [np.sort(rng.choice(pool, per_row, replace=False)) for _ in range(rows)]
+    col = np.concatenate(rc).astype(np.int32)
+    ro = np.arange(0, rows * per_row + 1, per_row, dtype=np.int32)
+    val = rng.uniform(-1, 1, col.size).astype(np.float32)
+    xs = rng.uniform(-1, 1, pool.size).astype(np.float32)
+    x = torch.zeros(cols, dtype=torch.float32, device=G.DEV)
+    x[G.t(pool.astype(np.int64))] = G.t(xs)
+    xmap = dict(zip(pool.tolist(), xs.tolist()))
+    prod = val.astype(np.float64) * np.array([xmap[c] for c in col.tolist()])
+    ref = prod.reshape(rows, per_row).sum(axis=1)
+    bound = np.abs(prod).reshape(rows, per_row).sum(axis=1)
+    ri = np.repeat(np.arange(rows, dtype=np.int32), per_row)
+    for p in (4, 8, 16):
+        opts = f"spmv-mapping=wave-per-position spmv-positions-per-lane={p}"
+        G.say(f"x of {cols} floats, {opts}")
+        y = torch.full((rows,), float("nan"), device=G.DEV)
+        sw.spmv(G.t(ro), G.t(col), G.t(val), x, y, options=opts)
+        yc = torch.full((rows,), float("nan"), device=G.DEV)
+        sw.coo_spmv(G.t(ri), G.t(col), G.t(val), x, yc, options=opts)
+        torch.cuda.synchronize()
+        assert_within_bound(y.cpu().numpy(), ref, bound)
+        assert_within_bound(yc.cpu().numpy(), ref, bound)
+    del x
+    torch.cuda.empty_cache()
+
+
 @pytest.fixture(scope="module")
 def config2():
     return W.config2(seed=0)
