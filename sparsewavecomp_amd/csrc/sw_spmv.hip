@@ -26,7 +26,21 @@ namespace {
 // then needs DEEP times fewer memory trips.
 constexpr int kRowUnroll = 4;
 
-template <int DEEP = 0>
+// x[c].  NARROW (the host's guarantee that 4 * cols fits 32 bits): the
+// wave-uniform base x plus a 32-bit lane byte offset, which the load takes
+// directly; otherwise a 64-bit lane address.  On configuration 2 the narrow
+// form measured thread-per-row 453 -> 436 us, the position mapping
+// 209.1 -> 207.7 us, wave-per-row (16 lanes) 246.3 -> 245.8 us.
+template <bool NARROW>
+__device__ __forceinline__ float gather(const float *__restrict__ x,
+                                        int32_t c) {
+  if constexpr (NARROW)
+    return *at_bytes(x, 4u * (uint32_t)c);
+  else
+    return x[c];
+}
+
+template <bool NARROW, int DEEP = 0>
 __device__ __forceinline__ float strided_dot(const int32_t *__restrict__ col,
                                              const float *__restrict__ val,
                                              const float *__restrict__ x,
@@ -43,7 +57,7 @@ __device__ __forceinline__ float strided_dot(const int32_t *__restrict__ col,
       }
 #pragma unroll
       for (int u = 0; u < DEEP; ++u)
-        xv[u] = x[c[u]];
+        xv[u] = gather<NARROW>(x, c[u]);
 #pragma unroll
       for (int u = 0; u < DEEP; ++u)
         acc = __builtin_fmaf(v[u], xv[u], acc);
@@ -59,13 +73,13 @@ __device__ __forceinline__ float strided_dot(const int32_t *__restrict__ col,
     }
 #pragma unroll
     for (int u = 0; u < kRowUnroll; ++u)
-      xv[u] = x[c[u]];
+      xv[u] = gather<NARROW>(x, c[u]);
 #pragma unroll
     for (int u = 0; u < kRowUnroll; ++u)
       acc = __builtin_fmaf(v[u], xv[u], acc);
   }
   for (; p < e; p += stride)
-    acc = __builtin_fmaf(ld_stream(val + p), x[ld_stream(col + p)], acc);
+    acc = __builtin_fmaf(ld_stream(val + p), gather<NARROW>(x, col[p]), acc);
   return acc;
 }
 
@@ -74,6 +88,7 @@ __device__ __forceinline__ float strided_dot(const int32_t *__restrict__ col,
 // Long rows take steps of kThreadRowDeep positions: the kernel's time is the
 // longest rows' chain of memory trips (config 2 has rows of 4096).
 constexpr int kThreadRowDeep = 16;
+template <bool NARROW>
 __global__ __launch_bounds__(1024) void spmv_thread_per_row(
     const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
     const float *__restrict__ val, const float *__restrict__ x,
@@ -82,7 +97,7 @@ __global__ __launch_bounds__(1024) void spmv_thread_per_row(
   if (r >= rows)
     return;
   int32_t s = ro[r], e = ro[r + 1];
-  y[r] = strided_dot<kThreadRowDeep>(col, val, x, s, e, 1, 0.0f);
+  y[r] = strided_dot<NARROW, kThreadRowDeep>(col, val, x, s, e, 1, 0.0f);
 }
 
 // ---------------------------------------------------------------------------
@@ -92,7 +107,7 @@ __global__ __launch_bounds__(1024) void spmv_thread_per_row(
 // of long rows take steps of kGroupRowDeep positions (16 lanes per row:
 // 276 -> 247 us on configuration 2, 32 lanes: 274 -> 263 us).
 constexpr int kGroupRowDeep = 16;
-template <int G>
+template <int G, bool NARROW>
 __global__ __launch_bounds__(1024) void spmv_group_per_row(
     const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
     const float *__restrict__ val, const float *__restrict__ x,
@@ -103,7 +118,8 @@ __global__ __launch_bounds__(1024) void spmv_group_per_row(
   float acc = 0.0f;
   if (r < rows) {
     int32_t s = ro[r], e = ro[r + 1];
-    acc = strided_dot<kGroupRowDeep>(col, val, x, s + gl, e, G, 0.0f);
+    acc = strided_dot<NARROW, kGroupRowDeep>(col, val, x, s + gl, e, G,
+                                             0.0f);
   }
   // every lane of the wave takes part in the butterfly
   acc = group_sum<G>(acc);
@@ -114,6 +130,7 @@ __global__ __launch_bounds__(1024) void spmv_group_per_row(
 // ---------------------------------------------------------------------------
 // block-per-row: the block strides the row, each wave reduces its partial
 // sum, partials meet in LDS, wave 0 reduces them and lane 0 stores.
+template <bool NARROW>
 __global__ __launch_bounds__(1024) void spmv_block_per_row(
     const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
     const float *__restrict__ val, const float *__restrict__ x,
@@ -125,7 +142,7 @@ __global__ __launch_bounds__(1024) void spmv_block_per_row(
   float acc = 0.0f;
   if (r < rows) {
     int32_t s = ro[r], e = ro[r + 1];
-    acc = strided_dot(col, val, x, s + t, e, B, 0.0f);
+    acc = strided_dot<NARROW>(col, val, x, s + t, e, B, 0.0f);
   }
   // blockDim.x is a multiple of 64 (validated), so every wave is full
   float w = wave_sum(acc);
@@ -319,13 +336,11 @@ __global__ __launch_bounds__(1024) void spmv_wave_position(
           vv[q + 1] = v.y;
           vv[q + 2] = v.z;
           vv[q + 3] = v.w;
-          // x[c] as the uniform base x plus a 32-bit byte offset (the host
-          // takes VEC only when 4 * cols fits 32 bits): 209.1 -> 207.7 us
-          // on configuration 2 against 64-bit lane addresses
-          xg[q + 0] = *at_bytes(x, 4u * (uint32_t)c.x);
-          xg[q + 1] = *at_bytes(x, 4u * (uint32_t)c.y);
-          xg[q + 2] = *at_bytes(x, 4u * (uint32_t)c.z);
-          xg[q + 3] = *at_bytes(x, 4u * (uint32_t)c.w);
+          // the host takes VEC only when 4 * cols fits 32 bits
+          xg[q + 0] = gather<true>(x, c.x);
+          xg[q + 1] = gather<true>(x, c.y);
+          xg[q + 2] = gather<true>(x, c.z);
+          xg[q + 3] = gather<true>(x, c.w);
         }
       }
     }
@@ -524,11 +539,11 @@ __global__ __launch_bounds__(1024) void coo_run_segmented(
         rr[q + 1] = r.y;
         rr[q + 2] = r.z;
         rr[q + 3] = r.w;
-        // 32-bit byte offsets from x (VEC only when 4 * cols fits)
-        prod[q + 0] = v.x * *at_bytes(x, 4u * (uint32_t)c.x);
-        prod[q + 1] = v.y * *at_bytes(x, 4u * (uint32_t)c.y);
-        prod[q + 2] = v.z * *at_bytes(x, 4u * (uint32_t)c.z);
-        prod[q + 3] = v.w * *at_bytes(x, 4u * (uint32_t)c.w);
+        // the host takes VEC only when 4 * cols fits 32 bits
+        prod[q + 0] = v.x * gather<true>(x, c.x);
+        prod[q + 1] = v.y * gather<true>(x, c.y);
+        prod[q + 2] = v.z * gather<true>(x, c.z);
+        prod[q + 3] = v.w * gather<true>(x, c.w);
       }
     }
   }
@@ -590,9 +605,13 @@ void launch_coo_runs(int64_t grid, int64_t B, hipStream_t st,
 template <int G>
 void launch_group(dim3 grid, dim3 block, hipStream_t st, const int32_t *ro,
                   const int32_t *col, const float *val, const float *x,
-                  float *y, int32_t rows) {
-  hipLaunchKernelGGL(spmv_group_per_row<G>, grid, block, 0, st, ro, col, val,
-                     x, y, rows);
+                  float *y, int32_t rows, bool narrow) {
+  if (narrow)
+    hipLaunchKernelGGL((spmv_group_per_row<G, true>), grid, block, 0, st, ro,
+                       col, val, x, y, rows);
+  else
+    hipLaunchKernelGGL((spmv_group_per_row<G, false>), grid, block, 0, st, ro,
+                       col, val, x, y, rows);
 }
 
 template <int P, bool VEC>
@@ -644,10 +663,16 @@ int launch_spmv(const int32_t *ro, const int32_t *col, const float *val,
                 int64_t nnz, const sw_options &o, hipStream_t st) {
   const int64_t B = o.spmv_block_size;
   const int32_t n = (int32_t)rows;
+  const bool narrow = narrow_offsets(cols, 1);
   if (streq(o.spmv_mapping, "thread-per-row")) {
     int64_t grid = std::max<int64_t>(ceil_div(rows, B), 1);
-    hipLaunchKernelGGL(spmv_thread_per_row, dim3((unsigned)grid),
-                       dim3((unsigned)B), 0, st, ro, col, val, x, y, n);
+    dim3 g((unsigned)grid), b((unsigned)B);
+    if (narrow)
+      hipLaunchKernelGGL(spmv_thread_per_row<true>, g, b, 0, st, ro, col, val,
+                         x, y, n);
+    else
+      hipLaunchKernelGGL(spmv_thread_per_row<false>, g, b, 0, st, ro, col, val,
+                         x, y, n);
     return launch_check("thread-per-row SpMV kernel");
   }
   if (streq(o.spmv_mapping, "wave-per-row")) {
@@ -658,13 +683,13 @@ int launch_spmv(const int32_t *ro, const int32_t *col, const float *val,
       return rc;
     dim3 g((unsigned)grid), b((unsigned)B);
     switch (G) {
-    case 1: launch_group<1>(g, b, st, ro, col, val, x, y, n); break;
-    case 2: launch_group<2>(g, b, st, ro, col, val, x, y, n); break;
-    case 4: launch_group<4>(g, b, st, ro, col, val, x, y, n); break;
-    case 8: launch_group<8>(g, b, st, ro, col, val, x, y, n); break;
-    case 16: launch_group<16>(g, b, st, ro, col, val, x, y, n); break;
-    case 32: launch_group<32>(g, b, st, ro, col, val, x, y, n); break;
-    default: launch_group<64>(g, b, st, ro, col, val, x, y, n); break;
+    case 1: launch_group<1>(g, b, st, ro, col, val, x, y, n, narrow); break;
+    case 2: launch_group<2>(g, b, st, ro, col, val, x, y, n, narrow); break;
+    case 4: launch_group<4>(g, b, st, ro, col, val, x, y, n, narrow); break;
+    case 8: launch_group<8>(g, b, st, ro, col, val, x, y, n, narrow); break;
+    case 16: launch_group<16>(g, b, st, ro, col, val, x, y, n, narrow); break;
+    case 32: launch_group<32>(g, b, st, ro, col, val, x, y, n, narrow); break;
+    default: launch_group<64>(g, b, st, ro, col, val, x, y, n, narrow); break;
     }
     return launch_check("wave-per-row SpMV kernel");
   }
@@ -673,8 +698,13 @@ int launch_spmv(const int32_t *ro, const int32_t *col, const float *val,
     int rc = check_grid(grid, "block-per-row SpMV");
     if (rc)
       return rc;
-    hipLaunchKernelGGL(spmv_block_per_row, dim3((unsigned)grid),
-                       dim3((unsigned)B), 0, st, ro, col, val, x, y, n);
+    dim3 g((unsigned)grid), b((unsigned)B);
+    if (narrow)
+      hipLaunchKernelGGL(spmv_block_per_row<true>, g, b, 0, st, ro, col, val,
+                         x, y, n);
+    else
+      hipLaunchKernelGGL(spmv_block_per_row<false>, g, b, 0, st, ro, col, val,
+                         x, y, n);
     return launch_check("block-per-row SpMV kernel");
   }
   int rc;
@@ -714,8 +744,7 @@ int launch_spmv(const int32_t *ro, const int32_t *col, const float *val,
     return rc;
   if (nnz == 0)
     return SW_OK;
-  const bool vec =
-      aligned16(col) && aligned16(val) && narrow_offsets(cols, 1);
+  const bool vec = aligned16(col) && aligned16(val) && narrow;
   dim3 g((unsigned)grid), b((unsigned)B);
   const int32_t z = (int32_t)nnz;
   switch (P) {

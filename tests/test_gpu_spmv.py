@@ -107,9 +107,9 @@ def test_unaligned_operands(dev, orc):
 
 
 def test_vector_past_four_gib(dev):
-    """Columns at and past 2^30: the 128-bit position and COO kernels address
-    x with 32-bit byte offsets only when every offset fits, so a 4 GiB+ x must
-    take the scalar-load path and still gather the right entries."""
+    """Columns at and past 2^30: the kernels address x with 32-bit byte
+    offsets only when every offset fits, so a 4 GiB+ x must take their 64-bit
+    form and still gather the right entries."""
     cols = (1 << 30) + 64
     rng = np.random.default_rng(5)
     rows, per_row = 64, 8
@@ -137,6 +137,14 @@ def test_vector_past_four_gib(dev):
         torch.cuda.synchronize()
         assert_within_bound(y.cpu().numpy(), ref, bound)
         assert_within_bound(yc.cpu().numpy(), ref, bound)
+    for opts in ("spmv-mapping=thread-per-row", "spmv-mapping=wave-per-row",
+                 "spmv-mapping=wave-per-row spmv-lanes-per-row=4",
+                 "spmv-mapping=block-per-row spmv-block-size=128"):
+        G.say(f"x of {cols} floats, {opts}")
+        y = torch.full((rows,), float("nan"), device=G.DEV)
+        sw.spmv(G.t(ro), G.t(col), G.t(val), x, y, options=opts)
+        torch.cuda.synchronize()
+        assert_within_bound(y.cpu().numpy(), ref, bound)
     del x
     torch.cuda.empty_cache()
 
