@@ -21,8 +21,8 @@ using namespace swd;
 
 namespace sw {
 int launch_spmm(const int32_t *ro, const int32_t *col, const float *val,
-                const float *rhs, float *out, int64_t rows, int64_t nnz,
-                int64_t k, const sw_options &o, const char *what,
+                const float *rhs, float *out, int64_t rows, int64_t rhs_rows,
+                int64_t nnz, int64_t k, const sw_options &o, const char *what,
                 hipStream_t st);
 }
 
@@ -1087,7 +1087,8 @@ extern "C" int sw_sparse_attention_f32(
     if (dv == 0)
       return SW_OK;
     return sw::launch_spmm(row_offsets, column_indices, scores, value, output,
-                           rows, nnz, dv, o, "attention output SpMM", st);
+                           rows, cols, nnz, dv, o, "attention output SpMM",
+                           st);
   }
   rc = sw::launch_row_reduce(row_offsets, scores, row_maximum, rows, true, o, st);
   if (rc)
@@ -1110,5 +1111,5 @@ extern "C" int sw_sparse_attention_f32(
   if (dv == 0)
     return SW_OK;
   return sw::launch_spmm(row_offsets, column_indices, scores, value, output,
-                         rows, nnz, dv, o, "attention output SpMM", st);
+                         rows, cols, nnz, dv, o, "attention output SpMM", st);
 }

@@ -101,6 +101,41 @@ def test_ragged(dev, orc, opts, k):
     _check(orc, csr, rhs, G.spmm(csr, rhs, opts))
 
 
+def test_rhs_past_four_gib(dev):
+    """A 4 GiB+ right-hand side: kernels that address B with 32-bit byte
+    offsets when 4 * rows(B) * K fits must take their 64-bit form here."""
+    import torch
+    import sparsewavecomp_amd as sw
+    k = 64
+    brows = (1 << 24) + 32          # 4 * brows * k > 2^32
+    rng = np.random.default_rng(9)
+    rows, per_row = 32, 8
+    pool = np.concatenate([rng.choice(1 << 16, 16, replace=False),
+                           (1 << 24) - 16 + np.arange(48)])
+    rc = [np.sort(rng.choice(pool, per_row, replace=False)) for _ in range(rows)]
+    col = np.concatenate(rc).astype(np.int32)
+    ro = np.arange(0, rows * per_row + 1, per_row, dtype=np.int32)
+    val = rng.uniform(-1, 1, col.size).astype(np.float32)
+    bp = rng.uniform(-1, 1, (pool.size, k)).astype(np.float32)
+    rhs = torch.zeros((brows, k), dtype=torch.float32, device=G.DEV)
+    rhs[G.t(pool.astype(np.int64))] = G.t(bp)
+    where = {c: j for j, c in enumerate(pool.tolist())}
+    bg = bp[[where[c] for c in col.tolist()]].astype(np.float64)
+    prod = val.astype(np.float64)[:, None] * bg
+    ref = prod.reshape(rows, per_row, k).sum(axis=1)
+    bound = np.abs(prod).reshape(rows, per_row, k).sum(axis=1)
+    for opts in ("spmm-mapping=thread-per-output",
+                 "spmm-mapping=wave-per-row-tile spmm-tile-size=32",
+                 "spmm-mapping=wave-per-position"):
+        G.say(f"rhs of {brows} x {k}, {opts}")
+        out = torch.full((rows, k), float("nan"), device=G.DEV)
+        sw.spmm(G.t(ro), G.t(col), G.t(val), rhs, out, options=opts)
+        torch.cuda.synchronize()
+        assert_within_bound(out.cpu().numpy(), ref, bound)
+    del rhs
+    torch.cuda.empty_cache()
+
+
 @pytest.fixture(scope="module")
 def config3():
     csr, _ = W.config2(seed=0)
