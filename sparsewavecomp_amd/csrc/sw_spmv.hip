@@ -329,9 +329,13 @@ __global__ __launch_bounds__(1024) void spmv_wave_position(
           // values non-temporal, columns plain: the same speed as plain
           // loads for both (209.8 us on configuration 2 at P = 8) with 14%
           // less L2-to-fabric traffic (x stays in L2 longer: hit rate 82.5%
-          // against 79.2%); non-temporal columns as well measured 218 us
-          v4i c = ld_stream(reinterpret_cast<const v4i *>(col + p0 + q));
-          v4f v = ld_nontemporal(reinterpret_cast<const v4f *>(val + p0 + q));
+          // against 79.2%); non-temporal columns as well measured 218 us.
+          // Both as a uniform base plus a 32-bit byte offset (VEC implies
+          // 4 * nnz fits): 207.4 -> 206.9 us
+          const uint32_t bo = 4u * (uint32_t)(p0 + q);
+          v4i c = ld_stream(at_bytes(reinterpret_cast<const v4i *>(col), bo));
+          v4f v =
+              ld_nontemporal(at_bytes(reinterpret_cast<const v4f *>(val), bo));
           vv[q + 0] = v.x;
           vv[q + 1] = v.y;
           vv[q + 2] = v.z;
@@ -744,7 +748,8 @@ int launch_spmv(const int32_t *ro, const int32_t *col, const float *val,
     return rc;
   if (nnz == 0)
     return SW_OK;
-  const bool vec = aligned16(col) && aligned16(val) && narrow;
+  const bool vec = aligned16(col) && aligned16(val) && narrow &&
+                   narrow_offsets(nnz, 1);
   dim3 g((unsigned)grid), b((unsigned)B);
   const int32_t z = (int32_t)nnz;
   switch (P) {

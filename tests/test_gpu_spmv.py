@@ -149,6 +149,35 @@ def test_vector_past_four_gib(dev):
     torch.cuda.empty_cache()
 
 
+def test_positions_past_four_gib(dev):
+    """More than 2^30 nonzeros: the position kernel reads columns and values
+    with 32-bit byte offsets only when 4 * nnz fits, so this matrix must take
+    its 64-bit form.  Values and x are ones, so y is each row's length,
+    exact in fp32 (rows of 1024 or 1088 entries)."""
+    rows = 1 << 20
+    lengths = torch.full((rows,), 1024, dtype=torch.int64, device=G.DEV)
+    lengths[-1] += 64                    # nnz = 2^30 + 64
+    ro = torch.zeros(rows + 1, dtype=torch.int64, device=G.DEV)
+    ro[1:] = torch.cumsum(lengths, 0)
+    nnz = int(ro[-1])
+    cols = 1 << 16
+    col = (torch.arange(nnz, device=G.DEV, dtype=torch.int64) % cols).to(
+        torch.int32)
+    val = torch.ones(nnz, dtype=torch.float32, device=G.DEV)
+    x = torch.ones(cols, dtype=torch.float32, device=G.DEV)
+    ro32 = ro.to(torch.int32)
+    del ro
+    for p in (4, 8):
+        opts = f"spmv-mapping=wave-per-position spmv-positions-per-lane={p}"
+        G.say(f"nnz={nnz}, {opts}")
+        y = torch.full((rows,), float("nan"), device=G.DEV)
+        sw.spmv(ro32, col, val, x, y, options=opts)
+        torch.cuda.synchronize()
+        assert torch.equal(y, lengths.to(torch.float32))
+    del col, val
+    torch.cuda.empty_cache()
+
+
 @pytest.fixture(scope="module")
 def config2():
     return W.config2(seed=0)
