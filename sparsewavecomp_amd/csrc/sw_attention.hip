@@ -325,17 +325,6 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
-// Maximum over aligned groups of 32 lanes, every lane of a group receiving
-// it (the 32-lane half of wave_max).
-__device__ __forceinline__ float group_max32(float v) {
-  v = maximumf(v, dpp_f<kQuadXor1>(-INFINITY, v));
-  v = maximumf(v, dpp_f<kQuadXor2>(-INFINITY, v));
-  v = maximumf(v, dpp_f<kRowHalfMirror>(-INFINITY, v));
-  v = maximumf(v, dpp_f<kRowMirror>(-INFINITY, v));
-  v = maximumf(v, swizzle_xor16(v));
-  return v;
-}
-
 template <bool MAX>
 __global__ __launch_bounds__(256) void row_reduce_wave(
     const int32_t *__restrict__ ro, const float *__restrict__ val,
