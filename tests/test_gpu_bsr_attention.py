@@ -382,6 +382,52 @@ def test_attention_fused_paths(dev, orc, shape, d, dv):
     _check_attention(orc, csr, *_attention_case(orc, csr, d, dv, FUSED))
 
 
+@pytest.mark.parametrize("opts", [FUSED] + ATT_OPTS[:2])
+def test_attention_masked_out_entries(dev, orc, opts):
+    """Mask values of -inf with beta = 1 (entries masked out) follow IEEE
+    arithmetic as the reference's ops do: a masked entry's probability is 0,
+    and a row whose entries are all masked has row maximum -inf and NaN row
+    sum, probabilities and output."""
+    csr = _tile_structure_csr()
+    rng = np.random.default_rng(77)
+    mask = rng.uniform(-1, 1, csr.nnz).astype(np.float32)
+    mask[rng.random(csr.nnz) < 0.2] = -np.inf
+    lens = np.diff(csr.row_offsets)
+    dead = int(np.flatnonzero(lens > 20)[1])       # a row of a shared tile
+    mask[csr.row_offsets[dead]:csr.row_offsets[dead + 1]] = -np.inf
+    d = dv = 64
+    q = rng.standard_normal((csr.rows, d)).astype(np.float32)
+    kt = rng.standard_normal((d, csr.cols)).astype(np.float32)
+    v = rng.standard_normal((csr.cols, dv)).astype(np.float32)
+    alpha, beta = 0.125, 1.0
+    G.say(f"attention with masked entries opts={opts!r}")
+    nan = float("nan")
+    scores = torch.full((csr.nnz,), nan, device=G.DEV)
+    rmax = torch.full((csr.rows,), nan, device=G.DEV)
+    rsum = torch.full((csr.rows,), nan, device=G.DEV)
+    out = torch.full((csr.rows, dv), nan, device=G.DEV)
+    sw.sparse_attention(G.t(csr.row_offsets), G.t(csr.column_indices),
+                        G.t(mask), G.t(q), G.t(kt), G.t(v), scores, rmax,
+                        rsum, out, alpha, beta, options=opts)
+    torch.cuda.synchronize()
+    s_ref, m_ref, sum_ref, ref = orc.sparse_attention(
+        csr.row_offsets, csr.column_indices, mask, q, kt, v, alpha, beta)
+    np.testing.assert_allclose(scores.cpu().numpy(), s_ref, rtol=1e-4,
+                               atol=1e-6, equal_nan=True)
+    np.testing.assert_allclose(rmax.cpu().numpy(), m_ref, rtol=1e-5,
+                               atol=1e-5, equal_nan=True)
+    np.testing.assert_allclose(rsum.cpu().numpy(), sum_ref, rtol=1e-4,
+                               equal_nan=True)
+    assert m_ref[dead] == -np.inf and np.isnan(sum_ref[dead])
+    o = out.cpu().numpy()
+    assert np.isnan(o[dead]).all() and np.isnan(ref[dead]).all()
+    live = np.ones(csr.rows, bool)
+    live[dead] = False
+    bound = orc.spmm_abs_bound(csr.row_offsets, csr.column_indices,
+                               np.nan_to_num(s_ref), v)
+    assert_within_bound(o[live], ref[live], bound[live], rel=2e-5)
+
+
 def _check_attention(orc, csr, scores, rmax, rsum, out, refs, v):
     s_ref, m_ref, sum_ref, ref = refs
     bound = orc.spmm_abs_bound(csr.row_offsets, csr.column_indices, s_ref, v)
