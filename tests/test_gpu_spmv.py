@@ -87,6 +87,37 @@ def test_edge_shapes(dev, orc, opts):
         _check(orc, csr, x, G.spmv(csr, x, opts))
 
 
+@pytest.mark.parametrize("opts", MAPPINGS)
+def test_non_finite_values(dev, orc, opts):
+    """inf and NaN in the values and the vector propagate as in the
+    reference's sequential sum: a row is NaN, +inf or -inf exactly when the
+    oracle's is (any summation order gives the same class), and finite rows
+    meet the usual bound."""
+    csr = W.random_csr(2000, 1500, 12.0, 8, empty_fraction=0.1,
+                       max_len=600, lognormal=True)
+    rng = np.random.default_rng(8)
+    val = csr.values.copy()
+    pick = rng.choice(csr.nnz, 40, replace=False)
+    val[pick[:15]] = np.inf
+    val[pick[15:30]] = -np.inf
+    val[pick[30:]] = np.nan
+    csr = W.CSR(csr.rows, csr.cols, csr.row_offsets, csr.column_indices, val)
+    x = rng.uniform(-1, 1, csr.cols).astype(np.float32)
+    x[rng.choice(csr.cols, 5, replace=False)] = np.nan
+    ref = orc.spmv(csr.row_offsets, csr.column_indices, csr.values, x)
+    y = G.spmv(csr, x, opts)
+    fin = np.isfinite(ref)
+    assert np.array_equal(np.isnan(y), np.isnan(ref))
+    assert np.array_equal(np.isposinf(y), np.isposinf(ref))
+    assert np.array_equal(np.isneginf(y), np.isneginf(ref))
+    assert (~fin).sum() > 10
+    ok = W.CSR(csr.rows, csr.cols, csr.row_offsets, csr.column_indices,
+               np.where(np.isfinite(val), val, 0).astype(np.float32))
+    bound = orc.spmv_abs_bound(ok.row_offsets, ok.column_indices, ok.values,
+                               np.nan_to_num(x))
+    assert_within_bound(y[fin], ref[fin], bound[fin])
+
+
 def test_unaligned_operands(dev, orc):
     """col/val starting at an odd element take the scalar-load path."""
     csr, x = W.config1(seed=3)
