@@ -101,6 +101,35 @@ def test_ragged(dev, orc, opts, k):
     _check(orc, csr, rhs, G.spmm(csr, rhs, opts))
 
 
+@pytest.mark.parametrize("opts", MAPPINGS)
+def test_non_finite_values(dev, orc, opts):
+    """inf and NaN in the values and in B propagate per output element as in
+    the reference's sequential sum (the class NaN / +inf / -inf does not
+    depend on the order); finite elements meet the usual bound."""
+    k = 8
+    csr = W.random_csr(600, 500, 12.0, 12, empty_fraction=0.1, max_len=400,
+                       lognormal=True)
+    rng = np.random.default_rng(12)
+    val = csr.values.copy()
+    pick = rng.choice(csr.nnz, 24, replace=False)
+    val[pick[:8]] = np.inf
+    val[pick[8:16]] = -np.inf
+    val[pick[16:]] = np.nan
+    csr = W.CSR(csr.rows, csr.cols, csr.row_offsets, csr.column_indices, val)
+    rhs = rng.uniform(-1, 1, (csr.cols, k)).astype(np.float32)
+    rhs[rng.choice(csr.cols, 4, replace=False), rng.integers(0, k, 4)] = np.nan
+    ref = orc.spmm(csr.row_offsets, csr.column_indices, csr.values, rhs)
+    out = G.spmm(csr, rhs, opts)
+    for cls in (np.isnan, np.isposinf, np.isneginf):
+        assert np.array_equal(cls(out), cls(ref))
+    fin = np.isfinite(ref)
+    assert (~fin).sum() > 20
+    bound = orc.spmm_abs_bound(csr.row_offsets, csr.column_indices,
+                               np.where(np.isfinite(val), val, 0).astype(
+                                   np.float32), np.nan_to_num(rhs))
+    assert_within_bound(out[fin], ref[fin], bound[fin])
+
+
 def test_rhs_past_four_gib(dev):
     """A 4 GiB+ right-hand side: kernels that address B with 32-bit byte
     offsets when 4 * rows(B) * K fits must take their 64-bit form here."""
