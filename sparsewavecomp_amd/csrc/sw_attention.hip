@@ -525,6 +525,7 @@ __global__ __launch_bounds__(64 * W) void attention_tile_fused(
   __shared__ float wred[2][W][16];       // [max, sum][wave][row]
   __shared__ int32_t lcol[kFusedCols];   // the last row's columns
   __shared__ int verdict;
+  __shared__ int v_nonfinite; // a V value of the tile is inf or NaN
   const int r0 = blockIdx.x * 16;
   const int nt = std::min(16, rows - r0);
   const int wave = threadIdx.x / kWave;
@@ -556,8 +557,10 @@ __global__ __launch_bounds__(64 * W) void attention_tile_fused(
   // row to LDS, where both products read their K / V row indices.
   bool ok = len_last <= kFusedCols; // workgroup-uniform
   if (ok) {
-    if (threadIdx.x == 0)
+    if (threadIdx.x == 0) {
       verdict = 1;
+      v_nonfinite = 0;
+    }
     int32_t x[2][8], yl[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
@@ -770,6 +773,14 @@ __global__ __launch_bounds__(64 * W) void attention_tile_fused(
             acc[n] = __builtin_amdgcn_mfma_f32_16x16x4f32(
                 sv[2 * it + h][st], b[h][n][st], acc[n], 0, 0, 0);
   };
+  // The rows of a tile share each MFMA's V operand, so an inf or NaN in a V
+  // row that a shorter row of the tile leaves out would reach that row as
+  // 0 * inf.  The tile's last row holds every entry, so such a value makes
+  // some output of the tile non-finite: a tile with a non-finite output
+  // has it recomputed row by row from the stored scores, adding exactly
+  // each row's own entries (the same values wherever the MFMA result was
+  // right).
+  bool nonfinite = false;
   for (int64_t nb = 0; nb < dv; nb += 64) {
     const int ntiles = (int)std::min<int64_t>(4, (dv - nb) / 16);
     v4f acc[4];
@@ -785,7 +796,7 @@ __global__ __launch_bounds__(64 * W) void attention_tile_fused(
       load_v(1, nb, bv);
       __builtin_amdgcn_sched_barrier(0);
       mfma_pair(1, bv, acc);
-    }
+      }
 #pragma unroll
     for (int n = 0; n < 4; ++n)
 #pragma unroll
@@ -800,12 +811,21 @@ __global__ __launch_bounds__(64 * W) void attention_tile_fused(
         for (int w = 0; w < W; ++w)
           sum += part[w][wave][v][l];
         const int rr = 4 * g + v;
-        if (rr < nt)
+        if (rr < nt) {
           out[(int64_t)(r0 + rr) * dv + nb + 16 * wave + i] = sum;
+          nonfinite |= !__builtin_isfinite(sum);
+        }
       }
+      if (__builtin_amdgcn_ballot_w64(nonfinite) != 0 && l == 0)
+        v_nonfinite = 1;
     }
     __syncthreads();
   }
+  // workgroup-uniform; the barrier above also made every wave's stored
+  // scores visible to the others
+  if (v_nonfinite != 0)
+    for (int r = r0 + wave; r < r0 + nt; r += W)
+      attention_row_output(ro, col, scores, value, out, r, dv);
 }
 
 int grid_for(int64_t work, int64_t per_block, const char *what,

@@ -549,11 +549,15 @@ __global__ __launch_bounds__(64 * W) void spmm_tile_mfma(
   const int32_t ra = ro[r0 + ic];
   const int32_t la = i < nt ? ro[r0 + ic + 1] - ra : 0;
   __shared__ int verdict;
+  __shared__ int nonfinite_out; // an output of the tile is inf or NaN
+  if (threadIdx.x == 0)
+    nonfinite_out = 0; // read only after the check's barriers
   if (!tile_prefix_ok_block(ro, col, r0, nt, &verdict)) {
     for (int r = r0 + wave; r < r0 + nt; r += W)
       spmm_row_wave(ro, col, val, rhs, out, r, k);
     return;
   }
+  bool nonfinite = false;
   for (int64_t nb = 0; nb < k; nb += 64) {
     const int ntiles = (int)std::min<int64_t>(4, (k - nb) / 16);
     v4f acc[4];
@@ -614,12 +618,23 @@ __global__ __launch_bounds__(64 * W) void spmm_tile_mfma(
         for (int w = 0; w < W; ++w)
           sum += part[w][wave][v][l];
         const int rr = 4 * g + v;
-        if (rr < nt)
+        if (rr < nt) {
           out[(int64_t)(r0 + rr) * k + nb + 16 * wave + i] = sum;
+          nonfinite |= !__builtin_isfinite(sum);
+        }
       }
+      if (__builtin_amdgcn_ballot_w64(nonfinite) != 0 && lane_id() == 0)
+        nonfinite_out = 1;
     }
     __syncthreads();
   }
+  // The tile's rows share each MFMA's B operand, so an inf or NaN in a B row
+  // that a shorter row leaves out reaches that row as 0 * inf; the last row
+  // holds every entry, so the tile then has a non-finite output.  Such a
+  // tile is recomputed row by row, adding exactly each row's own entries.
+  if (nonfinite_out != 0) // workgroup-uniform after the barrier above
+    for (int r = r0 + wave; r < r0 + nt; r += W)
+      spmm_row_wave(ro, col, val, rhs, out, r, k);
 }
 
 

@@ -428,6 +428,48 @@ def test_attention_masked_out_entries(dev, orc, opts):
     assert_within_bound(o[live], ref[live], bound[live], rel=2e-5)
 
 
+@pytest.mark.parametrize("opts", [FUSED] + ATT_OPTS[:2])
+def test_attention_non_finite_value_rows(dev, orc, opts):
+    """inf / NaN in V rows that a tile's last row includes but its shorter
+    rows leave out: only the rows whose entries name them become non-finite,
+    as in the reference (the fused kernel recomputes such a tile's output
+    row by row)."""
+    csr = _tile_structure_csr()
+    rng = np.random.default_rng(78)
+    d = dv = 64
+    q = rng.standard_normal((csr.rows, d)).astype(np.float32)
+    kt = rng.standard_normal((d, csr.cols)).astype(np.float32)
+    v = rng.standard_normal((csr.cols, dv)).astype(np.float32)
+    last = csr.column_indices[csr.row_offsets[15]:csr.row_offsets[16]]
+    v[last[150], 3] = np.inf           # rows 0..15: only those past 150
+    v[last[120], 7] = np.nan
+    v[last[190], :] = -np.inf
+    alpha, beta = 0.125, 0.5
+    G.say(f"attention with non-finite V rows opts={opts!r}")
+    nan = float("nan")
+    scores = torch.full((csr.nnz,), nan, device=G.DEV)
+    rmax = torch.full((csr.rows,), nan, device=G.DEV)
+    rsum = torch.full((csr.rows,), nan, device=G.DEV)
+    out = torch.full((csr.rows, dv), nan, device=G.DEV)
+    sw.sparse_attention(G.t(csr.row_offsets), G.t(csr.column_indices),
+                        G.t(csr.values), G.t(q), G.t(kt), G.t(v), scores,
+                        rmax, rsum, out, alpha, beta, options=opts)
+    torch.cuda.synchronize()
+    s_ref, m_ref, sum_ref, ref = orc.sparse_attention(
+        csr.row_offsets, csr.column_indices, csr.values, q, kt, v, alpha,
+        beta)
+    o = out.cpu().numpy()
+    for cls in (np.isnan, np.isposinf, np.isneginf):
+        assert np.array_equal(cls(o), cls(ref))
+    fin = np.isfinite(ref)
+    assert (~fin).any() and fin[:15].any()
+    bound = orc.spmm_abs_bound(csr.row_offsets, csr.column_indices, s_ref,
+                               np.nan_to_num(v, posinf=0, neginf=0))
+    assert_within_bound(o[fin], ref[fin], bound[fin], rel=2e-5)
+    np.testing.assert_allclose(scores.cpu().numpy(), s_ref, rtol=1e-4,
+                               atol=1e-6)
+
+
 def _check_attention(orc, csr, scores, rmax, rsum, out, refs, v):
     s_ref, m_ref, sum_ref, ref = refs
     bound = orc.spmm_abs_bound(csr.row_offsets, csr.column_indices, s_ref, v)

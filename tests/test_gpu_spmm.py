@@ -101,6 +101,36 @@ def test_ragged(dev, orc, opts, k):
     _check(orc, csr, rhs, G.spmm(csr, rhs, opts))
 
 
+@pytest.mark.parametrize("opts", ["spmm-mapping=row-tile-mfma",
+                                  "spmm-mapping=thread-per-output"])
+@pytest.mark.parametrize("k", [16, 64, 80])
+def test_block_structured_non_finite_rhs(dev, orc, opts, k):
+    """inf / NaN in B rows that the causal diagonal block of a 16-row tile
+    names for its longer rows only: just the rows holding those entries are
+    non-finite, as in the reference (the MFMA tiles that meet a non-finite
+    output are recomputed row by row)."""
+    mask = W.attention_mask(seq=512, block=64, window=3, random_blocks=1,
+                            seed=5)
+    rng = np.random.default_rng(k + 1)
+    vals = rng.uniform(-1, 1, mask.nnz).astype(np.float32)
+    csr = W.CSR(mask.rows, mask.cols, mask.row_offsets,
+                mask.column_indices, vals)
+    rhs = rng.uniform(-1, 1, (mask.cols, k)).astype(np.float32)
+    rhs[70, 1] = np.inf       # diagonal block of rows 64..127: rows >= 70
+    rhs[200, k - 1] = np.nan
+    rhs[333, :] = -np.inf
+    ref = orc.spmm(csr.row_offsets, csr.column_indices, csr.values, rhs)
+    out = G.spmm(csr, rhs, opts)
+    for cls in (np.isnan, np.isposinf, np.isneginf):
+        assert np.array_equal(cls(out), cls(ref))
+    fin = np.isfinite(ref)
+    assert (~fin).any() and fin[64:70].all()
+    bound = orc.spmm_abs_bound(csr.row_offsets, csr.column_indices,
+                               csr.values, np.nan_to_num(rhs, posinf=0,
+                                                         neginf=0))
+    assert_within_bound(out[fin], ref[fin], bound[fin])
+
+
 @pytest.mark.parametrize("opts", MAPPINGS)
 def test_non_finite_values(dev, orc, opts):
     """inf and NaN in the values and in B propagate per output element as in
