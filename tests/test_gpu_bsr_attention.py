@@ -60,6 +60,39 @@ def test_bsr_fp32(dev, orc, opts, b, k):
     assert_within_bound(out, ref, bound)
 
 
+@pytest.mark.parametrize("opts", BSR_OPTS)
+@pytest.mark.parametrize("k", [128, 30])
+def test_bsr_non_finite(dev, orc, opts, k):
+    """inf / NaN in block values and in B: each output is NaN / +inf / -inf
+    exactly when the oracle's is.  Stored blocks are dense, so an explicit
+    zero of a block times an inf of B is NaN in the reference as well."""
+    b = 16
+    bsr = W.bsr_banded(seed=k, rows=b * 64, block_size=b, blocks_per_row=6,
+                       band=3, band_blocks=3, value_std=0.5)
+    rng = np.random.default_rng(k + 2)
+    vals = bsr.block_values.copy()
+    flat = vals.reshape(-1)
+    pick = rng.choice(flat.size, 6, replace=False)
+    flat[pick[:2]] = np.inf
+    flat[pick[2:4]] = -np.inf
+    flat[pick[4:]] = np.nan
+    bsr = W.BSR(bsr.rows, bsr.cols, b, bsr.block_row_offsets,
+                bsr.block_column_indices, vals)
+    rhs = rng.standard_normal((bsr.cols, k)).astype(np.float32)
+    rhs[rng.integers(0, bsr.cols), rng.integers(0, k)] = np.inf
+    out = _bsr_run(bsr, rhs, opts)
+    ref = orc.bsr_spmm(bsr.block_row_offsets, bsr.block_column_indices,
+                       bsr.block_values, rhs, b)
+    for cls in (np.isnan, np.isposinf, np.isneginf):
+        assert np.array_equal(cls(out), cls(ref))
+    fin = np.isfinite(ref)
+    assert (~fin).any() and fin.any()
+    bound = orc.bsr_abs_bound(bsr.block_row_offsets, bsr.block_column_indices,
+                              np.nan_to_num(vals, posinf=0, neginf=0),
+                              np.nan_to_num(rhs, posinf=0, neginf=0), b)
+    assert_within_bound(out[fin], ref[fin], bound[fin])
+
+
 @pytest.mark.parametrize("opts", ["bsr-use-mfma=1", "bsr-use-mfma=0"])
 @pytest.mark.parametrize("k", [128, 36, 30])
 def test_bsr_bf16(dev, orc, opts, k):

@@ -73,6 +73,36 @@ def test_ragged(dev, orc, opts, order):
 
 
 @pytest.mark.parametrize("opts", MAPPINGS)
+@pytest.mark.parametrize("order", ["sorted", "shuffled"])
+def test_non_finite_values(dev, orc, opts, order):
+    """inf and NaN in values and x: a row is NaN / +inf / -inf exactly when
+    the oracle's is (any summation order gives the same class)."""
+    csr = W.random_csr(1500, 1200, 10.0, 21, empty_fraction=0.1,
+                       max_len=500, lognormal=True)
+    ri, ci, val = _coo(csr)
+    rng = np.random.default_rng(22)
+    val = val.copy()
+    pick = rng.choice(val.size, 30, replace=False)
+    val[pick[:10]] = np.inf
+    val[pick[10:20]] = -np.inf
+    val[pick[20:]] = np.nan
+    x = rng.uniform(-1, 1, csr.cols).astype(np.float32)
+    x[rng.choice(csr.cols, 4, replace=False)] = np.nan
+    if order == "shuffled":
+        p = rng.permutation(ri.size)
+        ri, ci, val = ri[p], ci[p], val[p]
+    y = _run(csr.rows, ri, ci, val, x, opts)
+    ref, bound = orc.spmv_coo(csr.rows, ri, ci, val, x)
+    for cls in (np.isnan, np.isposinf, np.isneginf):
+        assert np.array_equal(cls(y), cls(ref))
+    fin = np.isfinite(ref)
+    assert (~fin).sum() > 10
+    _, fbound = orc.spmv_coo(csr.rows, ri, ci, np.where(
+        np.isfinite(val), val, 0).astype(np.float32), np.nan_to_num(x))
+    assert_within_bound(y[fin], ref[fin], fbound[fin])
+
+
+@pytest.mark.parametrize("opts", MAPPINGS)
 def test_duplicates_and_edges(dev, orc, opts):
     rng = np.random.default_rng(10)
     x = rng.uniform(-1, 1, 64).astype(np.float32)
