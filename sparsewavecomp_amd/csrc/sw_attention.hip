@@ -796,7 +796,7 @@ __global__ __launch_bounds__(64 * W) void attention_tile_fused(
       load_v(1, nb, bv);
       __builtin_amdgcn_sched_barrier(0);
       mfma_pair(1, bv, acc);
-      }
+    }
 #pragma unroll
     for (int n = 0; n < 4; ++n)
 #pragma unroll
