@@ -118,6 +118,34 @@ def test_non_finite_values(dev, orc, opts):
     assert_within_bound(y[fin], ref[fin], bound[fin])
 
 
+def test_runs_on_the_current_stream(dev, orc):
+    """Without a stream argument the launch goes to torch's current stream
+    (also inside a `torch.cuda.stream` context); with one, to that stream.
+    Each launch is queued behind a matrix product and a NaN fill on the
+    side stream, so a launch on any other stream would run first and leave
+    NaN behind."""
+    csr, x = W.config1(seed=4)
+    ro, col, val = G.t(csr.row_offsets), G.t(csr.column_indices), G.t(
+        csr.values)
+    xv = G.t(x)
+    ref = orc.spmv(csr.row_offsets, csr.column_indices, csr.values, x)
+    bound = orc.spmv_abs_bound(csr.row_offsets, csr.column_indices,
+                               csr.values, x)
+    side = torch.cuda.Stream()
+    busy = torch.ones((4096, 4096), device=G.DEV)
+    for explicit in (False, True):
+        y = torch.empty(csr.rows, device=G.DEV)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(side):
+            torch.mm(busy, busy)             # about a millisecond of work
+            y.fill_(float("nan"))
+            sw.spmv(ro, col, val, xv, y,
+                    options="spmv-mapping=wave-per-position",
+                    stream=side if explicit else None)
+        side.synchronize()
+        assert_within_bound(y.cpu().numpy(), ref, bound)
+
+
 def test_unaligned_operands(dev, orc):
     """col/val starting at an odd element take the scalar-load path."""
     csr, x = W.config1(seed=3)
