@@ -61,7 +61,8 @@ def parse():
                          "harness's SuiteSparse workloads)")
     ap.add_argument("--profile", default="",
                     choices=["", "spmv", "floor", "coo", "spmm", "bsr",
-                             "bsr-bf16", "attention", "copy"],
+                             "bsr-bf16", "bsr-bf16-f32out", "attention",
+                             "attention-bf16", "copy"],
                     help="run one workload --steps times with no timing or "
                          "JSON (for rocprofv3 kernel-trace / pmc runs)")
     ap.add_argument("--opts", default="",
@@ -130,23 +131,26 @@ def profile(args):
             out = torch.empty((csr.rows, args.k), device=dev)
             for _ in range(n):
                 sw.spmm(ro, col, val, rhs, out, options=o)
-    elif w in ("bsr", "bsr-bf16"):
+    elif w in ("bsr", "bsr-bf16", "bsr-bf16-f32out"):
         bsr, rhs = W.config4(seed=0)
-        dt = torch.bfloat16 if w == "bsr-bf16" else None
+        dt = torch.bfloat16 if w != "bsr" else None
         a4 = (T(bsr.block_row_offsets), T(bsr.block_column_indices),
               T(bsr.block_values, dt), T(rhs, dt))
-        out = torch.empty((bsr.rows, 128), device=dev)
+        out = torch.empty((bsr.rows, 128), device=dev,
+                          dtype=torch.bfloat16 if w == "bsr-bf16"
+                          else torch.float32)
         o = sw.Options.parse(args.opts)
         for _ in range(n):
             sw.bsr_spmm(*a4, out, 16, options=o)
-    elif w == "attention":
+    elif w in ("attention", "attention-bf16"):
         mask, q, kt, v, alpha = W.config5(seed=0)
-        att = (T(mask.row_offsets), T(mask.column_indices), T(mask.values),
-               T(q), T(kt), T(v))
-        s = torch.empty(mask.nnz, device=dev)
-        rm = torch.empty(mask.rows, device=dev)
-        rs = torch.empty(mask.rows, device=dev)
-        out = torch.empty((mask.rows, 64), device=dev)
+        dt = torch.bfloat16 if w == "attention-bf16" else torch.float32
+        att = (T(mask.row_offsets), T(mask.column_indices),
+               T(mask.values, dt), T(q, dt), T(kt, dt), T(v, dt))
+        s = torch.empty(mask.nnz, device=dev, dtype=dt)
+        rm = torch.empty(mask.rows, device=dev, dtype=dt)
+        rs = torch.empty(mask.rows, device=dev, dtype=dt)
+        out = torch.empty((mask.rows, 64), device=dev, dtype=dt)
         o = sw.Options.parse(args.opts or (
             "sddmm-mapping=row-tile-mfma sddmm-lanes-per-row=64 "
             "spmm-mapping=row-tile-mfma"))
@@ -411,52 +415,63 @@ def main():
         torch.cuda.empty_cache()
 
         # ---- configuration 4: BSR SpMM fp32 and bf16 ------------------------
+        # bf16: the op's same-type form (bf16 output) and the fp32-output
+        # extension
         log("generating configuration 4 (BSR 262,144, b=16)")
         bsr, rhs4 = W.config4(seed=0)
         flops4 = 2 * bsr.nnzb * 16 * 16 * 128
-        for bf16 in (False, True):
-            dt = torch.bfloat16 if bf16 else None
+        for name, dt, odt in (("fp32", None, torch.float32),
+                              ("bf16", torch.bfloat16, torch.bfloat16),
+                              ("bf16_f32out", torch.bfloat16, torch.float32)):
             args4 = (T(bsr.block_row_offsets), T(bsr.block_column_indices),
                      T(bsr.block_values, dt), T(rhs4, dt))
-            out4 = torch.empty((bsr.rows, 128), device=dev)
+            out4 = torch.empty((bsr.rows, 128), device=dev, dtype=odt)
             o = sw.Options(bsr_use_mfma=1)
-            log(f"BSR SpMM {'bf16' if bf16 else 'fp32'}")
+            log(f"BSR SpMM {name}")
             ms = time_steps(lambda: sw.bsr_spmm(*args4, out4, 16, options=o),
                             K, Wm, WARM_MS)
-            b = W.algorithmic_bytes_bsr(bsr.rows, bsr.cols, bsr.nnzb, 16, 128,
-                                        2 if bf16 else 4)
-            peak = BF16_MFMA_PEAK_TFLOPS if bf16 else FP32_MFMA_PEAK_TFLOPS
+            b = W.algorithmic_bytes_bsr(
+                bsr.rows, bsr.cols, bsr.nnzb, 16, 128,
+                4 if dt is None else 2, 4 if odt == torch.float32 else 2)
+            peak = (FP32_MFMA_PEAK_TFLOPS if dt is None
+                    else BF16_MFMA_PEAK_TFLOPS)
             tf = flops4 / ms / 1e9
             # ceiling = min(MFMA peak, HBM peak x arithmetic intensity)
             ceiling = min(peak, HBM_PEAK_GBS / 1e3 * flops4 / b)
-            workloads[f"bsr_config4_{'bf16' if bf16 else 'fp32'}"] = {
+            workloads[f"bsr_config4_{name}"] = {
                 "ms": ms, "TFLOP/s": tf, "mfma_frac": tf / peak,
-                "GB/s": b / ms / 1e6, "hbm_frac": b / ms / 1e6 / HBM_PEAK_GBS,
+                "bytes": b, "GB/s": b / ms / 1e6,
+                "hbm_frac": b / ms / 1e6 / HBM_PEAK_GBS,
                 "roofline_ceiling_TFLOP/s": ceiling,
                 "roofline_frac": tf / ceiling}
             log(f"  {ms * 1e3:.1f} us  {tf:.1f} TFLOP/s")
             del args4, out4
         del bsr, rhs4
 
-        # ---- configuration 5: sparse attention ------------------------------
+        # ---- configuration 5: sparse attention, fp32 and the bf16 option ---
         mask, q, kt, v, alpha = W.config5(seed=0)
-        att = (T(mask.row_offsets), T(mask.column_indices), T(mask.values),
-               T(q), T(kt), T(v))
-        scores = torch.empty(mask.nnz, device=dev)
-        rmax = torch.empty(mask.rows, device=dev)
-        rsum = torch.empty(mask.rows, device=dev)
-        outa = torch.empty((mask.rows, 64), device=dev)
-        for opts in ["", "sddmm-mapping=row-tile-mfma sddmm-lanes-per-row=64 "
-                         "spmm-mapping=row-tile-mfma"]:
-            o = sw.Options.parse(opts)
-            log(f"attention '{opts}'")
-            ms = time_steps(lambda: sw.sparse_attention(
-                *att, scores, rmax, rsum, outa, alpha, 0.0, options=o), K, Wm,
-                WARM_MS)
-            workloads.setdefault("attention_config5", {})[
-                opts or "reference defaults"] = {
-                "ms": ms, "GFLOP/s": 4 * mask.nnz * 64 / ms / 1e6}
-            log(f"  {ms * 1e3:.1f} us")
+        for dname, dt in (("fp32", torch.float32), ("bf16", torch.bfloat16)):
+            att = (T(mask.row_offsets), T(mask.column_indices),
+                   T(mask.values, dt), T(q, dt), T(kt, dt), T(v, dt))
+            scores = torch.empty(mask.nnz, device=dev, dtype=dt)
+            rmax = torch.empty(mask.rows, device=dev, dtype=dt)
+            rsum = torch.empty(mask.rows, device=dev, dtype=dt)
+            outa = torch.empty((mask.rows, 64), device=dev, dtype=dt)
+            for opts in ["", "sddmm-mapping=row-tile-mfma "
+                             "sddmm-lanes-per-row=64 "
+                             "spmm-mapping=row-tile-mfma"]:
+                o = sw.Options.parse(opts)
+                log(f"attention {dname} '{opts}'")
+                ms = time_steps(lambda: sw.sparse_attention(
+                    *att, scores, rmax, rsum, outa, alpha, 0.0, options=o),
+                    K, Wm, WARM_MS)
+                key = opts or "reference defaults"
+                if dname == "bf16":
+                    key = "bf16: " + key
+                workloads.setdefault("attention_config5", {})[key] = {
+                    "ms": ms, "GFLOP/s": 4 * mask.nnz * 64 / ms / 1e6}
+                log(f"  {ms * 1e3:.1f} us")
+            del att, scores, rmax, rsum, outa
 
     # ---- CPU baseline -------------------------------------------------------
     cpu = None
@@ -464,15 +479,20 @@ def main():
         import oracle
         oracle.build()
         log("CPU baseline (oracle, 1 thread)")
-        reps, t0 = 0, time.time()
-        while time.time() - t0 < args.cpu_seconds or reps == 0:
+        # each pass timed on its own; the value is the median pass (at
+        # least five), as the reference's harness reports medians
+        passes, t0 = [], time.time()
+        while time.time() - t0 < args.cpu_seconds or len(passes) < 5:
+            t1 = time.perf_counter()
             oracle.spmv(csr.row_offsets, csr.column_indices, csr.values, x)
-            reps += 1
-        dt = (time.time() - t0) / reps
+            passes.append(time.perf_counter() - t1)
+        dt = float(np.median(passes))
         cpu = {"value": spmv_bytes / dt / 1e9, "unit": "GB/s", "cores": 1,
                "kind": "port",
-               "sample": f"{reps} full configuration-2 SpMV passes "
-                         f"({dt * 1e3:.1f} ms each) of oracle/sw_oracle.c, "
+               "sample": f"median of {len(passes)} timed full "
+                         f"configuration-2 SpMV passes ({dt * 1e3:.1f} ms; "
+                         f"min {min(passes) * 1e3:.1f}, max "
+                         f"{max(passes) * 1e3:.1f}) of oracle/sw_oracle.c, "
                          "the scalar restatement of "
                          "benchmark/SparseBenchmarkUtils.cpp:211-229"}
         reps_mt, t0 = 0, time.time()

@@ -10,6 +10,17 @@
  * paraphrases the reference's diagnostic.  Index arrays are i32, values f32
  * (bf16 where the name says so).
  *
+ * bf16 entry points (_bf16): every value buffer of the op -- inputs and
+ * outputs alike -- holds bf16 as raw 16-bit patterns (uint16_t), because
+ * the reference's ops require one element type for all of their value
+ * operands (SparseWaveOps.cpp:340-372 for bsr_spmm, :374-425 for sddmm, and
+ * the same rule for spmm, csr_row_reduce and csr_rowwise_map).  Kernels
+ * widen to fp32, accumulate in fp32 (on the matrix cores where the name of
+ * the mapping says mfma) and round each stored result to nearest even once.
+ * The reference's own lowering of a bf16 op would also accumulate in bf16;
+ * fp32 accumulation is the more accurate choice and parity with the fp32
+ * path is tolerance-based (rel-L2 <= 1e-2).
+ *
  * Citations are path:line into the reference (sott0n/SparseWaveComp).
  */
 #ifndef SPARSEWAVE_AMD_H
@@ -168,6 +179,18 @@ int sw_spmm_csr_f32(const int32_t *row_offsets, const int32_t *column_indices,
                     int64_t rows, int64_t cols, int64_t nnz, int64_t k,
                     const sw_options *opts, void *stream);
 
+/* sparsewave.spmm on bf16 memrefs (values, rhs and output bf16), the output
+ * SpMM of the bf16 attention chain.  Mappings thread-per-output,
+ * wave-per-row-tile, wave-per-row-balanced and row-tile-mfma (bf16 matrix
+ * cores when k % 64 == 0); thread-per-position and wave-per-position add
+ * partial sums into the output and are rejected with
+ * SW_ERR_INVALID_OPTION. */
+int sw_spmm_csr_bf16(const int32_t *row_offsets,
+                     const int32_t *column_indices, const uint16_t *values,
+                     const uint16_t *rhs, uint16_t *output, int64_t rows,
+                     int64_t cols, int64_t nnz, int64_t k,
+                     const sw_options *opts, void *stream);
+
 /*
  * sparsewave.bsr_spmm: output[rows][k] = A * rhs[cols][k], A in BSR with
  * square block_size blocks stored row-major [nnzb][b][b]
@@ -181,14 +204,26 @@ int sw_bsr_spmm_f32(const int32_t *block_row_offsets,
                     int64_t rows, int64_t cols, int64_t nnzb, int64_t k,
                     int64_t block_size, const sw_options *opts, void *stream);
 
-/* BSR SpMM with bf16 block values and bf16 rhs (raw bf16 bits as uint16),
- * fp32 accumulation and fp32 output.  Same operands as sw_bsr_spmm_f32. */
+/* sparsewave.bsr_spmm on bf16 memrefs: block values, rhs and output all
+ * bf16 (BSRSpMMOp::verify, SparseWaveOps.cpp:355-360, requires the output
+ * to have the block values' element type).  fp32 accumulation, the output
+ * rounded to bf16.  Same operands as sw_bsr_spmm_f32. */
 int sw_bsr_spmm_bf16(const int32_t *block_row_offsets,
                      const int32_t *block_column_indices,
                      const uint16_t *block_values, const uint16_t *rhs,
-                     float *output, int64_t rows, int64_t cols, int64_t nnzb,
-                     int64_t k, int64_t block_size, const sw_options *opts,
-                     void *stream);
+                     uint16_t *output, int64_t rows, int64_t cols,
+                     int64_t nnzb, int64_t k, int64_t block_size,
+                     const sw_options *opts, void *stream);
+
+/* Extension with no reference op: bf16 block values and rhs, fp32 output
+ * (the fp32 accumulators stored unrounded).  A caller binding
+ * sparsewave.bsr_spmm on bf16 memrefs uses sw_bsr_spmm_bf16 instead. */
+int sw_bsr_spmm_bf16_f32out(const int32_t *block_row_offsets,
+                            const int32_t *block_column_indices,
+                            const uint16_t *block_values, const uint16_t *rhs,
+                            float *output, int64_t rows, int64_t cols,
+                            int64_t nnzb, int64_t k, int64_t block_size,
+                            const sw_options *opts, void *stream);
 
 /* Scalar regions the reference attaches to sddmm
  * (SparseWaveOps.td:171-223).  SW_SDDMM_AFFINE is the attention form
@@ -208,6 +243,18 @@ int sw_sddmm_csr_f32(const int32_t *row_offsets, const int32_t *column_indices,
                      int64_t nnz, int64_t kdim, int combine, float alpha,
                      float beta, const sw_options *opts, void *stream);
 
+/* sparsewave.sddmm on bf16 memrefs (SDDMMOp::verify,
+ * SparseWaveOps.cpp:374-425: values, lhs, rhs and output values share one
+ * element type).  The region is evaluated in fp32 on the fp32 dot product
+ * and rounded once.  sddmm-mapping=row-tile-mfma with kdim in {64,128,256}
+ * runs v_mfma_f32_16x16x32_bf16 tiles (lhs 16-byte aligned). */
+int sw_sddmm_csr_bf16(const int32_t *row_offsets,
+                      const int32_t *column_indices, const uint16_t *values,
+                      const uint16_t *lhs, const uint16_t *rhs,
+                      uint16_t *output_values, int64_t rows, int64_t cols,
+                      int64_t nnz, int64_t kdim, int combine, float alpha,
+                      float beta, const sw_options *opts, void *stream);
+
 /*
  * sparsewave.csr_row_reduce: output[r] = fold over row r's stored values.
  * kind "sum" (identity 0) or "max" (identity -inf, NaN-propagating maximum)
@@ -219,6 +266,14 @@ int sw_csr_row_reduce_f32(const int32_t *row_offsets,
                           float *output, int64_t rows, int64_t nnz,
                           const char *kind, const sw_options *opts,
                           void *stream);
+
+/* csr_row_reduce on bf16 memrefs: fp32 fold, the result rounded to bf16 (a
+ * maximum is exact). */
+int sw_csr_row_reduce_bf16(const int32_t *row_offsets,
+                           const int32_t *column_indices,
+                           const uint16_t *values, uint16_t *output,
+                           int64_t rows, int64_t nnz, const char *kind,
+                           const sw_options *opts, void *stream);
 
 /* Scalar regions of csr_rowwise_map (attention: exp-sub and div,
  * SparseAttentionToSparseWave.cpp:288-309). */
@@ -238,6 +293,15 @@ int sw_csr_rowwise_map_f32(const int32_t *row_offsets,
                            int64_t rows, int64_t nnz, int map,
                            const sw_options *opts, void *stream);
 
+/* csr_rowwise_map on bf16 memrefs: f evaluated in fp32, rounded once. */
+int sw_csr_rowwise_map_bf16(const int32_t *row_offsets,
+                            const int32_t *column_indices,
+                            const uint16_t *values,
+                            const uint16_t *row_values,
+                            uint16_t *output_values, int64_t rows,
+                            int64_t nnz, int map, const sw_options *opts,
+                            void *stream);
+
 /*
  * The sparse-attention chain: the six ops of
  * examples/pytorch/integration/SparseAttentionToSparseWave.cpp:230-315 in
@@ -255,6 +319,29 @@ int sw_sparse_attention_f32(const int32_t *row_offsets,
                             float *output, int64_t rows, int64_t cols,
                             int64_t nnz, int64_t d, int64_t dv, float alpha,
                             float beta, const sw_options *opts, void *stream);
+
+/*
+ * The same chain with all ten buffers' values in bf16 (the bf16 option of
+ * the attention bundle): the six ops on bf16 buffers, each op computing in
+ * fp32 and storing its result rounded to bf16 -- scores after the SDDMM,
+ * the exponentials, row sums and normalised scores, then the output.  The
+ * fused one-kernel form (sddmm-mapping=row-tile-mfma sddmm-lanes-per-row=64
+ * spmm-mapping=row-tile-mfma, d in {64,128}, dv % 64 == 0, query 16-byte and
+ * value / output 8-byte aligned) keeps the scores in registers and rounds
+ * them at the same points, with Q K^T on v_mfma_f32_16x16x32_bf16 and P V on
+ * v_mfma_f32_16x16x16_bf16.
+ */
+int sw_sparse_attention_bf16(const int32_t *row_offsets,
+                             const int32_t *column_indices,
+                             const uint16_t *mask_values,
+                             const uint16_t *query,
+                             const uint16_t *transposed_key,
+                             const uint16_t *value, uint16_t *scores,
+                             uint16_t *row_maximum, uint16_t *row_sum,
+                             uint16_t *output, int64_t rows, int64_t cols,
+                             int64_t nnz, int64_t d, int64_t dv, float alpha,
+                             float beta, const sw_options *opts,
+                             void *stream);
 
 /*
  * sparsewave.csr_row_at_position for a batch of positions:

@@ -63,6 +63,11 @@ def _declare(l):
     l.oracle_sparse_attention_f32.argtypes = [_I64, _I64, _I64, _I64, _P, _P,
                                               _P, _P, _P, _P, _P, _P, _P, _P,
                                               ctypes.c_float, ctypes.c_float]
+    l.oracle_sparse_attention_bf16.argtypes = [_I64, _I64, _I64, _I64, _P, _P,
+                                               _P, _P, _P, _P, _P, _P, _P, _P,
+                                               ctypes.c_float, ctypes.c_float]
+    l.oracle_round_bf16.argtypes = [_I64, _P, _P]
+    l.oracle_bf16_to_f32.argtypes = [_I64, _P, _P]
     l.oracle_csr_row_at_position.argtypes = [_I64, _P, _I64]
     l.oracle_csr_row_at_position.restype = _I64
     l.oracle_csr_rows_at_positions.argtypes = [_I64, _P, _I64, _P, _P]
@@ -217,6 +222,50 @@ def sparse_attention(ro, col, mask_values, query, transposed_key, value,
                                       _ptr(mv), _ptr(q), _ptr(kt), _ptr(v),
                                       _ptr(scores), _ptr(rmax), _ptr(rsum),
                                       _ptr(out), alpha, beta)
+    return scores, rmax, rsum, out
+
+
+def round_bf16(a):
+    """fp32 -> bf16 bit patterns (uint16), round to nearest even."""
+    a = _c(a, np.float32)
+    out = np.empty(a.shape, np.uint16)
+    lib().oracle_round_bf16(a.size, _ptr(a), _ptr(out))
+    return out
+
+
+def bf16_to_f32(h):
+    """bf16 bit patterns (uint16) -> their exact fp32 values."""
+    h = _c(h, np.uint16)
+    out = np.empty(h.shape, np.float32)
+    lib().oracle_bf16_to_f32(h.size, _ptr(h), _ptr(out))
+    return out
+
+
+def as_bf16(a):
+    """The fp32 values of a rounded to bf16 (what a bf16 buffer holds)."""
+    return bf16_to_f32(round_bf16(a))
+
+
+def sparse_attention_bf16(ro, col, mask_values, query, transposed_key, value,
+                          alpha, beta=0.0):
+    """The six ops on bf16 buffers, each op's result rounded to bf16
+    (SparseAttentionToSparseWave.cpp:270-312 with a bf16 element type).
+    Inputs are rounded to bf16 first.  Returns the fp32 values of the bf16
+    (scores, row_max, row_sum, output)."""
+    ro, col = _c(ro, np.int32), _c(col, np.int32)
+    mv = as_bf16(mask_values)
+    q, kt, v = as_bf16(query), as_bf16(transposed_key), as_bf16(value)
+    rows, d = q.shape
+    cols = kt.shape[1]
+    dv = v.shape[1]
+    scores = np.empty(col.size, np.float32)
+    rmax = np.empty(rows, np.float32)
+    rsum = np.empty(rows, np.float32)
+    out = np.empty((rows, dv), np.float32)
+    lib().oracle_sparse_attention_bf16(rows, cols, d, dv, _ptr(ro), _ptr(col),
+                                       _ptr(mv), _ptr(q), _ptr(kt), _ptr(v),
+                                       _ptr(scores), _ptr(rmax), _ptr(rsum),
+                                       _ptr(out), alpha, beta)
     return scores, rmax, rsum, out
 
 

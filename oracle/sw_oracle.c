@@ -13,6 +13,13 @@
  * path:line into sott0n/SparseWaveComp.
  *
  * Parity pins (what checks each function; see tests/test_oracle.py):
+ *   round_bf16 / bf16_to_f32: torch's float32 -> bfloat16 conversion on
+ *       random, tie, subnormal, overflow and non-finite patterns, and hand
+ *       cases (1 + 2^-8 -> 1, 1 + 3 * 2^-8 -> 1 + 2^-6).
+ *   sparse_attention_bf16: a dense torch restatement of the six ops with
+ *       torch's bf16 rounding between them, the golden attention vector
+ *       within bf16 accuracy, and a mutation (one rounding left out) that
+ *       the dense check catches.
  *   spmv / spmm / bsr / sddmm / row_reduce / rowwise_map / attention:
  *       golden vectors held by the reference's runtime tests, scipy.sparse
  *       and dense numpy closed forms on random inputs, mutation tests.
@@ -276,6 +283,81 @@ void oracle_sparse_attention_f32(int64_t rows, int64_t cols, int64_t d,
   oracle_csr_rowwise_map_f32(rows, ro, scores, row_sum, scores,
                              SW_ORACLE_MAP_DIV);
   oracle_spmm_csr_f32(rows, dv, ro, col, scores, value, output);
+}
+
+/* fp32 -> bf16, round to nearest with ties to even: the 16 dropped low bits
+ * of the binary32 pattern round the kept upper half (a carry may ripple into
+ * the exponent, reaching infinity above the largest bf16), and a NaN keeps
+ * its sign and becomes a quiet NaN.  This is the conversion the bf16 paths
+ * apply once to every stored result (the bfloat16 format keeps the binary32
+ * sign, exponent and the top 7 fraction bits). */
+static uint16_t round_bf16(float f) {
+  uint32_t u;
+  memcpy(&u, &f, sizeof u);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u)
+    return (uint16_t)((u >> 16) | 0x0040u);
+  const uint32_t lsb = (u >> 16) & 1u;
+  return (uint16_t)((u + 0x7FFFu + lsb) >> 16);
+}
+
+static float widen_bf16(uint16_t h) {
+  uint32_t u = (uint32_t)h << 16;
+  float f;
+  memcpy(&f, &u, sizeof f);
+  return f;
+}
+
+void oracle_round_bf16(int64_t n, const float *in, uint16_t *out) {
+  for (int64_t i = 0; i < n; ++i)
+    out[i] = round_bf16(in[i]);
+}
+
+void oracle_bf16_to_f32(int64_t n, const uint16_t *in, float *out) {
+  for (int64_t i = 0; i < n; ++i)
+    out[i] = widen_bf16(in[i]);
+}
+
+/* A result as a bf16 buffer stores it (rounded, kept as its fp32 value). */
+static void store_bf16(int64_t n, float *v) {
+  for (int64_t i = 0; i < n; ++i)
+    v[i] = widen_bf16(round_bf16(v[i]));
+}
+
+/* The six-op attention chain on bf16 buffers (the bf16 option of the
+ * attention bundle): the ops of SparseAttentionToSparseWave.cpp:270-312 in
+ * order, each computing in fp32 from its bf16 operands exactly as the fp32
+ * restatements above do, and each storing its result rounded to bf16 -- the
+ * scores after the SDDMM, the exponentials, the row sums, the normalised
+ * scores and the output (a row maximum is one of its bf16 inputs, so it
+ * needs no rounding).  Every input must already hold bf16 values; outputs
+ * are returned as the fp32 values of their bf16 patterns.  The reference's
+ * ops require one element type for all value operands
+ * (SparseWaveOps.cpp:374-425); computing each op in fp32 rather than in the
+ * element type is this build's stated choice. */
+void oracle_sparse_attention_bf16(int64_t rows, int64_t cols, int64_t d,
+                                  int64_t dv, const int32_t *ro,
+                                  const int32_t *col, const float *mask_values,
+                                  const float *query,
+                                  const float *transposed_key,
+                                  const float *value, float *scores,
+                                  float *row_max, float *row_sum,
+                                  float *output, float alpha, float beta) {
+  const int64_t nnz = ro[rows];
+  oracle_sddmm_csr_f32(rows, d, cols, ro, col, mask_values, query,
+                       transposed_key, scores, SW_ORACLE_SDDMM_AFFINE, alpha,
+                       beta);
+  store_bf16(nnz, scores);
+  oracle_csr_row_reduce_f32(rows, ro, scores, row_max, SW_ORACLE_REDUCE_MAX);
+  oracle_csr_rowwise_map_f32(rows, ro, scores, row_max, scores,
+                             SW_ORACLE_MAP_EXP_SUB);
+  store_bf16(nnz, scores);
+  oracle_csr_row_reduce_f32(rows, ro, scores, row_sum, SW_ORACLE_REDUCE_SUM);
+  store_bf16(rows, row_sum);
+  oracle_csr_rowwise_map_f32(rows, ro, scores, row_sum, scores,
+                             SW_ORACLE_MAP_DIV);
+  store_bf16(nnz, scores);
+  oracle_spmm_csr_f32(rows, dv, ro, col, scores, value, output);
+  store_bf16(rows * dv, output);
 }
 
 /* Row recovery for a CSR position: search [1, rows+1) of row_offsets for the

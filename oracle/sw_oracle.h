@@ -59,6 +59,16 @@ void oracle_sparse_attention_f32(int64_t rows, int64_t cols, int64_t d,
                                  const float *value, float *scores,
                                  float *row_max, float *row_sum, float *output,
                                  float alpha, float beta);
+void oracle_round_bf16(int64_t n, const float *in, uint16_t *out);
+void oracle_bf16_to_f32(int64_t n, const uint16_t *in, float *out);
+void oracle_sparse_attention_bf16(int64_t rows, int64_t cols, int64_t d,
+                                  int64_t dv, const int32_t *ro,
+                                  const int32_t *col, const float *mask_values,
+                                  const float *query,
+                                  const float *transposed_key,
+                                  const float *value, float *scores,
+                                  float *row_max, float *row_sum,
+                                  float *output, float alpha, float beta);
 int64_t oracle_csr_row_at_position(int64_t rows, const int32_t *ro,
                                    int64_t position);
 void oracle_csr_rows_at_positions(int64_t rows, const int32_t *ro,

@@ -16,7 +16,8 @@ import ctypes
 import os
 
 __all__ = [
-    "Options", "SparseWaveError", "library_path", "load_library", "spmv",
+    "Options", "SparseWaveError", "ShapeError", "library_path",
+    "load_library", "spmv",
     "coo_spmv", "spmv_gather_floor",
     "spmm", "bsr_spmm", "sddmm", "csr_row_reduce", "csr_rowwise_map",
     "sparse_attention", "csr_row_at_position", "SDDMM_MUL", "SDDMM_AFFINE",
@@ -34,9 +35,12 @@ EXPORTED_SYMBOLS = (
     "sw_options_init", "sw_options_set", "sw_options_parse",
     "sw_validate_options", "sw_last_error", "sw_version", "sw_spmv_csr_f32",
     "sw_spmv_coo_f32", "sw_spmv_gather_floor_f32",
-    "sw_spmm_csr_f32", "sw_bsr_spmm_f32", "sw_bsr_spmm_bf16",
-    "sw_sddmm_csr_f32", "sw_csr_row_reduce_f32", "sw_csr_rowwise_map_f32",
-    "sw_sparse_attention_f32", "sw_csr_row_at_position",
+    "sw_spmm_csr_f32", "sw_spmm_csr_bf16", "sw_bsr_spmm_f32",
+    "sw_bsr_spmm_bf16", "sw_bsr_spmm_bf16_f32out", "sw_sddmm_csr_f32",
+    "sw_sddmm_csr_bf16", "sw_csr_row_reduce_f32", "sw_csr_row_reduce_bf16",
+    "sw_csr_rowwise_map_f32", "sw_csr_rowwise_map_bf16",
+    "sw_sparse_attention_f32", "sw_sparse_attention_bf16",
+    "sw_csr_row_at_position",
     "sw_host_matrix_free", "sw_host_bsr_free", "sw_matrix_market_read",
     "sw_csr_binary_write", "sw_coo_binary_write", "sw_csr_binary_read",
     "sw_coo_binary_read", "sw_convert_to_bsr", "sw_bsr_binary_write",
@@ -114,19 +118,32 @@ def load_library():
         "sw_spmv_gather_floor_f32": (ctypes.c_int, [P, P, P, P, I64, P]),
         "sw_spmm_csr_f32": (ctypes.c_int, [P, P, P, P, P, I64, I64, I64, I64,
                                            OP, P]),
+        "sw_spmm_csr_bf16": (ctypes.c_int, [P, P, P, P, P, I64, I64, I64, I64,
+                                            OP, P]),
         "sw_bsr_spmm_f32": (ctypes.c_int, [P, P, P, P, P, I64, I64, I64, I64,
                                            I64, OP, P]),
         "sw_bsr_spmm_bf16": (ctypes.c_int, [P, P, P, P, P, I64, I64, I64, I64,
                                             I64, OP, P]),
+        "sw_bsr_spmm_bf16_f32out": (ctypes.c_int, [P, P, P, P, P, I64, I64,
+                                                   I64, I64, I64, OP, P]),
         "sw_sddmm_csr_f32": (ctypes.c_int, [P, P, P, P, P, P, I64, I64, I64,
                                             I64, ctypes.c_int, F, F, OP, P]),
+        "sw_sddmm_csr_bf16": (ctypes.c_int, [P, P, P, P, P, P, I64, I64, I64,
+                                             I64, ctypes.c_int, F, F, OP, P]),
         "sw_csr_row_reduce_f32": (ctypes.c_int, [P, P, P, P, I64, I64, C, OP,
                                                  P]),
+        "sw_csr_row_reduce_bf16": (ctypes.c_int, [P, P, P, P, I64, I64, C, OP,
+                                                  P]),
         "sw_csr_rowwise_map_f32": (ctypes.c_int, [P, P, P, P, P, I64, I64,
                                                   ctypes.c_int, OP, P]),
+        "sw_csr_rowwise_map_bf16": (ctypes.c_int, [P, P, P, P, P, I64, I64,
+                                                   ctypes.c_int, OP, P]),
         "sw_sparse_attention_f32": (ctypes.c_int, [P, P, P, P, P, P, P, P, P,
                                                    P, I64, I64, I64, I64, I64,
                                                    F, F, OP, P]),
+        "sw_sparse_attention_bf16": (ctypes.c_int, [P, P, P, P, P, P, P, P, P,
+                                                    P, I64, I64, I64, I64,
+                                                    I64, F, F, OP, P]),
         "sw_csr_row_at_position": (ctypes.c_int, [P, I64, P, P, I64, P]),
     }
     for name, (res, args) in sig.items():
@@ -223,11 +240,49 @@ def _stream(stream):
     return ctypes.c_void_p(stream.cuda_stream)
 
 
+class ShapeError(SparseWaveError, ValueError):
+    """Operand shapes that do not fit the op, caught before the C ABI is
+    called (SW_ERR_INVALID_SHAPE)."""
+
+    def __init__(self, message: str):
+        super().__init__(-2, message)
+
+
+def _need(cond, message):
+    if not cond:
+        raise ShapeError(message)
+
+
+def _rows_of(row_offsets, name="row_offsets"):
+    _need(row_offsets.dim() == 1 and row_offsets.numel() >= 1,
+          f"{name} must be a 1-D tensor of rows + 1 offsets")
+    return row_offsets.numel() - 1
+
+
+def _value_dtype(t, name):
+    """fp32 or bf16: the element type shared by an op's value operands."""
+    import torch
+    if t.dtype not in (torch.float32, torch.bfloat16):
+        raise TypeError(f"{name} must be float32 or bfloat16, got {t.dtype}")
+    return t.dtype
+
+
+def _fn(base, dtype):
+    import torch
+    return getattr(load_library(),
+                   base + ("_bf16" if dtype == torch.bfloat16 else "_f32"))
+
+
 def spmv(row_offsets, column_indices, values, vector, output, options=None,
          stream=None):
     """sparsewave.spmv (SparseWaveOps.td:17-52): output = A @ vector."""
     import torch
-    rows = row_offsets.numel() - 1
+    rows = _rows_of(row_offsets)
+    _need(column_indices.numel() == values.numel(),
+          "column indices and values must have the same length")
+    _need(vector.dim() == 1, "vector must be 1-D")
+    _need(output.dim() == 1 and output.numel() == rows,
+          f"output must hold rows = {rows} values")
     _check(load_library().sw_spmv_csr_f32(
         _dev(row_offsets, torch.int32, "row_offsets"),
         _dev(column_indices, torch.int32, "column_indices"),
@@ -243,9 +298,11 @@ def coo_spmv(row_indices, column_indices, values, vector, output,
     """sparsewave.coo_spmv (SparseWaveOps.td:54-88): output = A @ vector with
     A as COO entries (any order, repeated coordinates add up)."""
     import torch
-    if not (row_indices.numel() == column_indices.numel() == values.numel()):
-        raise SparseWaveError(-2, "COO row indices, column indices and values "
-                                  "must have the same length")
+    _need(row_indices.numel() == column_indices.numel() == values.numel(),
+          "COO row indices, column indices and values must have the same "
+          "length")
+    _need(vector.dim() == 1 and output.dim() == 1,
+          "vector and output must be 1-D")
     _check(load_library().sw_spmv_coo_f32(
         _dev(row_indices, torch.int32, "row_indices"),
         _dev(column_indices, torch.int32, "column_indices"),
@@ -262,11 +319,10 @@ def spmv_gather_floor(column_indices, values, vector, partial, stream=None):
     i.e. a CSR SpMV's column/value reads and x gathers without its rows."""
     import torch
     nnz = values.numel()
-    if column_indices.numel() != nnz:
-        raise SparseWaveError(-2, "column indices and values must have the "
-                                  "same length")
-    if partial.numel() < (nnz + 511) // 512:
-        raise SparseWaveError(-2, "partial needs ceil(nnz / 512) entries")
+    _need(column_indices.numel() == nnz,
+          "column indices and values must have the same length")
+    _need(partial.numel() >= (nnz + 511) // 512,
+          "partial needs ceil(nnz / 512) entries")
     _check(load_library().sw_spmv_gather_floor_f32(
         _dev(column_indices, torch.int32, "column_indices"),
         _dev(values, torch.float32, "values"),
@@ -277,57 +333,77 @@ def spmv_gather_floor(column_indices, values, vector, partial, stream=None):
 
 def spmm(row_offsets, column_indices, values, rhs, output, options=None,
          stream=None):
-    """sparsewave.spmm (SparseWaveOps.td:91-124): output = A @ rhs."""
+    """sparsewave.spmm (SparseWaveOps.td:91-124): output = A @ rhs.  values,
+    rhs and output share one element type, float32 or bfloat16."""
     import torch
-    rows = row_offsets.numel() - 1
-    if rhs.dim() != 2 or output.dim() != 2 or output.shape != (rows,
-                                                                 rhs.shape[1]):
-        raise ValueError("expected rhs [cols, k] and output [rows, k]")
-    _check(load_library().sw_spmm_csr_f32(
+    rows = _rows_of(row_offsets)
+    dt = _value_dtype(values, "values")
+    _need(column_indices.numel() == values.numel(),
+          "column indices and values must have the same length")
+    _need(rhs.dim() == 2 and output.dim() == 2 and
+          tuple(output.shape) == (rows, rhs.shape[1]),
+          "expected rhs [cols, k] and output [rows, k]")
+    _check(_fn("sw_spmm_csr", dt)(
         _dev(row_offsets, torch.int32, "row_offsets"),
         _dev(column_indices, torch.int32, "column_indices"),
-        _dev(values, torch.float32, "values"),
-        _dev(rhs, torch.float32, "rhs"),
-        _dev(output, torch.float32, "output"), rows, rhs.shape[0],
-        values.numel(), rhs.shape[1], _opts(options), _stream(stream)))
+        _dev(values, dt, "values"), _dev(rhs, dt, "rhs"),
+        _dev(output, dt, "output"), rows, rhs.shape[0], values.numel(),
+        rhs.shape[1], _opts(options), _stream(stream)))
     return output
 
 
 def bsr_spmm(block_row_offsets, block_column_indices, block_values, rhs,
              output, block_size, options=None, stream=None):
-    """sparsewave.bsr_spmm (SparseWaveOps.td:126-169); fp32 or bf16 inputs."""
+    """sparsewave.bsr_spmm (SparseWaveOps.td:126-169).  float32 operands, or
+    bfloat16 block values and rhs with a bfloat16 output (the op's
+    same-element-type rule) or, as an extension, a float32 output."""
     import torch
-    rows = (block_row_offsets.numel() - 1) * block_size
-    if rhs.dim() != 2 or output.shape != (rows, rhs.shape[1]):
-        raise ValueError("expected rhs [cols, k] and output [rows, k]")
-    bf16 = block_values.dtype == torch.bfloat16
-    vdt = torch.bfloat16 if bf16 else torch.float32
-    fn = (load_library().sw_bsr_spmm_bf16 if bf16
-          else load_library().sw_bsr_spmm_f32)
+    _need(block_size >= 1, "block size must be positive")
+    rows = _rows_of(block_row_offsets, "block_row_offsets") * block_size
     nnzb = block_column_indices.numel()
+    dt = _value_dtype(block_values, "block_values")
+    _need(block_values.numel() == nnzb * block_size * block_size,
+          "block values must hold nnzb * block_size^2 entries")
+    _need(rhs.dim() == 2 and output.dim() == 2 and
+          tuple(output.shape) == (rows, rhs.shape[1]),
+          "expected rhs [cols, k] and output [rows, k]")
+    lib = load_library()
+    if dt == torch.float32:
+        fn, odt = lib.sw_bsr_spmm_f32, torch.float32
+    elif output.dtype == torch.float32:
+        fn, odt = lib.sw_bsr_spmm_bf16_f32out, torch.float32
+    else:
+        fn, odt = lib.sw_bsr_spmm_bf16, torch.bfloat16
     _check(fn(_dev(block_row_offsets, torch.int32, "block_row_offsets"),
               _dev(block_column_indices, torch.int32, "block_column_indices"),
-              _dev(block_values, vdt, "block_values"), _dev(rhs, vdt, "rhs"),
-              _dev(output, torch.float32, "output"), rows, rhs.shape[0], nnzb,
+              _dev(block_values, dt, "block_values"), _dev(rhs, dt, "rhs"),
+              _dev(output, odt, "output"), rows, rhs.shape[0], nnzb,
               rhs.shape[1], block_size, _opts(options), _stream(stream)))
     return output
 
 
 def sddmm(row_offsets, column_indices, values, lhs, rhs, output_values,
           combine=SDDMM_MUL, alpha=1.0, beta=0.0, options=None, stream=None):
-    """sparsewave.sddmm (SparseWaveOps.td:171-223)."""
+    """sparsewave.sddmm (SparseWaveOps.td:171-223); float32 or bfloat16."""
     import torch
-    rows = row_offsets.numel() - 1
-    if lhs.dim() != 2 or rhs.dim() != 2 or lhs.shape[1] != rhs.shape[0]:
-        raise ValueError("expected lhs [rows, k] and rhs [k, cols]")
-    _check(load_library().sw_sddmm_csr_f32(
+    rows = _rows_of(row_offsets)
+    nnz = column_indices.numel()
+    dt = _value_dtype(output_values, "output_values")
+    _need(lhs.dim() == 2 and rhs.dim() == 2 and lhs.shape[1] == rhs.shape[0],
+          "expected lhs [rows, k] and rhs [k, cols]")
+    _need(lhs.shape[0] == rows, f"lhs must have rows = {rows} rows")
+    _need(output_values.numel() == nnz,
+          "output values must hold one value per stored entry")
+    if combine != SDDMM_DOT:
+        _need(values.numel() == nnz,
+              "values must hold one value per stored entry")
+    vals = values if combine != SDDMM_DOT else output_values
+    _check(_fn("sw_sddmm_csr", dt)(
         _dev(row_offsets, torch.int32, "row_offsets"),
         _dev(column_indices, torch.int32, "column_indices"),
-        _dev(values, torch.float32, "values"),
-        _dev(lhs, torch.float32, "lhs"), _dev(rhs, torch.float32, "rhs"),
-        _dev(output_values, torch.float32, "output_values"), rows,
-        rhs.shape[1], column_indices.numel(), lhs.shape[1], combine, alpha,
-        beta, _opts(options), _stream(stream)))
+        _dev(vals, dt, "values"), _dev(lhs, dt, "lhs"), _dev(rhs, dt, "rhs"),
+        _dev(output_values, dt, "output_values"), rows, rhs.shape[1], nnz,
+        lhs.shape[1], combine, alpha, beta, _opts(options), _stream(stream)))
     return output_values
 
 
@@ -335,14 +411,18 @@ def csr_row_reduce(row_offsets, column_indices, values, output, kind="sum",
                    options=None, stream=None):
     """sparsewave.csr_row_reduce (SparseWaveOps.td:225-257)."""
     import torch
-    rows = row_offsets.numel() - 1
+    rows = _rows_of(row_offsets)
+    dt = _value_dtype(values, "values")
+    _need(output.numel() == rows, f"output must hold rows = {rows} values")
+    if column_indices is not None:
+        _need(column_indices.numel() == values.numel(),
+              "column indices and values must have the same length")
     ci = (None if column_indices is None else
           _dev(column_indices, torch.int32, "column_indices"))
-    _check(load_library().sw_csr_row_reduce_f32(
+    _check(_fn("sw_csr_row_reduce", dt)(
         _dev(row_offsets, torch.int32, "row_offsets"), ci,
-        _dev(values, torch.float32, "values"),
-        _dev(output, torch.float32, "output"), rows, values.numel(),
-        kind.encode(), _opts(options), _stream(stream)))
+        _dev(values, dt, "values"), _dev(output, dt, "output"), rows,
+        values.numel(), kind.encode(), _opts(options), _stream(stream)))
     return output
 
 
@@ -351,15 +431,22 @@ def csr_rowwise_map(row_offsets, column_indices, values, row_values,
                     stream=None):
     """sparsewave.csr_rowwise_map (SparseWaveOps.td:259-299)."""
     import torch
-    rows = row_offsets.numel() - 1
+    rows = _rows_of(row_offsets)
+    dt = _value_dtype(values, "values")
+    _need(row_values.numel() == rows,
+          f"row values must hold rows = {rows} values")
+    _need(output_values.numel() == values.numel(),
+          "output values and values must have the same length")
+    if column_indices is not None:
+        _need(column_indices.numel() == values.numel(),
+              "column indices and values must have the same length")
     ci = (None if column_indices is None else
           _dev(column_indices, torch.int32, "column_indices"))
-    _check(load_library().sw_csr_rowwise_map_f32(
+    _check(_fn("sw_csr_rowwise_map", dt)(
         _dev(row_offsets, torch.int32, "row_offsets"), ci,
-        _dev(values, torch.float32, "values"),
-        _dev(row_values, torch.float32, "row_values"),
-        _dev(output_values, torch.float32, "output_values"), rows,
-        values.numel(), kind, _opts(options), _stream(stream)))
+        _dev(values, dt, "values"), _dev(row_values, dt, "row_values"),
+        _dev(output_values, dt, "output_values"), rows, values.numel(), kind,
+        _opts(options), _stream(stream)))
     return output_values
 
 
@@ -367,24 +454,34 @@ def sparse_attention(row_offsets, column_indices, mask_values, query,
                      transposed_key, value, scores, row_maximum, row_sum,
                      output, alpha, beta=0.0, options=None, stream=None):
     """The six-op sparse attention chain
-    (SparseAttentionToSparseWave.cpp:230-315), ten-buffer ABI."""
+    (SparseAttentionToSparseWave.cpp:230-315), ten-buffer ABI; all value
+    buffers float32, or all bfloat16 (the bf16 option)."""
     import torch
-    rows = row_offsets.numel() - 1
-    d = query.shape[1]
-    dv = value.shape[1]
-    _check(load_library().sw_sparse_attention_f32(
+    rows = _rows_of(row_offsets)
+    nnz = column_indices.numel()
+    dt = _value_dtype(query, "query")
+    _need(query.dim() == 2 and transposed_key.dim() == 2 and
+          value.dim() == 2 and output.dim() == 2,
+          "query, transposed_key, value and output must be 2-D")
+    d, cols, dv = query.shape[1], transposed_key.shape[1], value.shape[1]
+    _need(query.shape[0] == rows, f"query must have rows = {rows} rows")
+    _need(transposed_key.shape[0] == d,
+          "transposed key must have head-dim rows")
+    _need(value.shape[0] == cols,
+          "value must have one row per key (transposed key column)")
+    _need(mask_values.numel() == nnz and scores.numel() == nnz,
+          "mask values and scores must hold one value per stored entry")
+    _need(row_maximum.numel() == rows and row_sum.numel() == rows,
+          f"row maximum and row sum must hold rows = {rows} values")
+    _need(tuple(output.shape) == (rows, dv), "expected output [rows, dv]")
+    _check(_fn("sw_sparse_attention", dt)(
         _dev(row_offsets, torch.int32, "row_offsets"),
         _dev(column_indices, torch.int32, "column_indices"),
-        _dev(mask_values, torch.float32, "mask_values"),
-        _dev(query, torch.float32, "query"),
-        _dev(transposed_key, torch.float32, "transposed_key"),
-        _dev(value, torch.float32, "value"),
-        _dev(scores, torch.float32, "scores"),
-        _dev(row_maximum, torch.float32, "row_maximum"),
-        _dev(row_sum, torch.float32, "row_sum"),
-        _dev(output, torch.float32, "output"), rows, transposed_key.shape[1],
-        column_indices.numel(), d, dv, alpha, beta, _opts(options),
-        _stream(stream)))
+        _dev(mask_values, dt, "mask_values"), _dev(query, dt, "query"),
+        _dev(transposed_key, dt, "transposed_key"), _dev(value, dt, "value"),
+        _dev(scores, dt, "scores"), _dev(row_maximum, dt, "row_maximum"),
+        _dev(row_sum, dt, "row_sum"), _dev(output, dt, "output"), rows, cols,
+        nnz, d, dv, alpha, beta, _opts(options), _stream(stream)))
     return output
 
 

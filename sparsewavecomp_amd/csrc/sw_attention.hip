@@ -24,6 +24,10 @@ int launch_spmm(const int32_t *ro, const int32_t *col, const float *val,
                 const float *rhs, float *out, int64_t rows, int64_t rhs_rows,
                 int64_t nnz, int64_t k, const sw_options &o, const char *what,
                 hipStream_t st);
+int launch_spmm(const int32_t *ro, const int32_t *col, const uint16_t *val,
+                const uint16_t *rhs, uint16_t *out, int64_t rows,
+                int64_t rhs_rows, int64_t nnz, int64_t k, const sw_options &o,
+                const char *what, hipStream_t st);
 }
 
 namespace {
@@ -50,6 +54,18 @@ __device__ __forceinline__ float maximumf(float a, float b) {
   return a > b ? a : b;
 }
 
+// A result as its op stores it: unchanged in fp32, rounded to bf16 (and
+// widened back) for bf16 buffers.  The fused bf16 kernels round each
+// intermediate where the separate ops would store it, so every bf16 schedule
+// computes the six ops on bf16 buffers.
+template <typename T>
+__device__ __forceinline__ float as_stored(float v) {
+  if constexpr (sizeof(T) == 4)
+    return v;
+  else
+    return bf16_to_f32(f32_to_bf16(v));
+}
+
 __device__ __forceinline__ float map_value(int kind, float v, float rv) {
   switch (kind) {
   case SW_MAP_EXP_SUB:
@@ -66,15 +82,16 @@ __device__ __forceinline__ float map_value(int kind, float v, float rv) {
 // ---- SDDMM -----------------------------------------------------------------
 constexpr int kSddmmRowPos = 4;
 
+template <typename T>
 __global__ __launch_bounds__(1024) void sddmm_thread_per_row(
     const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
-    const float *__restrict__ val, const float *__restrict__ lhs,
-    const float *__restrict__ rhs, float *__restrict__ out, int32_t rows,
+    const T *__restrict__ val, const T *__restrict__ lhs,
+    const T *__restrict__ rhs, T *__restrict__ out, int32_t rows,
     int64_t cols, int32_t kdim, int kind, float alpha, float beta) {
   int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (r >= rows)
     return;
-  const float *a = lhs + r * kdim;
+  const T *a = lhs + r * kdim;
   // kSddmmRowPos positions at a time, sixteen terms of each in flight: the
   // launch has one thread per row (8192 rows are 128 waves), so a row is a
   // chain of memory trips and registers are plentiful.  Each position's dot
@@ -93,12 +110,12 @@ __global__ __launch_bounds__(1024) void sddmm_thread_per_row(
       float av[16], bv[kSddmmRowPos][16];
 #pragma unroll
       for (int u = 0; u < 16; ++u)
-        av[u] = a[i + u];
+        av[u] = ldv(a + i + u);
 #pragma unroll
       for (int j = 0; j < kSddmmRowPos; ++j)
 #pragma unroll
         for (int u = 0; u < 16; ++u)
-          bv[j][u] = rhs[(int64_t)(i + u) * cols + c[j]];
+          bv[j][u] = ldv(rhs + (int64_t)(i + u) * cols + c[j]);
 #pragma unroll
       for (int j = 0; j < kSddmmRowPos; ++j)
 #pragma unroll
@@ -106,30 +123,33 @@ __global__ __launch_bounds__(1024) void sddmm_thread_per_row(
           dot[j] = __builtin_fmaf(av[u], bv[j][u], dot[j]);
     }
     for (; i < kdim; ++i) {
-      const float av = a[i];
+      const float av = ldv(a + i);
 #pragma unroll
       for (int j = 0; j < kSddmmRowPos; ++j)
-        dot[j] = __builtin_fmaf(av, rhs[(int64_t)i * cols + c[j]], dot[j]);
+        dot[j] = __builtin_fmaf(av, ldv(rhs + (int64_t)i * cols + c[j]),
+                                dot[j]);
     }
 #pragma unroll
     for (int j = 0; j < kSddmmRowPos; ++j)
       if (p + j < e)
-        out[p + j] = combine_sddmm(kind, val != nullptr ? val[p + j] : 0.0f,
-                                   dot[j], alpha, beta);
+        stv(out + p + j,
+            combine_sddmm(kind, val != nullptr ? ldv(val + p + j) : 0.0f,
+                          dot[j], alpha, beta));
   }
 }
 
 // One wave computes the SDDMM entries of row r: lane l takes positions
 // start+l, start+l+64, ...; the row of lhs is held 64 values at a time, one
 // per lane, and broadcast with v_readlane.
+template <typename T>
 __device__ __forceinline__ void sddmm_row_wave(
     const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
-    const float *__restrict__ val, const float *__restrict__ lhs,
-    const float *__restrict__ rhs, float *__restrict__ out, int64_t r,
+    const T *__restrict__ val, const T *__restrict__ lhs,
+    const T *__restrict__ rhs, T *__restrict__ out, int64_t r,
     int64_t cols, int32_t kdim, int kind, float alpha, float beta) {
   const int l = lane_id();
   const int32_t s = ro[r], e = ro[r + 1];
-  const float *a = lhs + r * kdim;
+  const T *a = lhs + r * kdim;
   for (int32_t p0 = s; p0 < e; p0 += 4 * kWave) {
     float dot[4] = {0.f, 0.f, 0.f, 0.f};
     int64_t c[4];
@@ -139,31 +159,32 @@ __device__ __forceinline__ void sddmm_row_wave(
       c[j] = p < e ? (int64_t)col[p] : 0;
     }
     for (int32_t i0 = 0; i0 < kdim; i0 += kWave) {
-      const float mine = (i0 + l < kdim) ? a[i0 + l] : 0.0f;
+      const float mine = (i0 + l < kdim) ? ldv(a + i0 + l) : 0.0f;
       const int n = std::min<int32_t>(kWave, kdim - i0);
       for (int t = 0; t < n; ++t) {
         const float av =
             __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), t));
-        const float *rrow = rhs + (int64_t)(i0 + t) * cols;
+        const T *rrow = rhs + (int64_t)(i0 + t) * cols;
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          dot[j] = __builtin_fmaf(av, rrow[c[j]], dot[j]);
+          dot[j] = __builtin_fmaf(av, ldv(rrow + c[j]), dot[j]);
       }
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       int32_t p = p0 + j * kWave + l;
       if (p < e)
-        out[p] = combine_sddmm(kind, val != nullptr ? val[p] : 0.0f, dot[j],
-                               alpha, beta);
+        stv(out + p, combine_sddmm(kind, val != nullptr ? ldv(val + p) : 0.0f,
+                                   dot[j], alpha, beta));
     }
   }
 }
 
+template <typename T>
 __global__ __launch_bounds__(256) void sddmm_wave_per_row(
     const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
-    const float *__restrict__ val, const float *__restrict__ lhs,
-    const float *__restrict__ rhs, float *__restrict__ out, int32_t rows,
+    const T *__restrict__ val, const T *__restrict__ lhs,
+    const T *__restrict__ rhs, T *__restrict__ out, int32_t rows,
     int64_t cols, int32_t kdim, int kind, float alpha, float beta) {
   const int64_t r = (int64_t)blockIdx.x * (blockDim.x / kWave) +
                     threadIdx.x / kWave;
@@ -280,10 +301,10 @@ __global__ __launch_bounds__(64 * W) void sddmm_tile_mfma(
   }
 }
 
-template <bool MAX>
+template <bool MAX, typename T>
 __global__ __launch_bounds__(1024) void row_reduce_thread(
-    const int32_t *__restrict__ ro, const float *__restrict__ val,
-    float *__restrict__ out, int32_t rows) {
+    const int32_t *__restrict__ ro, const T *__restrict__ val,
+    T *__restrict__ out, int32_t rows) {
   int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (r >= rows)
     return;
@@ -296,7 +317,7 @@ __global__ __launch_bounds__(1024) void row_reduce_thread(
     float v[16];
 #pragma unroll
     for (int u = 0; u < 16; ++u)
-      v[u] = val[p + u];
+      v[u] = ldv(val + p + u);
 #pragma unroll
     for (int u = 0; u < 16; ++u)
       acc = MAX ? maximumf(acc, v[u]) : acc + v[u];
@@ -305,14 +326,14 @@ __global__ __launch_bounds__(1024) void row_reduce_thread(
     float v[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u)
-      v[u] = val[p + u];
+      v[u] = ldv(val + p + u);
 #pragma unroll
     for (int u = 0; u < 4; ++u)
       acc = MAX ? maximumf(acc, v[u]) : acc + v[u];
   }
   for (; p < e; ++p)
-    acc = MAX ? maximumf(acc, val[p]) : acc + val[p];
-  out[r] = acc;
+    acc = MAX ? maximumf(acc, ldv(val + p)) : acc + ldv(val + p);
+  stv(out + r, acc);
 }
 
 __device__ __forceinline__ float wave_max(float v) {
@@ -325,10 +346,10 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
-template <bool MAX>
+template <bool MAX, typename T>
 __global__ __launch_bounds__(256) void row_reduce_wave(
-    const int32_t *__restrict__ ro, const float *__restrict__ val,
-    float *__restrict__ out, int32_t rows) {
+    const int32_t *__restrict__ ro, const T *__restrict__ val,
+    T *__restrict__ out, int32_t rows) {
   const int64_t r = (int64_t)blockIdx.x * (blockDim.x / kWave) +
                     threadIdx.x / kWave;
   if (r >= rows)
@@ -336,20 +357,21 @@ __global__ __launch_bounds__(256) void row_reduce_wave(
   const int l = lane_id();
   float acc = MAX ? -INFINITY : 0.0f;
   for (int32_t p = ro[r] + l; p < ro[r + 1]; p += kWave)
-    acc = MAX ? maximumf(acc, val[p]) : acc + val[p];
+    acc = MAX ? maximumf(acc, ldv(val + p)) : acc + ldv(val + p);
   acc = MAX ? wave_max(acc) : group_sum<kWave>(acc);
   if (l == 0)
-    out[r] = acc;
+    stv(out + r, acc);
 }
 
 // ---- row-wise map ----------------------------------------------------------
+template <typename T>
 __global__ __launch_bounds__(1024) void rowwise_map_thread(
-    const int32_t *__restrict__ ro, const float *val,
-    const float *__restrict__ rowv, float *out, int32_t rows, int kind) {
+    const int32_t *__restrict__ ro, const T *val,
+    const T *__restrict__ rowv, T *out, int32_t rows, int kind) {
   int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (r >= rows)
     return;
-  const float rv = rowv[r];
+  const float rv = ldv(rowv + r);
   const int32_t e = ro[r + 1];
   int32_t p = ro[r];
   // sixteen entries loaded before they are written back: out may be val
@@ -358,25 +380,26 @@ __global__ __launch_bounds__(1024) void rowwise_map_thread(
     float v[16];
 #pragma unroll
     for (int u = 0; u < 16; ++u)
-      v[u] = val[p + u];
+      v[u] = ldv(val + p + u);
 #pragma unroll
     for (int u = 0; u < 16; ++u)
-      out[p + u] = map_value(kind, v[u], rv);
+      stv(out + p + u, map_value(kind, v[u], rv));
   }
   for (; p < e; ++p)
-    out[p] = map_value(kind, val[p], rv);
+    stv(out + p, map_value(kind, ldv(val + p), rv));
 }
 
+template <typename T>
 __global__ __launch_bounds__(256) void rowwise_map_wave(
-    const int32_t *__restrict__ ro, const float *val,
-    const float *__restrict__ rowv, float *out, int32_t rows, int kind) {
+    const int32_t *__restrict__ ro, const T *val,
+    const T *__restrict__ rowv, T *out, int32_t rows, int kind) {
   const int64_t r = (int64_t)blockIdx.x * (blockDim.x / kWave) +
                     threadIdx.x / kWave;
   if (r >= rows)
     return;
-  const float rv = rowv[r];
+  const float rv = ldv(rowv + r);
   for (int32_t p = ro[r] + lane_id(); p < ro[r + 1]; p += kWave)
-    out[p] = map_value(kind, val[p], rv);
+    stv(out + p, map_value(kind, ldv(val + p), rv));
 }
 
 
@@ -387,9 +410,10 @@ __global__ __launch_bounds__(256) void rowwise_map_wave(
 // rowSum are written as the separate ops would write them.
 constexpr int kSoftmaxRegs = 8;
 
+template <typename T>
 __global__ __launch_bounds__(256) void row_softmax_wave(
-    const int32_t *__restrict__ ro, float *scores, float *__restrict__ rmax,
-    float *__restrict__ rsum, int32_t rows) {
+    const int32_t *__restrict__ ro, T *scores, T *__restrict__ rmax,
+    T *__restrict__ rsum, int32_t rows) {
   const int64_t r = (int64_t)blockIdx.x * (blockDim.x / kWave) +
                     threadIdx.x / kWave;
   if (r >= rows)
@@ -405,7 +429,7 @@ __global__ __launch_bounds__(256) void row_softmax_wave(
       // unconditional load from a clamped index, then select (a guarded
       // load would wait on the spot)
       const int32_t p = s + l + j * kWave;
-      const float x = scores[p < e ? p : e - 1];
+      const float x = ldv(scores + (p < e ? p : e - 1));
       v[j] = p < e ? x : -INFINITY;
       m = maximumf(m, v[j]);
     }
@@ -413,73 +437,76 @@ __global__ __launch_bounds__(256) void row_softmax_wave(
 #pragma unroll
     for (int j = 0; j < kSoftmaxRegs; ++j)
       if (s + l + j * kWave < e) {
-        v[j] = expf(v[j] - m);
+        v[j] = as_stored<T>(expf(v[j] - m));
         sum += v[j];
       }
-    sum = group_sum<kWave>(sum);
+    sum = as_stored<T>(group_sum<kWave>(sum));
 #pragma unroll
     for (int j = 0; j < kSoftmaxRegs; ++j) {
       const int32_t p = s + l + j * kWave;
       if (p < e)
-        scores[p] = v[j] / sum;
+        stv(scores + p, v[j] / sum);
     }
   } else {
     for (int32_t p = s + l; p < e; p += kWave)
-      m = maximumf(m, scores[p]);
+      m = maximumf(m, ldv(scores + p));
     m = wave_max(m);
     for (int32_t p = s + l; p < e; p += kWave) {
-      const float v = expf(scores[p] - m);
-      scores[p] = v;
+      const float v = as_stored<T>(expf(ldv(scores + p) - m));
+      stv(scores + p, v);
       sum += v;
     }
-    sum = group_sum<kWave>(sum);
+    sum = as_stored<T>(group_sum<kWave>(sum));
     for (int32_t p = s + l; p < e; p += kWave)
-      scores[p] = scores[p] / sum;
+      stv(scores + p, ldv(scores + p) / sum);
   }
   if (l == 0) {
-    rmax[r] = m;
-    rsum[r] = sum;
+    stv(rmax + r, m);
+    stv(rsum + r, sum);
   }
 }
 
 // Row r of the attention output computed by one wave from the row's
 // normalised scores (the fused kernel's per-row path): lanes over the output
 // columns, sequential over the row's positions.
+template <typename T>
 __device__ __forceinline__ void attention_row_output(
     const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
-    const float *scores, const float *__restrict__ value,
-    float *__restrict__ out, int64_t r, int64_t dv) {
+    const T *scores, const T *__restrict__ value, T *__restrict__ out,
+    int64_t r, int64_t dv) {
   const int32_t s = ro[r], e = ro[r + 1];
   for (int64_t c = lane_id(); c < dv; c += kWave) {
     float acc = 0.0f;
     for (int32_t p = s; p < e; ++p)
-      acc = __builtin_fmaf(scores[p], value[(int64_t)col[p] * dv + c], acc);
-    out[r * dv + c] = acc;
+      acc = __builtin_fmaf(ldv(scores + p),
+                           ldv(value + (int64_t)col[p] * dv + c), acc);
+    stv(out + r * dv + c, acc);
   }
 }
 
 // One row's softmax in global memory by one wave (the fused kernel's
 // per-row path): the long-row branch of row_softmax_wave.
+template <typename T>
 __device__ __forceinline__ void attention_row_softmax(
-    const int32_t *__restrict__ ro, float *scores, float *__restrict__ rmax,
-    float *__restrict__ rsum, int64_t r) {
+    const int32_t *__restrict__ ro, T *scores, T *__restrict__ rmax,
+    T *__restrict__ rsum, int64_t r) {
   const int l = lane_id();
   const int32_t s = ro[r], e = ro[r + 1];
   float m = -INFINITY, sum = 0.0f;
   for (int32_t p = s + l; p < e; p += kWave)
-    m = maximumf(m, scores[p]);
+    m = maximumf(m, ldv(scores + p));
   m = wave_max(m);
   for (int32_t p = s + l; p < e; p += kWave) {
-    const float v = expf(scores[p] - m);
-    scores[p] = v;
+    const float v = as_stored<T>(expf(ldv(scores + p) - m));
+    stv(scores + p, v);
     sum += v;
   }
-  sum = group_sum<kWave>(sum);
+  sum = as_stored<T>(group_sum<kWave>(sum));
   for (int32_t p = s + l; p < e; p += kWave)
-    scores[p] = scores[p] / sum;
+    stv(scores + p, ldv(scores + p) / sum);
   if (l == 0) {
-    rmax[r] = m;
-    rsum[r] = sum;
+    stv(rmax + r, m);
+    stv(rsum + r, sum);
   }
 }
 
@@ -828,6 +855,416 @@ __global__ __launch_bounds__(64 * W) void attention_tile_fused(
       attention_row_output(ro, col, scores, value, out, r, dv);
 }
 
+// ---- bf16 matrix-core kernels ----------------------------------------------
+// The bf16 forms of the SDDMM tile and the fused attention tile: the same
+// 16-row tiles, row structure check, fallbacks and outputs as the fp32
+// kernels above, with bf16 operands on the matrix cores (fp32 accumulation):
+//   Q K^T: v_mfma_f32_16x16x32_bf16, lane group g supplying K elements
+//     32 s + 8 g .. 32 s + 8 g + 7 at step s -- one 128-bit load of a Q row
+//     and eight 16-bit K^T gathers per lane and step;
+//   P V:   v_mfma_f32_16x16x16_bf16 per 16-entry chunk, lane group g
+//     supplying entries 4 g .. 4 g + 3 of the chunk, with four output tiles
+//     whose columns interleave (tile n's column j is output column
+//     4 j + n of the 64-column block), so that one 64-bit load of a V row
+//     gives a lane its values for all four tiles.
+// Every result is rounded to bf16 where the separate op would store it.
+
+// the eight K^T values K^T[32 s + 8 g + e][c] (e = 0..7) as four bf16 pairs;
+// base is K^T row 32 s, lane_off the byte offset of column c plus 8 g rows
+__device__ __forceinline__ v4u gather_kt8(const uint16_t *base,
+                                          uint32_t row_bytes,
+                                          uint32_t lane_off) {
+  uint32_t x[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    x[e] = *at_bytes(at_bytes(base, e * row_bytes), lane_off);
+  return v4u{x[0] | (x[1] << 16), x[2] | (x[3] << 16), x[4] | (x[5] << 16),
+             x[6] | (x[7] << 16)};
+}
+
+// SDDMM over 16-row tiles, bf16 (kdim = 64 * KB; the host guarantees that
+// 2 * kdim * cols and 2 * nnz fit 32 bits and that lhs is 16-byte aligned).
+template <int KB, int W>
+__global__ __launch_bounds__(64 * W) void sddmm_tile_mfma_bf16(
+    const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
+    const uint16_t *__restrict__ val, const uint16_t *__restrict__ lhs,
+    const uint16_t *__restrict__ rhs, uint16_t *__restrict__ out,
+    int32_t rows, int64_t cols, int32_t kdim, int kind, float alpha,
+    float beta) {
+  constexpr int S = 2 * KB; // 32-deep K steps
+  const int r0 = blockIdx.x * 16;
+  const int nt = std::min(16, rows - r0);
+  const int wave = threadIdx.x / kWave;
+  const int l = lane_id(), i = l & 15, g = l >> 4;
+  int32_t rb[4], rl[4];
+  {
+    int32_t b[5];
+#pragma unroll
+    for (int v = 0; v < 5; ++v)
+      b[v] = ro[std::min(r0 + 4 * g + v, rows)];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      rb[v] = b[v];
+      rl[v] = 4 * g + v < nt ? b[v + 1] - b[v] : 0;
+    }
+  }
+  // A operand: lhs row r0 + i, elements 32 s + 8 g .. + 7
+  v4u qa[S];
+  const int64_t qrow = (int64_t)std::min(r0 + i, rows - 1) * kdim;
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    const v4u x = *reinterpret_cast<const v4u *>(lhs + qrow + 32 * s + 8 * g);
+    qa[s] = i < nt ? x : v4u{0u, 0u, 0u, 0u};
+  }
+  __shared__ int verdict;
+  if (!tile_prefix_ok_block(ro, col, r0, nt, &verdict)) {
+    for (int r = r0 + wave; r < r0 + nt; r += W)
+      sddmm_row_wave(ro, col, val, lhs, rhs, out, r, cols, kdim, kind, alpha,
+                     beta);
+    return;
+  }
+  const int last = r0 + nt - 1;
+  const int32_t bl = ro[last];
+  const int32_t len_last = ro[last + 1] - bl;
+  const uint32_t row_bytes = 2u * (uint32_t)cols;
+  for (int32_t t0 = wave * 16; t0 < len_last; t0 += 32 * W) {
+    const int32_t t1 = t0 + 16 * W;
+    const bool two = t1 < len_last; // wave-uniform
+    const int32_t ta = t0 + i, tb = t1 + i;
+    const uint32_t cj0 = ta < len_last ? (uint32_t)col[bl + ta] : 0u;
+    const uint32_t cj1 = two && tb < len_last ? (uint32_t)col[bl + tb] : 0u;
+    float s0[4], s1[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const bool in0 = val != nullptr && ta < rl[v];
+      const bool in1 = val != nullptr && two && tb < rl[v];
+      const float x0 = val != nullptr ? ldv(val + (in0 ? rb[v] + ta : bl)) : 0.f;
+      const float x1 = val != nullptr ? ldv(val + (in1 ? rb[v] + tb : bl)) : 0.f;
+      s0[v] = in0 ? x0 : 0.0f;
+      s1[v] = in1 ? x1 : 0.0f;
+    }
+    const uint32_t lo0 = 2u * cj0 + 8u * g * row_bytes;
+    const uint32_t lo1 = 2u * cj1 + 8u * g * row_bytes;
+    v4f acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+    v4u b0[S], b1[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const uint16_t *base = rhs + (int64_t)(32 * s) * cols;
+      b0[s] = gather_kt8(base, row_bytes, lo0);
+      b1[s] = gather_kt8(base, row_bytes, lo1); // column 0 when !two
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      acc0 = mfma_16x16x32_bf16(qa[s], b0[s], acc0);
+      if (two)
+        acc1 = mfma_16x16x32_bf16(qa[s], b1[s], acc1);
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      if (ta < rl[v])
+        stv(out + rb[v] + ta,
+            combine_sddmm(kind, s0[v], acc0[v], alpha, beta));
+      if (two && tb < rl[v])
+        stv(out + rb[v] + tb,
+            combine_sddmm(kind, s1[v], acc1[v], alpha, beta));
+    }
+  }
+}
+
+// The attention chain fused over 16-row tiles, bf16 (d = 64 * KB,
+// dv % 64 == 0): the fp32 attention_tile_fused's tiles, waves, chunks,
+// structure check and fallbacks, with the products on bf16 matrix cores.
+// The host guarantees that the byte offsets into mask / scores (2 * nnz),
+// K^T (2 * d * cols) and V (2 * cols * dv) fit 32 bits and that Q is 16-byte
+// and V 8-byte aligned.
+template <int KB, int W>
+__global__ __launch_bounds__(64 * W) void attention_tile_fused_bf16(
+    const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
+    const uint16_t *__restrict__ mask, const uint16_t *__restrict__ q,
+    const uint16_t *__restrict__ kt, const uint16_t *__restrict__ value,
+    uint16_t *scores, uint16_t *__restrict__ rmax, uint16_t *__restrict__ rsum,
+    uint16_t *__restrict__ out, int32_t rows, int64_t cols, int32_t kdim,
+    int64_t dv, float alpha, float beta) {
+  static_assert(W == 8 && kFusedCols == 8 * kWave && kFusedChunks == 4,
+                "check layout");
+  constexpr int S = 2 * KB;
+  __shared__ float part[W][4][4][kWave]; // [wave][n tile][v][lane]
+  __shared__ float wred[2][W][16];       // [max, sum][wave][row]
+  __shared__ int32_t lcol[kFusedCols];   // the last row's columns
+  __shared__ int verdict;
+  __shared__ int v_nonfinite;
+  const int r0 = blockIdx.x * 16;
+  const int nt = std::min(16, rows - r0);
+  const int wave = threadIdx.x / kWave;
+  const int l = lane_id(), i = l & 15, g = l >> 4;
+  const int ic = i < nt ? i : nt - 1;
+  const int32_t rbase = ro[r0 + ic];
+  const int32_t la = i < nt ? ro[r0 + ic + 1] - rbase : 0;
+  // B operand of S^T = K_chunk Q^T: Q row r0 + i, elements 32 s + 8 g .. + 7
+  v4u qb[S];
+  const int64_t qrow = (int64_t)std::min(r0 + i, rows - 1) * kdim;
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    const v4u x = *reinterpret_cast<const v4u *>(q + qrow + 32 * s + 8 * g);
+    qb[s] = i < nt ? x : v4u{0u, 0u, 0u, 0u};
+  }
+  const int32_t my_ro = ro[r0 + (l < nt ? l : nt)];
+  const int32_t bl = __builtin_amdgcn_readlane(my_ro, nt - 1);
+  const int32_t len_last = __builtin_amdgcn_readlane(my_ro, nt) - bl;
+  bool ok = len_last <= kFusedCols; // workgroup-uniform
+  if (ok) {
+    if (threadIdx.x == 0) {
+      verdict = 1;
+      v_nonfinite = 0;
+    }
+    int32_t x[2][8], yl[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int32_t t = l + u * kWave;
+      yl[u] = col[len_last > 0 ? bl + std::min(t, len_last - 1) : 0];
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int rr = wave + h * W;
+      const int rc = rr < nt - 1 ? rr : 0;
+      const int32_t b = __builtin_amdgcn_readlane(my_ro, rc);
+      const int32_t len = __builtin_amdgcn_readlane(my_ro, rc + 1) - b;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int32_t t = l + u * kWave;
+        x[h][u] = col[len > 0 ? b + std::min(t, len - 1) : 0];
+      }
+    }
+    bool mine = true;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int rr = wave + h * W;
+      if (rr < nt - 1) { // wave-uniform
+        const int32_t b = __builtin_amdgcn_readlane(my_ro, rr);
+        const int32_t len = __builtin_amdgcn_readlane(my_ro, rr + 1) - b;
+        mine &= len <= len_last;
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          if (l + u * kWave < len)
+            mine &= x[h][u] == yl[u];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (u == wave && l + u * kWave < len_last)
+        lcol[l + u * kWave] = yl[u];
+    __syncthreads();
+    if (__builtin_amdgcn_ballot_w64(!mine) != 0 && l == 0)
+      verdict = 0;
+    __syncthreads();
+    ok = verdict != 0;
+  }
+  if (!ok) { // workgroup-uniform
+    for (int r = r0 + wave; r < r0 + nt; r += W) {
+      sddmm_row_wave(ro, col, mask, q, kt, scores, r, cols, kdim,
+                     SW_SDDMM_AFFINE, alpha, beta);
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+      attention_row_softmax(ro, scores, rmax, rsum, r);
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+      attention_row_output(ro, col, scores, value, out, r, dv);
+    }
+    return;
+  }
+  auto chunk_t0 = [&](int k) __attribute__((always_inline)) {
+    return 16 * (wave + W * k);
+  };
+  auto valid = [&](int k, int v) __attribute__((always_inline)) {
+    return chunk_t0(k) + 4 * g + v < la;
+  };
+  // A. S^T per chunk: sv[k][v] = score (i, t0(k) + 4g + v), rounded to bf16
+  const uint32_t row_bytes = 2u * (uint32_t)cols;
+  float sv[kFusedChunks][4];
+#pragma unroll
+  for (int it = 0; it < kFusedChunks / 2; ++it) {
+    const int32_t t0 = chunk_t0(2 * it), t1 = chunk_t0(2 * it + 1);
+    const bool one = t0 < len_last, two = t1 < len_last; // wave-uniform
+    const int32_t last = std::max(len_last - 1, 0);
+    const uint32_t cj0 = lcol[std::min(t0 + i, last)];
+    const uint32_t cj1 = lcol[std::min(two ? t1 + i : t0 + i, last)];
+    float s0[4] = {0.f, 0.f, 0.f, 0.f}, s1[4] = {0.f, 0.f, 0.f, 0.f};
+    v4f acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+    if (one) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const bool in0 = valid(2 * it, v), in1 = valid(2 * it + 1, v);
+        const float x0 = tof(
+            *at_bytes(mask, 2u * (in0 ? rbase + t0 + 4 * g + v : bl)));
+        const float x1 = tof(
+            *at_bytes(mask, 2u * (in1 ? rbase + t1 + 4 * g + v : bl)));
+        s0[v] = in0 ? x0 : 0.0f;
+        s1[v] = in1 ? x1 : 0.0f;
+      }
+      const uint32_t ko0 = 2u * cj0 + 8u * g * row_bytes;
+      const uint32_t ko1 = 2u * cj1 + 8u * g * row_bytes;
+      v4u a0[S], a1[S];
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        const uint16_t *base = kt + (int64_t)(32 * s) * cols;
+        a0[s] = gather_kt8(base, row_bytes, ko0);
+        a1[s] = gather_kt8(base, row_bytes, ko1);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        acc0 = mfma_16x16x32_bf16(a0[s], qb[s], acc0);
+        if (two)
+          acc1 = mfma_16x16x32_bf16(a1[s], qb[s], acc1);
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      sv[2 * it][v] = as_stored<uint16_t>(
+          combine_sddmm(SW_SDDMM_AFFINE, s0[v], acc0[v], alpha, beta));
+      sv[2 * it + 1][v] = as_stored<uint16_t>(
+          combine_sddmm(SW_SDDMM_AFFINE, s1[v], acc1[v], alpha, beta));
+    }
+  }
+  // C's V rows for chunks 2 it and 2 it + 1: lane (j, g) takes
+  // V[c_t][nb + 4j .. nb + 4j + 3] for t = t0(k) + 4g + st (zero past
+  // len_last, read from row 0)
+  auto load_v = [&](int it, int64_t nb, v2u (&bv)[2][4])
+      __attribute__((always_inline)) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        const int32_t t = chunk_t0(2 * it + h) + 4 * g + st;
+        const uint32_t c = lcol[std::max(std::min(t, len_last - 1), 0)];
+        const uint32_t vo =
+            2u * ((t < len_last ? c * (uint32_t)dv : 0u) + 4u * (uint32_t)i);
+        const v2u x = *reinterpret_cast<const v2u *>(at_bytes(value + nb, vo));
+        bv[h][st] = t < len_last ? x : v2u{0u, 0u};
+      }
+  };
+  v2u bv[2][4];
+  load_v(0, 0, bv); // in flight over the softmax
+  // B. row softmax on the stored (bf16) scores, each op's result rounded
+  {
+    float m = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < kFusedChunks; ++k)
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        if (valid(k, v))
+          m = maximumf(m, sv[k][v]);
+    m = maximumf(m, swizzle_xor16(m));
+    m = maximumf(m, shfl_xor32(m));
+    if (g == 0)
+      wred[0][wave][i] = m;
+    __syncthreads();
+    m = wred[0][0][i];
+#pragma unroll
+    for (int w = 1; w < W; ++w)
+      m = maximumf(m, wred[0][w][i]);
+    float sum = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kFusedChunks; ++k)
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        if (valid(k, v)) {
+          sv[k][v] = as_stored<uint16_t>(expf(sv[k][v] - m));
+          sum += sv[k][v];
+        }
+    sum += swizzle_xor16(sum);
+    sum += shfl_xor32(sum);
+    if (g == 0)
+      wred[1][wave][i] = sum;
+    __syncthreads();
+    sum = wred[1][0][i];
+#pragma unroll
+    for (int w = 1; w < W; ++w)
+      sum += wred[1][w][i];
+    sum = as_stored<uint16_t>(sum);
+#pragma unroll
+    for (int k = 0; k < kFusedChunks; ++k)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const bool in = valid(k, v);
+        const float p = in ? as_stored<uint16_t>(sv[k][v] / sum) : 0.0f;
+        if (in)
+          *at_bytes(scores + chunk_t0(k) + v, 2u * (rbase + 4 * g)) =
+              f32_to_bf16(p);
+        sv[k][v] = p;
+      }
+    if (wave == 0 && g == 0 && i < nt) {
+      stv(rmax + r0 + i, m);
+      stv(rsum + r0 + i, sum);
+    }
+  }
+  // C. output = P V: P from sv (lane (i, g) holds P[i][t0(k) + 4g + st])
+  auto mfma_pair = [&](int it, const v2u (&b)[2][4], v4f (&acc)[4])
+      __attribute__((always_inline)) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      if (chunk_t0(2 * it + h) < len_last) { // wave-uniform
+        const int k = 2 * it + h;
+        const v2u a = v2u{pack_bf16x2(sv[k][0], sv[k][1]),
+                          pack_bf16x2(sv[k][2], sv[k][3])};
+#pragma unroll
+        for (int n = 0; n < 4; ++n) {
+          const v2u bn =
+              v2u{bf16_half(b[h][0], n) | (bf16_half(b[h][1], n) << 16),
+                  bf16_half(b[h][2], n) | (bf16_half(b[h][3], n) << 16)};
+          acc[n] = mfma_16x16x16_bf16(a, bn, acc[n]);
+        }
+      }
+  };
+  bool nonfinite = false;
+  for (int64_t nb = 0; nb < dv; nb += 64) {
+    v4f acc[4];
+#pragma unroll
+    for (int n = 0; n < 4; ++n)
+      acc[n] = v4f{0.f, 0.f, 0.f, 0.f};
+    if (nb > 0)
+      load_v(0, nb, bv);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_pair(0, bv, acc);
+    if (chunk_t0(2) < len_last) { // wave-uniform
+      load_v(1, nb, bv);
+      __builtin_amdgcn_sched_barrier(0);
+      mfma_pair(1, bv, acc);
+    }
+#pragma unroll
+    for (int n = 0; n < 4; ++n)
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        part[wave][n][v][l] = acc[n][v];
+    __syncthreads();
+    if (wave < 4) {
+      // wave w finishes rows 4g + w, columns nb + 4i .. nb + 4i + 3
+      float o[4];
+      bool nf = false;
+#pragma unroll
+      for (int n = 0; n < 4; ++n) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int w = 0; w < W; ++w)
+          sum += part[w][n][wave][l];
+        o[n] = sum;
+        nf |= !__builtin_isfinite(sum);
+      }
+      const int rr = 4 * g + wave;
+      if (rr < nt) {
+        *reinterpret_cast<v2u *>(out + (int64_t)(r0 + rr) * dv + nb + 4 * i) =
+            v2u{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+        nonfinite |= nf;
+      }
+      if (__builtin_amdgcn_ballot_w64(nonfinite) != 0 && l == 0)
+        v_nonfinite = 1;
+    }
+    __syncthreads();
+  }
+  if (v_nonfinite != 0)
+    for (int r = r0 + wave; r < r0 + nt; r += W)
+      attention_row_output(ro, col, scores, value, out, r, dv);
+}
+
 int grid_for(int64_t work, int64_t per_block, const char *what,
              int64_t *grid) {
   *grid = std::max<int64_t>(sw::ceil_div(work, per_block), 1);
@@ -838,30 +1275,54 @@ int grid_for(int64_t work, int64_t per_block, const char *what,
 
 namespace sw {
 
-int launch_sddmm(const int32_t *ro, const int32_t *col, const float *val,
-                 const float *lhs, const float *rhs, float *out, int64_t rows,
-                 int64_t cols, int64_t kdim, int kind, float alpha, float beta,
-                 const sw_options &o, hipStream_t st) {
+template <typename T>
+int launch_sddmm(const int32_t *ro, const int32_t *col, const T *val,
+                 const T *lhs, const T *rhs, T *out, int64_t rows,
+                 int64_t cols, int64_t nnz, int64_t kdim, int kind,
+                 float alpha, float beta, const sw_options &o,
+                 hipStream_t st) {
   int64_t grid;
   if (streq(o.sddmm_mapping, "row-tile-mfma") &&
       (kdim == 64 || kdim == 128 || kdim == 256)) {
-    int rc = grid_for(rows, 16, "SDDMM", &grid);
-    if (rc)
-      return rc;
     const int kb = (int)(kdim / 64);
+    if constexpr (sizeof(T) == 4) {
+      int rc = grid_for(rows, 16, "SDDMM", &grid);
+      if (rc)
+        return rc;
 #define SW_SDDMM_TILE(KB)                                                     \
   hipLaunchKernelGGL((sddmm_tile_mfma<KB, kSddmmTileWaves>),                  \
                      dim3((unsigned)grid), dim3(64 * kSddmmTileWaves), 0, st, \
                      ro, col, val, lhs, rhs, out, (int32_t)rows, cols,        \
                      (int32_t)kdim, kind, alpha, beta)
-    if (kb == 1)
-      SW_SDDMM_TILE(1);
-    else if (kb == 2)
-      SW_SDDMM_TILE(2);
-    else
-      SW_SDDMM_TILE(4);
+      if (kb == 1)
+        SW_SDDMM_TILE(1);
+      else if (kb == 2)
+        SW_SDDMM_TILE(2);
+      else
+        SW_SDDMM_TILE(4);
 #undef SW_SDDMM_TILE
-    return launch_check("SDDMM tile MFMA kernel");
+      return launch_check("SDDMM tile MFMA kernel");
+    } else if (aligned16(lhs) && narrow_offsets(kdim, cols) &&
+               narrow_offsets(nnz, 1)) {
+      // bf16 tiles: a 128-bit lhs load per K step, K^T gathered with 32-bit
+      // lane byte offsets
+      int rc = grid_for(rows, 16, "SDDMM", &grid);
+      if (rc)
+        return rc;
+#define SW_SDDMM_TILE(KB)                                                     \
+  hipLaunchKernelGGL((sddmm_tile_mfma_bf16<KB, kSddmmTileWaves>),             \
+                     dim3((unsigned)grid), dim3(64 * kSddmmTileWaves), 0, st, \
+                     ro, col, val, lhs, rhs, out, (int32_t)rows, cols,        \
+                     (int32_t)kdim, kind, alpha, beta)
+      if (kb == 1)
+        SW_SDDMM_TILE(1);
+      else if (kb == 2)
+        SW_SDDMM_TILE(2);
+      else
+        SW_SDDMM_TILE(4);
+#undef SW_SDDMM_TILE
+      return launch_check("SDDMM tile MFMA kernel");
+    }
   }
   if (streq(o.sddmm_mapping, "wave-per-row") ||
       (streq(o.sddmm_mapping, "row-tile-mfma")) ||
@@ -869,34 +1330,34 @@ int launch_sddmm(const int32_t *ro, const int32_t *col, const float *val,
     int rc = grid_for(rows, 4, "SDDMM", &grid);
     if (rc)
       return rc;
-    hipLaunchKernelGGL(sddmm_wave_per_row, dim3((unsigned)grid), dim3(256), 0,
-                       st, ro, col, val, lhs, rhs, out, (int32_t)rows, cols,
+    hipLaunchKernelGGL(sddmm_wave_per_row<T>, dim3((unsigned)grid), dim3(256),
+                       0, st, ro, col, val, lhs, rhs, out, (int32_t)rows, cols,
                        (int32_t)kdim, kind, alpha, beta);
   } else {
     const int64_t B = o.sddmm_block_size;
     int rc = grid_for(rows, B, "SDDMM", &grid);
     if (rc)
       return rc;
-    hipLaunchKernelGGL(sddmm_thread_per_row, dim3((unsigned)grid),
+    hipLaunchKernelGGL(sddmm_thread_per_row<T>, dim3((unsigned)grid),
                        dim3((unsigned)B), 0, st, ro, col, val, lhs, rhs, out,
                        (int32_t)rows, cols, (int32_t)kdim, kind, alpha, beta);
   }
   return launch_check("SDDMM kernel");
 }
 
-int launch_row_reduce(const int32_t *ro, const float *val, float *out,
-                      int64_t rows, bool is_max, const sw_options &o,
-                      hipStream_t st) {
+template <typename T>
+int launch_row_reduce(const int32_t *ro, const T *val, T *out, int64_t rows,
+                      bool is_max, const sw_options &o, hipStream_t st) {
   int64_t grid;
   if (o.sddmm_lanes_per_row == 64) {
     int rc = grid_for(rows, 4, "CSR row reduction", &grid);
     if (rc)
       return rc;
     if (is_max)
-      hipLaunchKernelGGL(row_reduce_wave<true>, dim3((unsigned)grid), dim3(256),
-                         0, st, ro, val, out, (int32_t)rows);
+      hipLaunchKernelGGL((row_reduce_wave<true, T>), dim3((unsigned)grid),
+                         dim3(256), 0, st, ro, val, out, (int32_t)rows);
     else
-      hipLaunchKernelGGL(row_reduce_wave<false>, dim3((unsigned)grid),
+      hipLaunchKernelGGL((row_reduce_wave<false, T>), dim3((unsigned)grid),
                          dim3(256), 0, st, ro, val, out, (int32_t)rows);
   } else {
     const int64_t B = o.row_reduction_block_size;
@@ -904,35 +1365,263 @@ int launch_row_reduce(const int32_t *ro, const float *val, float *out,
     if (rc)
       return rc;
     if (is_max)
-      hipLaunchKernelGGL(row_reduce_thread<true>, dim3((unsigned)grid),
+      hipLaunchKernelGGL((row_reduce_thread<true, T>), dim3((unsigned)grid),
                          dim3((unsigned)B), 0, st, ro, val, out, (int32_t)rows);
     else
-      hipLaunchKernelGGL(row_reduce_thread<false>, dim3((unsigned)grid),
+      hipLaunchKernelGGL((row_reduce_thread<false, T>), dim3((unsigned)grid),
                          dim3((unsigned)B), 0, st, ro, val, out, (int32_t)rows);
   }
   return launch_check("CSR row reduction kernel");
 }
 
-int launch_rowwise_map(const int32_t *ro, const float *val, const float *rowv,
-                       float *out, int64_t rows, int kind, const sw_options &o,
+template <typename T>
+int launch_rowwise_map(const int32_t *ro, const T *val, const T *rowv, T *out,
+                       int64_t rows, int kind, const sw_options &o,
                        hipStream_t st) {
   int64_t grid;
   if (o.sddmm_lanes_per_row == 64) {
     int rc = grid_for(rows, 4, "CSR row-wise map", &grid);
     if (rc)
       return rc;
-    hipLaunchKernelGGL(rowwise_map_wave, dim3((unsigned)grid), dim3(256), 0,
+    hipLaunchKernelGGL(rowwise_map_wave<T>, dim3((unsigned)grid), dim3(256), 0,
                        st, ro, val, rowv, out, (int32_t)rows, kind);
   } else {
     const int64_t B = o.rowwise_map_block_size;
     int rc = grid_for(rows, B, "CSR row-wise map", &grid);
     if (rc)
       return rc;
-    hipLaunchKernelGGL(rowwise_map_thread, dim3((unsigned)grid),
+    hipLaunchKernelGGL(rowwise_map_thread<T>, dim3((unsigned)grid),
                        dim3((unsigned)B), 0, st, ro, val, rowv, out,
                        (int32_t)rows, kind);
   }
   return launch_check("CSR row-wise map kernel");
+}
+
+// ---- entry points (fp32 and bf16 share them) --------------------------------
+
+template <typename T>
+int sddmm_entry(const int32_t *row_offsets, const int32_t *column_indices,
+                const T *values, const T *lhs, const T *rhs, T *output_values,
+                int64_t rows, int64_t cols, int64_t nnz, int64_t kdim,
+                int combine, float alpha, float beta, const sw_options *opts,
+                void *stream) {
+  clear_error();
+  sw_options o;
+  int rc = resolve_options(opts, &o);
+  if (rc)
+    return rc;
+  if (combine != SW_SDDMM_MUL && combine != SW_SDDMM_AFFINE &&
+      combine != SW_SDDMM_DOT)
+    return fail(SW_ERR_INVALID_ARGUMENT, "unknown SDDMM combine kind %d",
+                combine);
+  rc = check_csr(row_offsets, column_indices,
+                 combine == SW_SDDMM_DOT ? (const void *)output_values
+                                         : (const void *)values,
+                 rows, nnz, true);
+  if (rc)
+    return rc;
+  if (cols < 0 || kdim < 0 || kdim > INT32_MAX)
+    return fail(SW_ERR_INVALID_SHAPE, "invalid SDDMM dense shapes");
+  if (rows == 0 || nnz == 0)
+    return SW_OK;
+  if (!output_values || (kdim > 0 && (!lhs || !rhs)))
+    return fail(SW_ERR_INVALID_ARGUMENT, "SDDMM operand pointer is null");
+  return launch_sddmm<T>(row_offsets, column_indices,
+                         combine == SW_SDDMM_DOT ? nullptr : values, lhs, rhs,
+                         output_values, rows, cols, nnz, kdim, combine, alpha,
+                         beta, o, as_stream(stream));
+}
+
+template <typename T>
+int row_reduce_entry(const int32_t *row_offsets, const int32_t *column_indices,
+                     const T *values, T *output, int64_t rows, int64_t nnz,
+                     const char *kind, const sw_options *opts, void *stream) {
+  clear_error();
+  sw_options o;
+  int rc = resolve_options(opts, &o);
+  if (rc)
+    return rc;
+  if (!kind || (!streq(kind, "sum") && !streq(kind, "max")))
+    return fail(SW_ERR_INVALID_ARGUMENT,
+                "expected CSR row reduction kind 'sum' or 'max', but got '%s'",
+                kind ? kind : "(null)");
+  rc = check_csr(row_offsets, column_indices, values, rows, nnz, false);
+  if (rc)
+    return rc;
+  if (rows == 0)
+    return SW_OK;
+  if (!output)
+    return fail(SW_ERR_INVALID_ARGUMENT, "output pointer is null");
+  return launch_row_reduce<T>(row_offsets, values, output, rows,
+                              streq(kind, "max"), o, as_stream(stream));
+}
+
+template <typename T>
+int rowwise_map_entry(const int32_t *row_offsets,
+                      const int32_t *column_indices, const T *values,
+                      const T *row_values, T *output_values, int64_t rows,
+                      int64_t nnz, int map, const sw_options *opts,
+                      void *stream) {
+  clear_error();
+  sw_options o;
+  int rc = resolve_options(opts, &o);
+  if (rc)
+    return rc;
+  if (map < SW_MAP_EXP_SUB || map > SW_MAP_MUL)
+    return fail(SW_ERR_INVALID_ARGUMENT, "unknown row-wise map kind %d", map);
+  rc = check_csr(row_offsets, column_indices, values, rows, nnz, false);
+  if (rc)
+    return rc;
+  if (rows == 0 || nnz == 0)
+    return SW_OK;
+  if (!output_values || !row_values)
+    return fail(SW_ERR_INVALID_ARGUMENT, "row-wise map pointer is null");
+  return launch_rowwise_map<T>(row_offsets, values, row_values, output_values,
+                               rows, map, o, as_stream(stream));
+}
+
+// The whole chain in one kernel per 16-row tile when the options ask for
+// matrix-core tiles and the shapes fit the fused kernel; returns true when it
+// was launched (rc holds the launch status).
+bool launch_fused_attention(const int32_t *ro, const int32_t *col,
+                            const float *mask, const float *q,
+                            const float *kt, const float *v, float *scores,
+                            float *rmax, float *rsum, float *out,
+                            int64_t rows, int64_t cols, int64_t nnz,
+                            int64_t d, int64_t dv, float alpha, float beta,
+                            hipStream_t st, int *rc) {
+  if (!((d == 64 || d == 128) && dv > 0 && dv % 16 == 0 &&
+        narrow_offsets(nnz, 1) && narrow_offsets(cols, d) &&
+        narrow_offsets(cols, dv)))
+    return false;
+  int64_t grid;
+  *rc = grid_for(rows, 16, "fused attention", &grid);
+  if (*rc)
+    return true;
+#define SW_FUSED(KB)                                                          \
+  hipLaunchKernelGGL((attention_tile_fused<KB, kFusedWaves>),                 \
+                     dim3((unsigned)grid), dim3(64 * kFusedWaves), 0, st, ro, \
+                     col, mask, q, kt, v, scores, rmax, rsum, out,            \
+                     (int32_t)rows, cols, (int32_t)d, dv, alpha, beta)
+  if (d == 64)
+    SW_FUSED(1);
+  else
+    SW_FUSED(2);
+#undef SW_FUSED
+  *rc = launch_check("fused attention kernel");
+  return true;
+}
+
+bool launch_fused_attention(const int32_t *ro, const int32_t *col,
+                            const uint16_t *mask, const uint16_t *q,
+                            const uint16_t *kt, const uint16_t *v,
+                            uint16_t *scores, uint16_t *rmax, uint16_t *rsum,
+                            uint16_t *out, int64_t rows, int64_t cols,
+                            int64_t nnz, int64_t d, int64_t dv, float alpha,
+                            float beta, hipStream_t st, int *rc) {
+  if (!((d == 64 || d == 128) && dv > 0 && dv % 64 == 0 && aligned16(q) &&
+        (reinterpret_cast<uintptr_t>(v) & 7u) == 0 &&
+        (reinterpret_cast<uintptr_t>(out) & 7u) == 0 &&
+        narrow_offsets(nnz, 1) && narrow_offsets(cols, d) &&
+        narrow_offsets(cols, dv)))
+    return false;
+  int64_t grid;
+  *rc = grid_for(rows, 16, "fused attention", &grid);
+  if (*rc)
+    return true;
+#define SW_FUSED(KB)                                                          \
+  hipLaunchKernelGGL((attention_tile_fused_bf16<KB, kFusedWaves>),            \
+                     dim3((unsigned)grid), dim3(64 * kFusedWaves), 0, st, ro, \
+                     col, mask, q, kt, v, scores, rmax, rsum, out,            \
+                     (int32_t)rows, cols, (int32_t)d, dv, alpha, beta)
+  if (d == 64)
+    SW_FUSED(1);
+  else
+    SW_FUSED(2);
+#undef SW_FUSED
+  *rc = launch_check("fused attention kernel");
+  return true;
+}
+
+template <typename T>
+int attention_entry(const int32_t *row_offsets, const int32_t *column_indices,
+                    const T *mask_values, const T *query,
+                    const T *transposed_key, const T *value, T *scores,
+                    T *row_maximum, T *row_sum, T *output, int64_t rows,
+                    int64_t cols, int64_t nnz, int64_t d, int64_t dv,
+                    float alpha, float beta, const sw_options *opts,
+                    void *stream) {
+  clear_error();
+  sw_options o;
+  int rc = resolve_options(opts, &o);
+  if (rc)
+    return rc;
+  rc = check_csr(row_offsets, column_indices, mask_values, rows, nnz, true);
+  if (rc)
+    return rc;
+  if (cols < 0 || d < 0 || dv < 0 || d > INT32_MAX)
+    return fail(SW_ERR_INVALID_SHAPE, "invalid attention shapes");
+  if (rows == 0)
+    return SW_OK;
+  if (!row_maximum || !row_sum || (dv > 0 && !output) ||
+      (nnz > 0 && (!scores || !query || !transposed_key || (dv > 0 && !value))))
+    return fail(SW_ERR_INVALID_ARGUMENT, "attention buffer pointer is null");
+  hipStream_t st = as_stream(stream);
+  if (nnz > 0 && o.sddmm_lanes_per_row == 64 &&
+      streq(o.sddmm_mapping, "row-tile-mfma") &&
+      streq(o.spmm_mapping, "row-tile-mfma") &&
+      launch_fused_attention(row_offsets, column_indices, mask_values, query,
+                             transposed_key, value, scores, row_maximum,
+                             row_sum, output, rows, cols, nnz, d, dv, alpha,
+                             beta, st, &rc))
+    return rc;
+  if (nnz > 0) {
+    rc = launch_sddmm<T>(row_offsets, column_indices, mask_values, query,
+                         transposed_key, scores, rows, cols, nnz, d,
+                         SW_SDDMM_AFFINE, alpha, beta, o, st);
+    if (rc)
+      return rc;
+  }
+  if (o.sddmm_lanes_per_row == 64) {
+    // wave row ops: the four softmax ops run as one kernel
+    int64_t grid = std::max<int64_t>(ceil_div(rows, 4), 1);
+    rc = check_grid(grid, "attention softmax");
+    if (rc)
+      return rc;
+    hipLaunchKernelGGL(row_softmax_wave<T>, dim3((unsigned)grid), dim3(256), 0,
+                       st, row_offsets, scores, row_maximum, row_sum,
+                       (int32_t)rows);
+    rc = launch_check("attention softmax kernel");
+    if (rc)
+      return rc;
+    if (dv == 0)
+      return SW_OK;
+    return launch_spmm(row_offsets, column_indices, scores, value, output,
+                       rows, cols, nnz, dv, o, "attention output SpMM", st);
+  }
+  rc = launch_row_reduce<T>(row_offsets, scores, row_maximum, rows, true, o,
+                            st);
+  if (rc)
+    return rc;
+  if (nnz > 0) {
+    rc = launch_rowwise_map<T>(row_offsets, scores, row_maximum, scores, rows,
+                               SW_MAP_EXP_SUB, o, st);
+    if (rc)
+      return rc;
+  }
+  rc = launch_row_reduce<T>(row_offsets, scores, row_sum, rows, false, o, st);
+  if (rc)
+    return rc;
+  if (nnz > 0) {
+    rc = launch_rowwise_map<T>(row_offsets, scores, row_sum, scores, rows,
+                               SW_MAP_DIV, o, st);
+    if (rc)
+      return rc;
+  }
+  if (dv == 0)
+    return SW_OK;
+  return launch_spmm(row_offsets, column_indices, scores, value, output, rows,
+                     cols, nnz, dv, o, "attention output SpMM", st);
 }
 
 } // namespace sw
@@ -945,30 +1634,22 @@ extern "C" int sw_sddmm_csr_f32(const int32_t *row_offsets,
                                 int64_t kdim, int combine, float alpha,
                                 float beta, const sw_options *opts,
                                 void *stream) {
-  sw::clear_error();
-  sw_options o;
-  int rc = sw::resolve_options(opts, &o);
-  if (rc)
-    return rc;
-  if (combine != SW_SDDMM_MUL && combine != SW_SDDMM_AFFINE &&
-      combine != SW_SDDMM_DOT)
-    return sw::fail(SW_ERR_INVALID_ARGUMENT, "unknown SDDMM combine kind %d",
-                    combine);
-  rc = sw::check_csr(row_offsets, column_indices,
-                     combine == SW_SDDMM_DOT ? output_values : values, rows,
-                     nnz, true);
-  if (rc)
-    return rc;
-  if (cols < 0 || kdim < 0 || kdim > INT32_MAX)
-    return sw::fail(SW_ERR_INVALID_SHAPE, "invalid SDDMM dense shapes");
-  if (rows == 0 || nnz == 0)
-    return SW_OK;
-  if (!output_values || (kdim > 0 && (!lhs || !rhs)))
-    return sw::fail(SW_ERR_INVALID_ARGUMENT, "SDDMM operand pointer is null");
-  return sw::launch_sddmm(row_offsets, column_indices,
-                          combine == SW_SDDMM_DOT ? nullptr : values, lhs, rhs,
-                          output_values, rows, cols, kdim, combine, alpha,
-                          beta, o, sw::as_stream(stream));
+  return sw::sddmm_entry<float>(row_offsets, column_indices, values, lhs, rhs,
+                                output_values, rows, cols, nnz, kdim, combine,
+                                alpha, beta, opts, stream);
+}
+
+extern "C" int sw_sddmm_csr_bf16(const int32_t *row_offsets,
+                                 const int32_t *column_indices,
+                                 const uint16_t *values, const uint16_t *lhs,
+                                 const uint16_t *rhs, uint16_t *output_values,
+                                 int64_t rows, int64_t cols, int64_t nnz,
+                                 int64_t kdim, int combine, float alpha,
+                                 float beta, const sw_options *opts,
+                                 void *stream) {
+  return sw::sddmm_entry<uint16_t>(row_offsets, column_indices, values, lhs,
+                                   rhs, output_values, rows, cols, nnz, kdim,
+                                   combine, alpha, beta, opts, stream);
 }
 
 extern "C" int sw_csr_row_reduce_f32(const int32_t *row_offsets,
@@ -977,27 +1658,18 @@ extern "C" int sw_csr_row_reduce_f32(const int32_t *row_offsets,
                                      int64_t rows, int64_t nnz,
                                      const char *kind, const sw_options *opts,
                                      void *stream) {
-  (void)column_indices;
-  sw::clear_error();
-  sw_options o;
-  int rc = sw::resolve_options(opts, &o);
-  if (rc)
-    return rc;
-  if (!kind || (!sw::streq(kind, "sum") && !sw::streq(kind, "max")))
-    return sw::fail(SW_ERR_INVALID_ARGUMENT,
-                    "expected CSR row reduction kind 'sum' or 'max', but got "
-                    "'%s'",
-                    kind ? kind : "(null)");
-  rc = sw::check_csr(row_offsets, column_indices, values, rows, nnz, false);
-  if (rc)
-    return rc;
-  if (rows == 0)
-    return SW_OK;
-  if (!output)
-    return sw::fail(SW_ERR_INVALID_ARGUMENT, "output pointer is null");
-  return sw::launch_row_reduce(row_offsets, values, output, rows,
-                               sw::streq(kind, "max"), o,
-                               sw::as_stream(stream));
+  return sw::row_reduce_entry<float>(row_offsets, column_indices, values,
+                                     output, rows, nnz, kind, opts, stream);
+}
+
+extern "C" int sw_csr_row_reduce_bf16(const int32_t *row_offsets,
+                                      const int32_t *column_indices,
+                                      const uint16_t *values, uint16_t *output,
+                                      int64_t rows, int64_t nnz,
+                                      const char *kind, const sw_options *opts,
+                                      void *stream) {
+  return sw::row_reduce_entry<uint16_t>(row_offsets, column_indices, values,
+                                        output, rows, nnz, kind, opts, stream);
 }
 
 extern "C" int sw_csr_rowwise_map_f32(const int32_t *row_offsets,
@@ -1007,24 +1679,21 @@ extern "C" int sw_csr_rowwise_map_f32(const int32_t *row_offsets,
                                       float *output_values, int64_t rows,
                                       int64_t nnz, int map,
                                       const sw_options *opts, void *stream) {
-  (void)column_indices;
-  sw::clear_error();
-  sw_options o;
-  int rc = sw::resolve_options(opts, &o);
-  if (rc)
-    return rc;
-  if (map < SW_MAP_EXP_SUB || map > SW_MAP_MUL)
-    return sw::fail(SW_ERR_INVALID_ARGUMENT, "unknown row-wise map kind %d",
-                    map);
-  rc = sw::check_csr(row_offsets, column_indices, values, rows, nnz, false);
-  if (rc)
-    return rc;
-  if (rows == 0 || nnz == 0)
-    return SW_OK;
-  if (!output_values || !row_values)
-    return sw::fail(SW_ERR_INVALID_ARGUMENT, "row-wise map pointer is null");
-  return sw::launch_rowwise_map(row_offsets, values, row_values, output_values,
-                                rows, map, o, sw::as_stream(stream));
+  return sw::rowwise_map_entry<float>(row_offsets, column_indices, values,
+                                      row_values, output_values, rows, nnz,
+                                      map, opts, stream);
+}
+
+extern "C" int sw_csr_rowwise_map_bf16(const int32_t *row_offsets,
+                                       const int32_t *column_indices,
+                                       const uint16_t *values,
+                                       const uint16_t *row_values,
+                                       uint16_t *output_values, int64_t rows,
+                                       int64_t nnz, int map,
+                                       const sw_options *opts, void *stream) {
+  return sw::rowwise_map_entry<uint16_t>(row_offsets, column_indices, values,
+                                         row_values, output_values, rows, nnz,
+                                         map, opts, stream);
 }
 
 extern "C" int sw_sparse_attention_f32(
@@ -1034,91 +1703,21 @@ extern "C" int sw_sparse_attention_f32(
     float *output, int64_t rows, int64_t cols, int64_t nnz, int64_t d,
     int64_t dv, float alpha, float beta, const sw_options *opts,
     void *stream) {
-  sw::clear_error();
-  sw_options o;
-  int rc = sw::resolve_options(opts, &o);
-  if (rc)
-    return rc;
-  rc = sw::check_csr(row_offsets, column_indices, mask_values, rows, nnz, true);
-  if (rc)
-    return rc;
-  if (cols < 0 || d < 0 || dv < 0 || d > INT32_MAX)
-    return sw::fail(SW_ERR_INVALID_SHAPE, "invalid attention shapes");
-  if (rows == 0)
-    return SW_OK;
-  if (!row_maximum || !row_sum || (dv > 0 && !output) ||
-      (nnz > 0 && (!scores || !query || !transposed_key || (dv > 0 && !value))))
-    return sw::fail(SW_ERR_INVALID_ARGUMENT, "attention buffer pointer is null");
-  hipStream_t st = sw::as_stream(stream);
-  if (nnz > 0 && o.sddmm_lanes_per_row == 64 &&
-      sw::streq(o.sddmm_mapping, "row-tile-mfma") &&
-      sw::streq(o.spmm_mapping, "row-tile-mfma") && (d == 64 || d == 128) &&
-      dv > 0 && dv % 16 == 0 && sw::narrow_offsets(nnz, 1) &&
-      sw::narrow_offsets(cols, d) && sw::narrow_offsets(cols, dv)) {
-    // the whole chain in one kernel per 16-row tile (its loads and stores
-    // take 32-bit byte offsets from wave-uniform bases)
-    int64_t grid;
-    rc = grid_for(rows, 16, "fused attention", &grid);
-    if (rc)
-      return rc;
-#define SW_FUSED(KB)                                                          \
-  hipLaunchKernelGGL((attention_tile_fused<KB, kFusedWaves>),                 \
-                     dim3((unsigned)grid), dim3(64 * kFusedWaves), 0, st,     \
-                     row_offsets, column_indices, mask_values, query,         \
-                     transposed_key, value, scores, row_maximum, row_sum,     \
-                     output, (int32_t)rows, cols, (int32_t)d, dv, alpha, beta)
-    if (d == 64)
-      SW_FUSED(1);
-    else
-      SW_FUSED(2);
-#undef SW_FUSED
-    return sw::launch_check("fused attention kernel");
-  }
-  if (nnz > 0) {
-    rc = sw::launch_sddmm(row_offsets, column_indices, mask_values, query,
-                          transposed_key, scores, rows, cols, d,
-                          SW_SDDMM_AFFINE, alpha, beta, o, st);
-    if (rc)
-      return rc;
-  }
-  if (o.sddmm_lanes_per_row == 64) {
-    // wave row ops: the four softmax ops run as one kernel
-    int64_t grid = std::max<int64_t>(sw::ceil_div(rows, 4), 1);
-    rc = sw::check_grid(grid, "attention softmax");
-    if (rc)
-      return rc;
-    hipLaunchKernelGGL(row_softmax_wave, dim3((unsigned)grid), dim3(256), 0,
-                       st, row_offsets, scores, row_maximum, row_sum,
-                       (int32_t)rows);
-    rc = sw::launch_check("attention softmax kernel");
-    if (rc)
-      return rc;
-    if (dv == 0)
-      return SW_OK;
-    return sw::launch_spmm(row_offsets, column_indices, scores, value, output,
-                           rows, cols, nnz, dv, o, "attention output SpMM",
-                           st);
-  }
-  rc = sw::launch_row_reduce(row_offsets, scores, row_maximum, rows, true, o, st);
-  if (rc)
-    return rc;
-  if (nnz > 0) {
-    rc = sw::launch_rowwise_map(row_offsets, scores, row_maximum, scores, rows,
-                                SW_MAP_EXP_SUB, o, st);
-    if (rc)
-      return rc;
-  }
-  rc = sw::launch_row_reduce(row_offsets, scores, row_sum, rows, false, o, st);
-  if (rc)
-    return rc;
-  if (nnz > 0) {
-    rc = sw::launch_rowwise_map(row_offsets, scores, row_sum, scores, rows,
-                                SW_MAP_DIV, o, st);
-    if (rc)
-      return rc;
-  }
-  if (dv == 0)
-    return SW_OK;
-  return sw::launch_spmm(row_offsets, column_indices, scores, value, output,
-                         rows, cols, nnz, dv, o, "attention output SpMM", st);
+  return sw::attention_entry<float>(
+      row_offsets, column_indices, mask_values, query, transposed_key, value,
+      scores, row_maximum, row_sum, output, rows, cols, nnz, d, dv, alpha,
+      beta, opts, stream);
+}
+
+extern "C" int sw_sparse_attention_bf16(
+    const int32_t *row_offsets, const int32_t *column_indices,
+    const uint16_t *mask_values, const uint16_t *query,
+    const uint16_t *transposed_key, const uint16_t *value, uint16_t *scores,
+    uint16_t *row_maximum, uint16_t *row_sum, uint16_t *output, int64_t rows,
+    int64_t cols, int64_t nnz, int64_t d, int64_t dv, float alpha, float beta,
+    const sw_options *opts, void *stream) {
+  return sw::attention_entry<uint16_t>(
+      row_offsets, column_indices, mask_values, query, transposed_key, value,
+      scores, row_maximum, row_sum, output, rows, cols, nnz, d, dv, alpha,
+      beta, opts, stream);
 }

@@ -23,25 +23,12 @@ using namespace swd;
 
 namespace {
 
-typedef short v4s __attribute__((ext_vector_type(4)));
-
 // thread-per-output for any block size: one thread per output element.
-template <typename T>
-__device__ __forceinline__ float to_f32(T v);
-template <>
-__device__ __forceinline__ float to_f32<float>(float v) {
-  return v;
-}
-template <>
-__device__ __forceinline__ float to_f32<uint16_t>(uint16_t v) {
-  return __uint_as_float((uint32_t)v << 16);
-}
-
-template <typename T>
+template <typename T, typename TO>
 __global__ __launch_bounds__(1024) void bsr_thread_per_output(
     const int32_t *__restrict__ bro, const int32_t *__restrict__ bcol,
     const T *__restrict__ bval, const T *__restrict__ rhs,
-    float *__restrict__ out, int64_t rows, int64_t k, int32_t b) {
+    TO *__restrict__ out, int64_t rows, int64_t k, int32_t b) {
   int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= rows * k)
     return;
@@ -52,10 +39,9 @@ __global__ __launch_bounds__(1024) void bsr_thread_per_output(
     const T *blk = bval + (int64_t)bp * b * b + lr * b;
     int64_t rb = (int64_t)bcol[bp] * b;
     for (int32_t lc = 0; lc < b; ++lc)
-      acc = __builtin_fmaf(to_f32<T>(blk[lc]), to_f32<T>(rhs[(rb + lc) * k + c]),
-                           acc);
+      acc = __builtin_fmaf(tof(blk[lc]), tof(rhs[(rb + lc) * k + c]), acc);
   }
-  out[e] = acc;
+  stv(out + e, acc);
 }
 
 // MFMA operand layouts (one 16 x 16 x K step, wave64, lane l):
@@ -139,11 +125,11 @@ __global__ __launch_bounds__(256) void bsr16_mfma_f32(
   }
 }
 
-template <int NB>
+template <int NB, typename TO>
 __global__ __launch_bounds__(256) void bsr16_mfma_bf16(
     const int32_t *__restrict__ bro, const int32_t *__restrict__ bcol,
     const uint16_t *__restrict__ bval, const uint16_t *__restrict__ rhs,
-    float *__restrict__ out, int64_t k, int nbr) {
+    TO *__restrict__ out, int64_t k, int nbr) {
   const int br = xcd_block_row(blockIdx.x, nbr);
   const int wave = threadIdx.x / kWave;
   const int l = lane_id();
@@ -184,13 +170,98 @@ __global__ __launch_bounds__(256) void bsr16_mfma_bf16(
   }
   // non-temporal stores: the output is not re-read, so it should not
   // displace RHS tiles from the caches
-  float *o = out + ((int64_t)br * 16 + g * 4) * k;
+  TO *o = out + ((int64_t)br * 16 + g * 4) * k;
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
     if (ok0)
-      __builtin_nontemporal_store(acc0[v], o + v * k + c0);
+      st1_nt(o + v * k + c0, acc0[v]);
     if (ok1)
-      __builtin_nontemporal_store(acc1[v], o + v * k + c1);
+      st1_nt(o + v * k + c1, acc1[v]);
+  }
+}
+
+// Column-interleaved bf16 kernel (k % 8 == 0, rhs and output 16-byte
+// aligned).  A wave owns one block row and a 128-column strip as eight
+// 16 x 16 tiles whose columns interleave -- tile t's MFMA column j is strip
+// column 8j + t -- so one 128-bit load of an RHS row gives a lane its eight
+// columns' values, one per tile: per block a lane issues one 64-bit A load
+// and four 128-bit B loads (the block's 16 x 128 RHS slab in four wave
+// instructions), then eight v_mfma_f32_16x16x16_bf16.  The B operand of tile
+// t is element t of the four loaded rows (lane group g: rows 4g .. 4g+3).
+// Each lane ends with eight consecutive columns of four output rows: one
+// 128-bit (bf16) or two 128-bit (fp32) stores per row.  Blocks are taken in
+// batches of NB, all loads of a batch before its MFMAs; waves of a
+// workgroup take consecutive block rows, workgroups in XCD-contiguous order.
+template <int NB, int WPB, typename TO>
+__global__ __launch_bounds__(64 * WPB) void bsr16_mfma_bf16_x8(
+    const int32_t *__restrict__ bro, const int32_t *__restrict__ bcol,
+    const uint16_t *__restrict__ bval, const uint16_t *__restrict__ rhs,
+    TO *__restrict__ out, int64_t k, int nbr) {
+  const int64_t br = xcd_contiguous(blockIdx.x, gridDim.x) * WPB +
+                     threadIdx.x / kWave;
+  if (br >= nbr)
+    return; // wave-uniform; the kernel has no barrier
+  const int l = lane_id();
+  const int j = l & 15, g = l >> 4;
+  const int64_t cb = (int64_t)blockIdx.y * 128 + 8 * j;
+  const bool ok = cb < k; // k % 8 == 0: all eight columns or none
+  v4f acc[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t)
+    acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
+  const int32_t s = bro[br], e = bro[br + 1];
+  for (int32_t b0 = s; b0 < e; b0 += NB) {
+    const int nb = e - b0 < NB ? e - b0 : NB; // wave-uniform
+    const int bcl = l < nb ? bcol[b0 + l] : 0;
+    v2u a[NB];
+    v4u q[NB][4];
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      if (u < nb) {
+        const int64_t bc = __builtin_amdgcn_readlane(bcl, u);
+        // A[j][4g .. 4g+3] of block b0 + u: 8 contiguous bytes
+        a[u] = ld_stream(reinterpret_cast<const v2u *>(
+            bval + (int64_t)(b0 + u) * 256 + j * 16 + g * 4));
+        const uint16_t *brow = rhs + (bc * 16 + g * 4) * k + cb;
+#pragma unroll
+        for (int st = 0; st < 4; ++st)
+          q[u][st] = ok ? *reinterpret_cast<const v4u *>(brow + st * k)
+                        : v4u{0u, 0u, 0u, 0u};
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      if (u < nb) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+          // element t of the four rows: dword t / 2, half t % 2
+          const int d = t >> 1, sh = 16 * (t & 1);
+          const uint32_t e0 = (q[u][0][d] >> sh) & 0xFFFFu;
+          const uint32_t e1 = (q[u][1][d] >> sh) & 0xFFFFu;
+          const uint32_t e2 = (q[u][2][d] >> sh) & 0xFFFFu;
+          const uint32_t e3 = (q[u][3][d] >> sh) & 0xFFFFu;
+          acc[t] = mfma_16x16x16_bf16(a[u], v2u{e0 | (e1 << 16), e2 | (e3 << 16)},
+                                      acc[t]);
+        }
+      }
+    }
+  }
+  if (ok) {
+    TO *o = out + (br * 16 + g * 4) * k + cb;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      if constexpr (sizeof(TO) == 2) {
+        __builtin_nontemporal_store(
+            v4u{pack_bf16x2(acc[0][v], acc[1][v]),
+                pack_bf16x2(acc[2][v], acc[3][v]),
+                pack_bf16x2(acc[4][v], acc[5][v]),
+                pack_bf16x2(acc[6][v], acc[7][v])},
+            reinterpret_cast<v4u *>(o + v * k));
+      } else {
+        st4_nt(o + v * k, v4f{acc[0][v], acc[1][v], acc[2][v], acc[3][v]});
+        st4_nt(o + v * k + 4, v4f{acc[4][v], acc[5][v], acc[6][v], acc[7][v]});
+      }
+    }
   }
 }
 
@@ -263,7 +334,7 @@ __global__ __launch_bounds__(256) void bsr16_mfma_f32_x4(
 }
 
 int check_bsr(const int32_t *bro, const int32_t *bcol, const void *bval,
-              const void *rhs, const float *out, int64_t rows, int64_t cols,
+              const void *rhs, const void *out, int64_t rows, int64_t cols,
               int64_t nnzb, int64_t k, int64_t b) {
   if (b < 1)
     return sw::fail(SW_ERR_INVALID_SHAPE,
@@ -289,27 +360,44 @@ int check_bsr(const int32_t *bro, const int32_t *bcol, const void *bval,
   return SW_OK;
 }
 
-template <typename T>
+// bf16 x8 kernel shape: blocks per batch and waves (block rows) per
+// workgroup
+constexpr int kBf16Batch = 4;
+constexpr int kBf16Waves = 4;
+
+template <typename T, typename TO>
 int launch_bsr(const int32_t *bro, const int32_t *bcol, const T *bval,
-               const T *rhs, float *out, int64_t rows, int64_t nnzb,
-               int64_t k, int64_t b, const sw_options &o, hipStream_t st,
-               bool mfma_ok) {
+               const T *rhs, TO *out, int64_t rows, int64_t nnzb, int64_t k,
+               int64_t b, const sw_options &o, hipStream_t st, bool mfma_ok) {
   (void)nnzb;
   if (rows == 0 || k == 0)
     return SW_OK;
-  // fp32 with k % 4 == 0 takes the column-interleaved kernel (measured on
-  // configuration 4: 167 us against 189 us); for bf16 the interleaved form
-  // measured slower (92 us against 81 us), so bf16 keeps the scalar loads
+  const int nbr = (int)(rows / 16);
   if constexpr (sizeof(T) == 4) {
+    // fp32 with k % 4 == 0 takes the column-interleaved kernel (measured on
+    // configuration 4: 167 us against 189 us)
     if (mfma_ok && k % 4 == 0 && sw::aligned16(rhs) && sw::aligned16(out)) {
       const int64_t strips = std::min<int64_t>(4, sw::ceil_div(k, 64));
       const int64_t gy = sw::ceil_div(k, 64 * strips);
       if (gy > 65535)
         return sw::fail(SW_ERR_INVALID_SHAPE, "rhs has too many columns");
-      const int nbr = (int)(rows / 16);
       hipLaunchKernelGGL(bsr16_mfma_f32_x4<4>, dim3((unsigned)nbr, (unsigned)gy),
                          dim3((unsigned)(64 * strips)), 0, st, bro, bcol, bval,
                          rhs, out, k, nbr);
+      return sw::launch_check("BSR MFMA kernel");
+    }
+  } else {
+    // bf16 with k % 8 == 0: eight interleaved tiles per wave, 128-bit RHS
+    // loads
+    if (mfma_ok && k % 8 == 0 && sw::aligned16(rhs) && sw::aligned16(out)) {
+      const int64_t gx = sw::ceil_div(nbr, kBf16Waves);
+      const int64_t gy = sw::ceil_div(k, 128);
+      if (gy > 65535)
+        return sw::fail(SW_ERR_INVALID_SHAPE, "rhs has too many columns");
+      hipLaunchKernelGGL((bsr16_mfma_bf16_x8<kBf16Batch, kBf16Waves, TO>),
+                         dim3((unsigned)gx, (unsigned)gy),
+                         dim3(64 * kBf16Waves), 0, st, bro, bcol, bval, rhs,
+                         out, k, nbr);
       return sw::launch_check("BSR MFMA kernel");
     }
   }
@@ -317,13 +405,12 @@ int launch_bsr(const int32_t *bro, const int32_t *bcol, const T *bval,
     int64_t gy = sw::ceil_div(k, 128);
     if (gy > 65535)
       return sw::fail(SW_ERR_INVALID_SHAPE, "rhs has too many columns");
-    const int nbr = (int)(rows / 16);
     dim3 grid((unsigned)nbr, (unsigned)gy);
     if constexpr (sizeof(T) == 4)
       hipLaunchKernelGGL(bsr16_mfma_f32<8>, grid, dim3(256), 0, st, bro, bcol,
                          bval, rhs, out, k, nbr);
     else
-      hipLaunchKernelGGL(bsr16_mfma_bf16<8>, grid, dim3(256), 0, st, bro,
+      hipLaunchKernelGGL((bsr16_mfma_bf16<8, TO>), grid, dim3(256), 0, st, bro,
                          bcol, bval, rhs, out, k, nbr);
     return sw::launch_check("BSR MFMA kernel");
   }
@@ -332,10 +419,38 @@ int launch_bsr(const int32_t *bro, const int32_t *bcol, const T *bval,
   int rc = sw::check_grid(grid, "BSR SpMM");
   if (rc)
     return rc;
-  hipLaunchKernelGGL(bsr_thread_per_output<T>, dim3((unsigned)grid),
+  hipLaunchKernelGGL((bsr_thread_per_output<T, TO>), dim3((unsigned)grid),
                      dim3((unsigned)B), 0, st, bro, bcol, bval, rhs, out, rows,
                      k, (int32_t)b);
   return sw::launch_check("thread-per-output BSR SpMM kernel");
+}
+
+template <typename T, typename TO>
+int bsr_entry(const int32_t *block_row_offsets,
+              const int32_t *block_column_indices, const T *block_values,
+              const T *rhs, TO *output, int64_t rows, int64_t cols,
+              int64_t nnzb, int64_t k, int64_t block_size,
+              const sw_options *opts, void *stream) {
+  sw::clear_error();
+  sw_options o;
+  int rc = sw::resolve_options(opts, &o);
+  if (rc)
+    return rc;
+  rc = check_bsr(block_row_offsets, block_column_indices, block_values, rhs,
+                 output, rows, cols, nnzb, k, block_size);
+  if (rc)
+    return rc;
+  // the MFMA kernels read A rows of a block as 16-byte (fp32) or 8-byte
+  // (bf16) vectors
+  const bool mfma = o.bsr_use_mfma && block_size == 16 &&
+                    (reinterpret_cast<uintptr_t>(block_values) &
+                     (4 * sizeof(T) - 1)) == 0;
+  if constexpr (sizeof(TO) == 2)
+    if (mfma && (reinterpret_cast<uintptr_t>(output) & 1u) != 0)
+      return sw::fail(SW_ERR_INVALID_ARGUMENT, "bf16 output is misaligned");
+  return launch_bsr<T, TO>(block_row_offsets, block_column_indices,
+                           block_values, rhs, output, rows, nnzb, k,
+                           block_size, o, sw::as_stream(stream), mfma);
 }
 
 } // namespace
@@ -346,41 +461,33 @@ extern "C" int sw_bsr_spmm_f32(const int32_t *block_row_offsets,
                                float *output, int64_t rows, int64_t cols,
                                int64_t nnzb, int64_t k, int64_t block_size,
                                const sw_options *opts, void *stream) {
-  sw::clear_error();
-  sw_options o;
-  int rc = sw::resolve_options(opts, &o);
-  if (rc)
-    return rc;
-  rc = check_bsr(block_row_offsets, block_column_indices, block_values, rhs,
-                 output, rows, cols, nnzb, k, block_size);
-  if (rc)
-    return rc;
-  bool mfma = o.bsr_use_mfma && block_size == 16 &&
-              sw::aligned16(block_values);
-  return launch_bsr<float>(block_row_offsets, block_column_indices,
-                           block_values, rhs, output, rows, nnzb, k,
-                           block_size, o, sw::as_stream(stream), mfma);
+  return bsr_entry<float, float>(block_row_offsets, block_column_indices,
+                                 block_values, rhs, output, rows, cols, nnzb,
+                                 k, block_size, opts, stream);
 }
 
 extern "C" int sw_bsr_spmm_bf16(const int32_t *block_row_offsets,
                                 const int32_t *block_column_indices,
                                 const uint16_t *block_values,
-                                const uint16_t *rhs, float *output,
+                                const uint16_t *rhs, uint16_t *output,
                                 int64_t rows, int64_t cols, int64_t nnzb,
                                 int64_t k, int64_t block_size,
                                 const sw_options *opts, void *stream) {
-  sw::clear_error();
-  sw_options o;
-  int rc = sw::resolve_options(opts, &o);
-  if (rc)
-    return rc;
-  rc = check_bsr(block_row_offsets, block_column_indices, block_values, rhs,
-                 output, rows, cols, nnzb, k, block_size);
-  if (rc)
-    return rc;
-  bool mfma = o.bsr_use_mfma && block_size == 16 &&
-              (reinterpret_cast<uintptr_t>(block_values) & 7u) == 0;
-  return launch_bsr<uint16_t>(block_row_offsets, block_column_indices,
-                              block_values, rhs, output, rows, nnzb, k,
-                              block_size, o, sw::as_stream(stream), mfma);
+  return bsr_entry<uint16_t, uint16_t>(block_row_offsets,
+                                       block_column_indices, block_values, rhs,
+                                       output, rows, cols, nnzb, k, block_size,
+                                       opts, stream);
+}
+
+extern "C" int sw_bsr_spmm_bf16_f32out(const int32_t *block_row_offsets,
+                                       const int32_t *block_column_indices,
+                                       const uint16_t *block_values,
+                                       const uint16_t *rhs, float *output,
+                                       int64_t rows, int64_t cols,
+                                       int64_t nnzb, int64_t k,
+                                       int64_t block_size,
+                                       const sw_options *opts, void *stream) {
+  return bsr_entry<uint16_t, float>(block_row_offsets, block_column_indices,
+                                    block_values, rhs, output, rows, cols,
+                                    nnzb, k, block_size, opts, stream);
 }

@@ -19,6 +19,10 @@ constexpr int kWave = 64;
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 __device__ __forceinline__ int lane_id() { return __lane_id(); }
 
@@ -160,6 +164,78 @@ __device__ __forceinline__ T ld_stream(const T *p) {
 template <typename T>
 __device__ __forceinline__ T ld_nontemporal(const T *p) {
   return __builtin_nontemporal_load(p);
+}
+
+// ---- bf16 storage ----------------------------------------------------------
+// bf16 operands travel as raw 16-bit patterns (uint16_t).  Kernels compute in
+// fp32: widening is exact, and every stored bf16 result is rounded to nearest
+// even once (v_cvt_pk_bf16_f32; NaN stays NaN, overflow rounds to inf).
+__device__ __forceinline__ float bf16_to_f32(uint32_t h) {
+  return __uint_as_float(h << 16);
+}
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
+}
+// bf16(lo) in bits 0..15, bf16(hi) in bits 16..31
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+}
+// fp32 value of an element stored as T (float, or bf16 bits as uint16_t)
+__device__ __forceinline__ float tof(float v) { return v; }
+__device__ __forceinline__ float tof(uint16_t v) { return bf16_to_f32(v); }
+template <typename T>
+__device__ __forceinline__ float ldv(const T *p) {
+  return tof(*p);
+}
+__device__ __forceinline__ void stv(float *p, float v) { *p = v; }
+__device__ __forceinline__ void stv(uint16_t *p, float v) {
+  *p = f32_to_bf16(v);
+}
+// Four consecutive elements as fp32 (16-byte aligned floats, 8-byte aligned
+// bf16), and their non-temporal store.
+__device__ __forceinline__ v4f ld4(const float *p) {
+  return *reinterpret_cast<const v4f *>(p);
+}
+__device__ __forceinline__ v4f ld4(const uint16_t *p) {
+  const v2u w = *reinterpret_cast<const v2u *>(p);
+  return v4f{bf16_to_f32(w.x & 0xFFFFu), bf16_to_f32(w.x >> 16),
+             bf16_to_f32(w.y & 0xFFFFu), bf16_to_f32(w.y >> 16)};
+}
+__device__ __forceinline__ void st4_nt(float *p, v4f v) {
+  __builtin_nontemporal_store(v, reinterpret_cast<v4f *>(p));
+}
+__device__ __forceinline__ void st4_nt(uint16_t *p, v4f v) {
+  __builtin_nontemporal_store(v2u{pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w)},
+                              reinterpret_cast<v2u *>(p));
+}
+template <typename T>
+__device__ __forceinline__ void st1_nt(T *p, float v) {
+  if constexpr (sizeof(T) == 4)
+    __builtin_nontemporal_store(v, reinterpret_cast<float *>(p));
+  else
+    __builtin_nontemporal_store(f32_to_bf16(v), reinterpret_cast<uint16_t *>(p));
+}
+
+// ---- bf16 matrix-core products ------------------------------------------------
+// D += A B over one 16 x 16 tile, fp32 accumulation.  Operand registers hold
+// bf16 pairs, element 2e in the low half of dword e.  Lane l supplies row (A)
+// or column (B) l % 16 of the operand and a block of K elements picked by
+// l / 16 -- the same K elements in A and in B, so any assignment of logical
+// K indices to (l / 16, element) works as long as both operands use it.  The
+// result is D[4 (l / 16) + v][l % 16] in accumulator register v.
+__device__ __forceinline__ v4f mfma_16x16x32_bf16(v4u a, v4u b, v4f c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+      __builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0,
+      0);
+}
+__device__ __forceinline__ v4f mfma_16x16x16_bf16(v2u a, v2u b, v4f c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
+      __builtin_bit_cast(v4s, a), __builtin_bit_cast(v4s, b), c, 0, 0, 0);
+}
+// Half n (0..3) of a 4-element bf16 vector held as two dwords.
+__device__ __forceinline__ uint32_t bf16_half(v2u w, int n) {
+  const uint32_t d = (n & 2) ? w.y : w.x;
+  return (n & 1) ? d >> 16 : d & 0xFFFFu;
 }
 
 // p advanced by b bytes.  With p wave-uniform this is the form the global

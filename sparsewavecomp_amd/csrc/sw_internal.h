@@ -62,19 +62,26 @@ inline int resolve_options(const sw_options *opts, sw_options *out) {
 
 inline bool streq(const char *a, const char *b) { return std::strcmp(a, b) == 0; }
 
+// Largest nnz a CSR operand may have.  Row loops step a position index past
+// the row's end by less than one step (at most 16 positions for each of up
+// to 1024 threads), so with nnz below INT32_MAX - 2^16 every position a
+// kernel computes in int32 stays in range.
+constexpr int64_t kMaxCsrNnz = (int64_t)INT32_MAX - 65536;
+
 // CSR shape checks mirroring verifyCSRStorage
 // (lib/Dialect/SparseWave/IR/SparseWaveOps.cpp:62-109): rows >= 0,
 // nnz within the i32 index range, and non-null arrays where data exists.
-inline int check_csr(const int32_t *ro, const int32_t *col, const float *val,
+inline int check_csr(const int32_t *ro, const int32_t *col, const void *val,
                      int64_t rows, int64_t nnz, bool need_col) {
   if (rows < 0 || nnz < 0)
     return fail(SW_ERR_INVALID_SHAPE,
                 "expected non-negative rows and nnz, but got %lld and %lld",
                 (long long)rows, (long long)nnz);
-  if (rows > INT32_MAX - 1 || nnz > INT32_MAX)
+  if (rows > INT32_MAX - 1 || nnz > kMaxCsrNnz)
     return fail(SW_ERR_INVALID_SHAPE,
-                "i32 CSR indices cannot address %lld rows / %lld nonzeros",
-                (long long)rows, (long long)nnz);
+                "i32 CSR indices cannot address %lld rows / %lld nonzeros "
+                "(at most %lld nonzeros)",
+                (long long)rows, (long long)nnz, (long long)kMaxCsrNnz);
   if (!ro)
     return fail(SW_ERR_INVALID_ARGUMENT, "row offsets pointer is null");
   if (nnz > 0 && ((need_col && !col) || !val))

@@ -28,20 +28,21 @@ constexpr int kOutputDeep = 16;
 // load takes directly; otherwise a 64-bit lane address, whose multiply by k
 // costs more than the load (configuration 3, thread-per-output: K=64
 // 1797 -> 1381 us, K=4 685 -> 653 us with the narrow form).
-template <bool NARROW>
-__device__ __forceinline__ float rhs_at(const float *__restrict__ rhs,
-                                        int32_t c, int64_t k, int64_t j) {
+template <bool NARROW, typename T>
+__device__ __forceinline__ float rhs_at(const T *__restrict__ rhs, int32_t c,
+                                        int64_t k, int64_t j) {
   if constexpr (NARROW)
-    return *at_bytes(rhs, 4u * ((uint32_t)c * (uint32_t)k + (uint32_t)j));
+    return tof(*at_bytes(rhs, (uint32_t)sizeof(T) *
+                                  ((uint32_t)c * (uint32_t)k + (uint32_t)j)));
   else
-    return rhs[(int64_t)c * k + j];
+    return ldv(rhs + (int64_t)c * k + j);
 }
 
-template <bool NARROW>
+template <bool NARROW, typename T>
 __global__ __launch_bounds__(1024) void spmm_thread_per_output(
     const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
-    const float *__restrict__ val, const float *__restrict__ rhs,
-    float *__restrict__ out, int64_t rows, int64_t k) {
+    const T *__restrict__ val, const T *__restrict__ rhs,
+    T *__restrict__ out, int64_t rows, int64_t k) {
   int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= rows * k)
     return;
@@ -54,7 +55,7 @@ __global__ __launch_bounds__(1024) void spmm_thread_per_output(
     int32_t cc[kOutputDeep];
 #pragma unroll
     for (int u = 0; u < kOutputDeep; ++u) {
-      v[u] = val[p + u];
+      v[u] = ldv(val + p + u);
       cc[u] = col[p + u];
     }
 #pragma unroll
@@ -69,7 +70,7 @@ __global__ __launch_bounds__(1024) void spmm_thread_per_output(
     int32_t cc[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      v[u] = val[p + u];
+      v[u] = ldv(val + p + u);
       cc[u] = col[p + u];
     }
 #pragma unroll
@@ -80,8 +81,8 @@ __global__ __launch_bounds__(1024) void spmm_thread_per_output(
       acc = __builtin_fmaf(v[u], b[u], acc);
   }
   for (; p < t; ++p)
-    acc = __builtin_fmaf(val[p], rhs_at<NARROW>(rhs, col[p], k, c), acc);
-  out[e] = acc;
+    acc = __builtin_fmaf(ldv(val + p), rhs_at<NARROW>(rhs, col[p], k, c), acc);
+  stv(out + e, acc);
 }
 
 // wave-per-row-tile, Wave64 lane layout.
@@ -99,11 +100,11 @@ __global__ __launch_bounds__(1024) void spmm_thread_per_output(
 // 1377 us; 8: 494 us and 1456 us on configuration 3)
 constexpr int kTileUnroll = 4;
 
-template <int V, int CL, int G>
+template <int V, int CL, int G, typename T>
 __global__ __launch_bounds__(1024) void spmm_row_tile(
     const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
-    const float *__restrict__ val, const float *__restrict__ rhs,
-    float *__restrict__ out, int64_t rows, int64_t k, int32_t tile,
+    const T *__restrict__ val, const T *__restrict__ rhs,
+    T *__restrict__ out, int64_t rows, int64_t k, int32_t tile,
     int64_t tiles_per_row) {
   constexpr int PL = G / CL;
   const int units_per_block = blockDim.x / G;
@@ -136,13 +137,13 @@ __global__ __launch_bounds__(1024) void spmm_row_tile(
         int64_t c[kTileUnroll];
 #pragma unroll
         for (int u = 0; u < kTileUnroll; ++u) {
-          v[u] = ld_stream(val + p + u * PL);
+          v[u] = tof(ld_stream(val + p + u * PL));
           c[u] = ld_stream(col + p + u * PL);
         }
         v4f b[kTileUnroll];
 #pragma unroll
         for (int u = 0; u < kTileUnroll; ++u)
-          b[u] = *reinterpret_cast<const v4f *>(rhs + c[u] * k + cb);
+          b[u] = ld4(rhs + c[u] * k + cb);
 #pragma unroll
         for (int u = 0; u < kTileUnroll; ++u) {
           acc[0] = __builtin_fmaf(v[u], b[u].x, acc[0]);
@@ -154,9 +155,9 @@ __global__ __launch_bounds__(1024) void spmm_row_tile(
         }
       }
       for (; p < e; p += PL) {
-        const float v = ld_stream(val + p);
+        const float v = tof(ld_stream(val + p));
         const int64_t c = ld_stream(col + p);
-        const v4f b = *reinterpret_cast<const v4f *>(rhs + c * k + cb);
+        const v4f b = ld4(rhs + c * k + cb);
         acc[0] = __builtin_fmaf(v, b.x, acc[0]);
         if constexpr (V == 4) {
           acc[1] = __builtin_fmaf(v, b.y, acc[1]);
@@ -166,13 +167,13 @@ __global__ __launch_bounds__(1024) void spmm_row_tile(
       }
     } else {
       for (int32_t p = s + pl; p < e; p += PL) {
-        const float v = ld_stream(val + p);
+        const float v = tof(ld_stream(val + p));
         const int64_t c = ld_stream(col + p);
-        const float *b = rhs + c * k + cb;
+        const T *b = rhs + c * k + cb;
 #pragma unroll
         for (int i = 0; i < V; ++i)
           if (cb + i < cend)
-            acc[i] = __builtin_fmaf(v, b[i], acc[i]);
+            acc[i] = __builtin_fmaf(v, ldv(b + i), acc[i]);
       }
     }
   }
@@ -184,19 +185,17 @@ __global__ __launch_bounds__(1024) void spmm_row_tile(
       acc[i] += __shfl_xor(acc[i], off, 64);
   }
   if (unit_ok && pl == 0 && cb < cend) {
-    float *o = out + r * k + cb;
+    T *o = out + r * k + cb;
     // non-temporal: the output is not re-read and should not displace RHS
     // rows from L2
     if (V == 4 && cb + 4 <= cend) {
-      __builtin_nontemporal_store(
-          v4f{acc[0], acc[V > 1 ? 1 : 0], acc[V > 2 ? 2 : 0],
-              acc[V > 3 ? 3 : 0]},
-          reinterpret_cast<v4f *>(o));
+      st4_nt(o, v4f{acc[0], acc[V > 1 ? 1 : 0], acc[V > 2 ? 2 : 0],
+                    acc[V > 3 ? 3 : 0]});
     } else {
 #pragma unroll
       for (int i = 0; i < V; ++i)
         if (cb + i < cend)
-          __builtin_nontemporal_store(acc[i], o + i);
+          st1_nt(o + i, acc[i]);
     }
   }
 }
@@ -500,18 +499,20 @@ bool dispatch_wpos_p(int P, int64_t grid, int64_t B, hipStream_t st,
 
 // Row r of C computed by one wave: lanes over the output columns, sequential
 // over the row's positions (the fallback of the tile kernel).
+template <typename T>
 __device__ __forceinline__ void spmm_row_wave(const int32_t *__restrict__ ro,
                                               const int32_t *__restrict__ col,
-                                              const float *__restrict__ val,
-                                              const float *__restrict__ rhs,
-                                              float *__restrict__ out,
-                                              int64_t r, int64_t k) {
+                                              const T *__restrict__ val,
+                                              const T *__restrict__ rhs,
+                                              T *__restrict__ out, int64_t r,
+                                              int64_t k) {
   const int32_t s = ro[r], e = ro[r + 1];
   for (int64_t c = lane_id(); c < k; c += kWave) {
     float acc = 0.0f;
     for (int32_t p = s; p < e; ++p)
-      acc = __builtin_fmaf(val[p], rhs[(int64_t)col[p] * k + c], acc);
-    out[r * k + c] = acc;
+      acc = __builtin_fmaf(ldv(val + p), ldv(rhs + (int64_t)col[p] * k + c),
+                           acc);
+    stv(out + r * k + c, acc);
   }
 }
 
@@ -642,6 +643,110 @@ __global__ __launch_bounds__(64 * W) void spmm_tile_mfma(
 }
 
 
+// SpMM over 16-row tiles, bf16 (k % 64 == 0; rhs and out 8-byte aligned).
+// The fp32 kernel's tiles, waves, structure check and fallbacks, with one
+// v_mfma_f32_16x16x16_bf16 per 16 stored entries and output tile: lane
+// (i, g) supplies val[ro[r0+i] + t0+4g .. t0+4g+3] (zero past the row), and
+// the four output tiles of a 64-column block interleave their columns (tile
+// n's column j is column 4j + n of the block), so one 64-bit load of an rhs
+// row gives a lane its B values for all four tiles.
+template <int W>
+__global__ __launch_bounds__(64 * W) void spmm_tile_mfma_bf16(
+    const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
+    const uint16_t *__restrict__ val, const uint16_t *__restrict__ rhs,
+    uint16_t *__restrict__ out, int32_t rows, int64_t k) {
+  constexpr int CH = 2; // 16-entry chunks per step
+  __shared__ float part[W][4][4][kWave]; // [wave][n tile][v][lane]
+  const int r0 = blockIdx.x * 16;
+  const int nt = std::min(16, rows - r0);
+  const int wave = threadIdx.x / kWave;
+  const int l = lane_id(), i = l & 15, g = l >> 4;
+  const int last = r0 + nt - 1;
+  const int32_t bl = ro[last];
+  const int32_t len_last = ro[last + 1] - bl;
+  const int ic = i < nt ? i : nt - 1;
+  const int32_t ra = ro[r0 + ic];
+  const int32_t la = i < nt ? ro[r0 + ic + 1] - ra : 0;
+  __shared__ int verdict;
+  __shared__ int nonfinite_out;
+  if (threadIdx.x == 0)
+    nonfinite_out = 0;
+  if (!tile_prefix_ok_block(ro, col, r0, nt, &verdict)) {
+    for (int r = r0 + wave; r < r0 + nt; r += W)
+      spmm_row_wave(ro, col, val, rhs, out, r, k);
+    return;
+  }
+  bool nonfinite = false;
+  for (int64_t nb = 0; nb < k; nb += 64) {
+    v4f acc[4];
+#pragma unroll
+    for (int n = 0; n < 4; ++n)
+      acc[n] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int32_t t0 = wave * 16 * CH; t0 < len_last; t0 += W * 16 * CH) {
+      v2u a[CH], bq[CH][4];
+#pragma unroll
+      for (int h = 0; h < CH; ++h) {
+        float av[4];
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+          const int32_t t = t0 + 16 * h + 4 * g + st;
+          const int32_t tc = std::min(t, len_last - 1); // len_last > 0 here
+          const float x = tof(val[t < la ? ra + t : bl + tc]);
+          const int64_t cx = col[bl + tc];
+          av[st] = t < la ? x : 0.0f;
+          // rhs[c][nb + 4i .. nb + 4i + 3] (row 0, zeroed, past len_last)
+          const v2u y = *reinterpret_cast<const v2u *>(
+              rhs + (t < len_last ? cx : 0) * k + nb + 4 * i);
+          bq[h][st] = t < len_last ? y : v2u{0u, 0u};
+        }
+        a[h] = v2u{pack_bf16x2(av[0], av[1]), pack_bf16x2(av[2], av[3])};
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int h = 0; h < CH; ++h)
+#pragma unroll
+        for (int n = 0; n < 4; ++n) {
+          const v2u bn =
+              v2u{bf16_half(bq[h][0], n) | (bf16_half(bq[h][1], n) << 16),
+                  bf16_half(bq[h][2], n) | (bf16_half(bq[h][3], n) << 16)};
+          acc[n] = mfma_16x16x16_bf16(a[h], bn, acc[n]);
+        }
+    }
+#pragma unroll
+    for (int n = 0; n < 4; ++n)
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        part[wave][n][v][l] = acc[n][v];
+    __syncthreads();
+    if (wave < 4) {
+      // wave w finishes rows 4g + w, columns nb + 4i .. nb + 4i + 3
+      float o[4];
+      bool nf = false;
+#pragma unroll
+      for (int n = 0; n < 4; ++n) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int w = 0; w < W; ++w)
+          sum += part[w][n][wave][l];
+        o[n] = sum;
+        nf |= !__builtin_isfinite(sum);
+      }
+      const int rr = 4 * g + wave;
+      if (rr < nt) {
+        *reinterpret_cast<v2u *>(out + (int64_t)(r0 + rr) * k + nb + 4 * i) =
+            v2u{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+        nonfinite |= nf;
+      }
+      if (__builtin_amdgcn_ballot_w64(nonfinite) != 0 && lane_id() == 0)
+        nonfinite_out = 1;
+    }
+    __syncthreads();
+  }
+  if (nonfinite_out != 0) // workgroup-uniform after the barrier above
+    for (int r = r0 + wave; r < r0 + nt; r += W)
+      spmm_row_wave(ro, col, val, rhs, out, r, k);
+}
+
 // Row-owner SpMM for wide rhs (Wave64 extension, k % 4 == 0).
 //
 // The nonzeros are cut into chunks of `chunk` positions; wave w owns the
@@ -654,11 +759,11 @@ __global__ __launch_bounds__(64 * W) void spmm_tile_mfma(
 // groups take positions s+g, s+g+PL, ... U at a time (U = 16 for rows longer
 // than 512 positions, 4 otherwise), and the groups' partial rows meet in an
 // xor butterfly.
-template <int CL>
+template <int CL, typename T>
 __global__ __launch_bounds__(256) void spmm_row_owner(
     const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
-    const float *__restrict__ val, const float *__restrict__ rhs,
-    float *__restrict__ out, int32_t rows, int32_t nnz, int64_t k,
+    const T *__restrict__ val, const T *__restrict__ rhs,
+    T *__restrict__ out, int32_t rows, int32_t nnz, int64_t k,
     int64_t chunk, int64_t chunks, int64_t tiles) {
   constexpr int PL = kWave / CL;
   const int64_t wave =
@@ -691,9 +796,9 @@ __global__ __launch_bounds__(256) void spmm_row_owner(
 #pragma unroll
           for (int u = 0; u < U; ++u) {
             const int32_t q = p + u * PL;
-            v[u] = q < e ? ld_stream(val + q) : 0.0f;
+            v[u] = q < e ? tof(ld_stream(val + q)) : 0.0f;
             const int64_t cc = q < e ? ld_stream(col + q) : 0;
-            b[u] = *reinterpret_cast<const v4f *>(rhs + cc * k + cb);
+            b[u] = ld4(rhs + cc * k + cb);
           }
 #pragma unroll
           for (int u = 0; u < U; ++u)
@@ -707,9 +812,9 @@ __global__ __launch_bounds__(256) void spmm_row_owner(
 #pragma unroll
           for (int u = 0; u < U; ++u) {
             const int32_t q = p + u * PL;
-            v[u] = q < e ? ld_stream(val + q) : 0.0f;
+            v[u] = q < e ? tof(ld_stream(val + q)) : 0.0f;
             const int64_t cc = q < e ? ld_stream(col + q) : 0;
-            b[u] = *reinterpret_cast<const v4f *>(rhs + cc * k + cb);
+            b[u] = ld4(rhs + cc * k + cb);
           }
 #pragma unroll
           for (int u = 0; u < U; ++u)
@@ -725,25 +830,23 @@ __global__ __launch_bounds__(256) void spmm_row_owner(
       acc.w += __shfl_xor(acc.w, off, kWave);
     }
     if (vl == 0 && col_ok)
-      __builtin_nontemporal_store(acc, reinterpret_cast<v4f *>(
-                                           out + (int64_t)r * k + cb));
+      st4_nt(out + (int64_t)r * k + cb, acc);
   }
 }
 
-template <int V, int CL, int G>
+template <int V, int CL, int G, typename T>
 void launch_tile(int64_t grid, int64_t B, hipStream_t st, const int32_t *ro,
-                 const int32_t *col, const float *val, const float *rhs,
-                 float *out, int64_t rows, int64_t k, int32_t tile,
-                 int64_t tpr) {
-  hipLaunchKernelGGL((spmm_row_tile<V, CL, G>), dim3((unsigned)grid),
+                 const int32_t *col, const T *val, const T *rhs, T *out,
+                 int64_t rows, int64_t k, int32_t tile, int64_t tpr) {
+  hipLaunchKernelGGL((spmm_row_tile<V, CL, G, T>), dim3((unsigned)grid),
                      dim3((unsigned)B), 0, st, ro, col, val, rhs, out, rows, k,
                      tile, tpr);
 }
 
-template <int V, int CL>
+template <int V, int CL, typename T>
 void dispatch_g(int G, int64_t rows, int64_t tpr, int64_t B, hipStream_t st,
-                const int32_t *ro, const int32_t *col, const float *val,
-                const float *rhs, float *out, int64_t k, int32_t tile,
+                const int32_t *ro, const int32_t *col, const T *val,
+                const T *rhs, T *out, int64_t k, int32_t tile,
                 int64_t *grid_out) {
   int64_t units = rows * tpr;
   int64_t grid = std::max<int64_t>(sw::ceil_div(units, B / G), 1);
@@ -753,8 +856,9 @@ void dispatch_g(int G, int64_t rows, int64_t tpr, int64_t B, hipStream_t st,
 #define SW_TILE_CASE(GG)                                                      \
   case GG:                                                                    \
     if constexpr (GG >= CL)                                                   \
-      launch_tile<V, CL, (GG >= CL ? GG : CL)>(grid, B, st, ro, col, val,     \
-                                               rhs, out, rows, k, tile, tpr); \
+      launch_tile<V, CL, (GG >= CL ? GG : CL), T>(grid, B, st, ro, col, val,  \
+                                                  rhs, out, rows, k, tile,    \
+                                                  tpr);                       \
     break;
   switch (G) {
     SW_TILE_CASE(1)
@@ -784,25 +888,133 @@ int launch_position_init(const int32_t *ro, float *out, int64_t rows,
                          int64_t k, int64_t chunk, int64_t P, int64_t units,
                          int64_t waves, hipStream_t st);
 
+// The mappings that need no partial sums in the output: thread-per-output,
+// row-tile-mfma, wave-per-row-balanced and wave-per-row-tile, for fp32 and
+// bf16.  Returns 1 (and sets *rc) when it handled the mapping.
+template <typename T>
+bool launch_spmm_rows(const int32_t *ro, const int32_t *col, const T *val,
+                      const T *rhs, T *out, int64_t rows, int64_t rhs_rows,
+                      int64_t nnz, int64_t k, const sw_options &o,
+                      const char *what, hipStream_t st, int *rc) {
+  const int64_t B = o.spmm_block_size;
+  // vector rhs / out access: 16 bytes (fp32) or 8 bytes (bf16) per 4 columns
+  auto vec_ok = [](const void *p) {
+    return (reinterpret_cast<uintptr_t>(p) & (4 * sizeof(T) - 1)) == 0;
+  };
+  if (streq(o.spmm_mapping, "thread-per-output")) {
+    int64_t grid = std::max<int64_t>(ceil_div(rows * k, B), 1);
+    *rc = check_grid(grid, what);
+    if (*rc)
+      return true;
+    dim3 g((unsigned)grid), b((unsigned)B);
+    if (narrow_offsets(rhs_rows, k))
+      hipLaunchKernelGGL((spmm_thread_per_output<true, T>), g, b, 0, st, ro,
+                         col, val, rhs, out, rows, k);
+    else
+      hipLaunchKernelGGL((spmm_thread_per_output<false, T>), g, b, 0, st, ro,
+                         col, val, rhs, out, rows, k);
+    *rc = launch_check("thread-per-output SpMM kernel");
+    return true;
+  }
+  if (streq(o.spmm_mapping, "row-tile-mfma")) {
+    int64_t grid = ceil_div(rows, 16);
+    if constexpr (sizeof(T) == 4) {
+      if (k % 16 == 0) {
+        *rc = check_grid(grid, what);
+        if (*rc)
+          return true;
+        hipLaunchKernelGGL(spmm_tile_mfma<8>, dim3((unsigned)grid), dim3(512),
+                           0, st, ro, col, val, rhs, out, (int32_t)rows, k);
+        *rc = launch_check("SpMM tile MFMA kernel");
+        return true;
+      }
+    } else {
+      if (k % 64 == 0 && vec_ok(rhs) && vec_ok(out)) {
+        *rc = check_grid(grid, what);
+        if (*rc)
+          return true;
+        hipLaunchKernelGGL(spmm_tile_mfma_bf16<8>, dim3((unsigned)grid),
+                           dim3(512), 0, st, ro, col, val, rhs, out,
+                           (int32_t)rows, k);
+        *rc = launch_check("SpMM tile MFMA kernel");
+        return true;
+      }
+    }
+  }
+  if ((streq(o.spmm_mapping, "wave-per-row-balanced") ||
+       (sizeof(T) == 2 && streq(o.spmm_mapping, "row-tile-mfma"))) &&
+      k % 4 == 0 && vec_ok(rhs) && vec_ok(out)) {
+    const int CL = std::min(16, next_pow2((int)std::min<int64_t>(k / 4, 16)));
+    const int64_t chunk = 64 * o.spmm_positions_per_lane;
+    const int64_t chunks = std::max<int64_t>(ceil_div(nnz, chunk), 1);
+    const int64_t tiles = ceil_div(k, (int64_t)CL * 4);
+    // the kernel is compiled for at most 256 threads per workgroup
+    const int64_t OB = std::min<int64_t>(B, 256);
+    const int64_t grid = ceil_div(chunks * tiles, OB / 64);
+    *rc = check_grid(grid, what);
+    if (*rc)
+      return true;
+#define SW_OWNER(CC)                                                          \
+  case CC:                                                                    \
+    hipLaunchKernelGGL((spmm_row_owner<CC, T>), dim3((unsigned)grid),         \
+                       dim3((unsigned)OB), 0, st, ro, col, val, rhs, out,     \
+                       (int32_t)rows, (int32_t)nnz, k, chunk, chunks, tiles); \
+    break;
+    switch (CL) {
+      SW_OWNER(1) SW_OWNER(2) SW_OWNER(4) SW_OWNER(8) SW_OWNER(16)
+    }
+#undef SW_OWNER
+    *rc = launch_check("row-owner SpMM kernel");
+    return true;
+  }
+  const bool row_tile = streq(o.spmm_mapping, "wave-per-row-tile");
+  if (!row_tile && sizeof(T) == 4)
+    return false; // fp32: the position schedule
+  // wave-per-row-tile (bf16 also for the shapes the mappings above decline)
+  const int T_ = (int)o.spmm_tile_size;
+  const int64_t tpr = ceil_div(k, T_);
+  const bool vec = (T_ % 4 == 0) && (k % 4 == 0) && vec_ok(rhs) && vec_ok(out);
+  const int V = vec ? 4 : 1;
+  const int CL = next_pow2(ceil_div(T_, V));
+  const int G = std::max<int>((int)o.spmm_lanes_per_row, CL);
+  int64_t grid = 0;
+  const int32_t tile = (int32_t)T_;
+#define SW_CL_CASE(VV, CC)                                                    \
+  if (V == VV && CL == CC)                                                    \
+    dispatch_g<VV, CC, T>(G, rows, tpr, B, st, ro, col, val, rhs, out, k,     \
+                          tile, &grid);
+  SW_CL_CASE(4, 1)
+  SW_CL_CASE(4, 2)
+  SW_CL_CASE(4, 4)
+  SW_CL_CASE(4, 8)
+  SW_CL_CASE(1, 1)
+  SW_CL_CASE(1, 2)
+  SW_CL_CASE(1, 4)
+  SW_CL_CASE(1, 8)
+  SW_CL_CASE(1, 16)
+  SW_CL_CASE(1, 32)
+#undef SW_CL_CASE
+  if (grid == 0) {
+    *rc = fail(SW_ERR_INVALID_OPTION,
+               "no wave-per-row-tile kernel for tile size %d", T_);
+    return true;
+  }
+  *rc = check_grid(grid, what);
+  if (*rc)
+    return true;
+  *rc = launch_check("wave-per-row-tile SpMM kernel");
+  return true;
+}
+
 int launch_spmm(const int32_t *ro, const int32_t *col, const float *val,
                 const float *rhs, float *out, int64_t rows, int64_t rhs_rows,
                 int64_t nnz, int64_t k, const sw_options &o, const char *what,
                 hipStream_t st) {
   const int64_t B = o.spmm_block_size;
-  if (streq(o.spmm_mapping, "thread-per-output")) {
-    int64_t grid = std::max<int64_t>(ceil_div(rows * k, B), 1);
-    int rc = check_grid(grid, what);
-    if (rc)
-      return rc;
-    dim3 g((unsigned)grid), b((unsigned)B);
-    if (narrow_offsets(rhs_rows, k))
-      hipLaunchKernelGGL(spmm_thread_per_output<true>, g, b, 0, st, ro, col,
-                         val, rhs, out, rows, k);
-    else
-      hipLaunchKernelGGL(spmm_thread_per_output<false>, g, b, 0, st, ro, col,
-                         val, rhs, out, rows, k);
-    return launch_check("thread-per-output SpMM kernel");
-  }
+  int rc = SW_OK;
+  if (launch_spmm_rows<float>(ro, col, val, rhs, out, rows, rhs_rows, nnz, k,
+                              o, what, st, &rc))
+    return rc;
   if (streq(o.spmm_mapping, "thread-per-position")) {
     int64_t n_out = rows * k;
     if (n_out > 0) {
@@ -830,42 +1042,9 @@ int launch_spmm(const int32_t *ro, const int32_t *col, const float *val,
                        (int32_t)rows, k, iters, chunk);
     return launch_check("thread-per-position SpMM kernel");
   }
-  if (streq(o.spmm_mapping, "row-tile-mfma") && k % 16 == 0) {
-    int64_t grid = ceil_div(rows, 16);
-    int rc = check_grid(grid, what);
-    if (rc)
-      return rc;
-    hipLaunchKernelGGL(spmm_tile_mfma<8>, dim3((unsigned)grid), dim3(512), 0,
-                       st, ro, col, val, rhs, out, (int32_t)rows, k);
-    return launch_check("SpMM tile MFMA kernel");
-  }
-  if (streq(o.spmm_mapping, "wave-per-row-balanced") && k % 4 == 0 &&
-      aligned16(rhs) && aligned16(out)) {
-    const int CL = std::min(16, next_pow2((int)std::min<int64_t>(k / 4, 16)));
-    const int64_t chunk = 64 * o.spmm_positions_per_lane;
-    const int64_t chunks = std::max<int64_t>(ceil_div(nnz, chunk), 1);
-    const int64_t tiles = ceil_div(k, (int64_t)CL * 4);
-    const int64_t grid = ceil_div(chunks * tiles, B / 64);
-    int rc = check_grid(grid, what);
-    if (rc)
-      return rc;
-#define SW_OWNER(CC)                                                          \
-  case CC:                                                                    \
-    hipLaunchKernelGGL(spmm_row_owner<CC>, dim3((unsigned)grid),              \
-                       dim3((unsigned)B), 0, st, ro, col, val, rhs, out,      \
-                       (int32_t)rows, (int32_t)nnz, k, chunk, chunks, tiles); \
-    break;
-    switch (CL) {
-      SW_OWNER(1) SW_OWNER(2) SW_OWNER(4) SW_OWNER(8) SW_OWNER(16)
-    }
-#undef SW_OWNER
-    return launch_check("row-owner SpMM kernel");
-  }
-  // row-tile-mfma with k not a multiple of 16 and wave-per-row-balanced
-  // without 128-bit rows take the position schedule
-  if (streq(o.spmm_mapping, "wave-per-position") ||
-      streq(o.spmm_mapping, "row-tile-mfma") ||
-      streq(o.spmm_mapping, "wave-per-row-balanced")) {
+  // wave-per-position, and row-tile-mfma with k not a multiple of 16 and
+  // wave-per-row-balanced without 128-bit rows: the position schedule
+  {
     const bool v4 = (k % 4 == 0) && aligned16(rhs) && aligned16(out);
     const int V = v4 ? 4 : 1;
     const int CL = std::min(16, next_pow2((int)std::min<int64_t>(
@@ -907,48 +1086,35 @@ int launch_spmm(const int32_t *ro, const int32_t *col, const float *val,
       return fail(SW_ERR_INVALID_OPTION, "no wave-per-position SpMM kernel");
     return launch_check("wave-per-position SpMM kernel");
   }
-  // wave-per-row-tile
-  const int T = (int)o.spmm_tile_size;
-  const int64_t tpr = ceil_div(k, T);
-  const bool vec = (T % 4 == 0) && (k % 4 == 0) && aligned16(rhs) &&
-                   aligned16(out);
-  const int V = vec ? 4 : 1;
-  const int CL = next_pow2(ceil_div(T, V));
-  const int G = std::max<int>((int)o.spmm_lanes_per_row, CL);
-  int64_t grid = 0;
-  const int32_t tile = (int32_t)T;
-#define SW_CL_CASE(VV, CC)                                                    \
-  if (V == VV && CL == CC)                                                    \
-    dispatch_g<VV, CC>(G, rows, tpr, B, st, ro, col, val, rhs, out, k, tile,  \
-                       &grid);
-  SW_CL_CASE(4, 1)
-  SW_CL_CASE(4, 2)
-  SW_CL_CASE(4, 4)
-  SW_CL_CASE(4, 8)
-  SW_CL_CASE(1, 1)
-  SW_CL_CASE(1, 2)
-  SW_CL_CASE(1, 4)
-  SW_CL_CASE(1, 8)
-  SW_CL_CASE(1, 16)
-  SW_CL_CASE(1, 32)
-#undef SW_CL_CASE
-  if (grid == 0)
+}
+
+int launch_spmm(const int32_t *ro, const int32_t *col, const uint16_t *val,
+                const uint16_t *rhs, uint16_t *out, int64_t rows,
+                int64_t rhs_rows, int64_t nnz, int64_t k, const sw_options &o,
+                const char *what, hipStream_t st) {
+  int rc = SW_OK;
+  if (streq(o.spmm_mapping, "thread-per-position") ||
+      streq(o.spmm_mapping, "wave-per-position"))
     return fail(SW_ERR_INVALID_OPTION,
-                "no wave-per-row-tile kernel for tile size %d", T);
-  int rc = check_grid(grid, what);
-  if (rc)
-    return rc;
-  return launch_check("wave-per-row-tile SpMM kernel");
+                "spmm-mapping=%s adds partial sums into the output across "
+                "workgroups, which a bf16 output cannot hold; bf16 takes "
+                "thread-per-output, wave-per-row-tile, wave-per-row-balanced "
+                "or row-tile-mfma",
+                o.spmm_mapping);
+  launch_spmm_rows<uint16_t>(ro, col, val, rhs, out, rows, rhs_rows, nnz, k,
+                             o, what, st, &rc);
+  return rc;
 }
 
 } // namespace sw
 
-extern "C" int sw_spmm_csr_f32(const int32_t *row_offsets,
-                               const int32_t *column_indices,
-                               const float *values, const float *rhs,
-                               float *output, int64_t rows, int64_t cols,
-                               int64_t nnz, int64_t k, const sw_options *opts,
-                               void *stream) {
+namespace {
+
+template <typename T>
+int spmm_entry(const int32_t *row_offsets, const int32_t *column_indices,
+               const T *values, const T *rhs, T *output, int64_t rows,
+               int64_t cols, int64_t nnz, int64_t k, const sw_options *opts,
+               void *stream) {
   sw::clear_error();
   sw_options o;
   int rc = sw::resolve_options(opts, &o);
@@ -966,6 +1132,27 @@ extern "C" int sw_spmm_csr_f32(const int32_t *row_offsets,
   if (!output || (nnz > 0 && !rhs))
     return sw::fail(SW_ERR_INVALID_ARGUMENT, "rhs or output pointer is null");
   return sw::launch_spmm(row_offsets, column_indices, values, rhs, output,
-                         rows, cols, nnz, k, o, "SpMM",
-                         sw::as_stream(stream));
+                         rows, cols, nnz, k, o, "SpMM", sw::as_stream(stream));
+}
+
+} // namespace
+
+extern "C" int sw_spmm_csr_f32(const int32_t *row_offsets,
+                               const int32_t *column_indices,
+                               const float *values, const float *rhs,
+                               float *output, int64_t rows, int64_t cols,
+                               int64_t nnz, int64_t k, const sw_options *opts,
+                               void *stream) {
+  return spmm_entry<float>(row_offsets, column_indices, values, rhs, output,
+                           rows, cols, nnz, k, opts, stream);
+}
+
+extern "C" int sw_spmm_csr_bf16(const int32_t *row_offsets,
+                                const int32_t *column_indices,
+                                const uint16_t *values, const uint16_t *rhs,
+                                uint16_t *output, int64_t rows, int64_t cols,
+                                int64_t nnz, int64_t k, const sw_options *opts,
+                                void *stream) {
+  return spmm_entry<uint16_t>(row_offsets, column_indices, values, rhs,
+                              output, rows, cols, nnz, k, opts, stream);
 }

@@ -40,6 +40,9 @@ __device__ __forceinline__ float gather(const float *__restrict__ x,
     return x[c];
 }
 
+// Sum of val[q] * x[col[q]] for q = p, p + stride, ... < e.  Every index
+// computed here is below e + DEEP * stride <= nnz + 2^14, which the host's
+// nnz limit (check_csr) keeps inside int32.
 template <bool NARROW, int DEEP = 0>
 __device__ __forceinline__ float strided_dot(const int32_t *__restrict__ col,
                                              const float *__restrict__ val,

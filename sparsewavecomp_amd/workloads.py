@@ -237,7 +237,8 @@ def algorithmic_bytes_spmm(rows: int, cols: int, nnz: int, k: int) -> int:
 
 
 def algorithmic_bytes_bsr(rows: int, cols: int, nnzb: int, b: int, k: int,
-                          value_bytes: int = 4) -> int:
+                          value_bytes: int = 4, out_bytes: int = 4) -> int:
+    """Block-row offsets, block columns, blocks and RHS once, output once."""
     nbr = rows // b
     return (4 * (nbr + 1) + 4 * nnzb + value_bytes * nnzb * b * b
-            + value_bytes * cols * k + 4 * rows * k)
+            + value_bytes * cols * k + out_bytes * rows * k)

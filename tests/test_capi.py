@@ -141,3 +141,127 @@ def test_entry_points_reject_before_launch():
     # empty problems are no-ops that never launch
     assert lib.sw_spmv_csr_f32(fake, None, None, None, None, 0, 0, 0, None,
                                None) == 0
+
+
+def test_bf16_entry_points_reject_before_launch():
+    """The bf16 entry points validate like the fp32 ones, and the bf16 SpMM
+    refuses the mappings that add partial sums into the output."""
+    lib = sw.load_library()
+    P = ctypes.c_void_p
+    fake = P(16)  # never dereferenced: every call below fails validation
+    for mapping in ("wave-per-position", "thread-per-position"):
+        o = sw.Options(spmm_mapping=mapping, spmm_block_size=64)
+        rc = lib.sw_spmm_csr_bf16(fake, fake, fake, fake, fake, 4, 4, 4, 8,
+                                  o.ref, None)
+        assert rc == -1
+        assert b"bf16 output cannot hold" in lib.sw_last_error()
+    rc = lib.sw_bsr_spmm_bf16(fake, fake, fake, fake, fake, 10, 10, 1, 2, 4,
+                              None, None)
+    assert rc == -2 and b"divisible" in lib.sw_last_error()
+    rc = lib.sw_bsr_spmm_bf16_f32out(fake, fake, fake, fake, fake, 10, 10, 1,
+                                     2, 4, None, None)
+    assert rc == -2 and b"divisible" in lib.sw_last_error()
+    rc = lib.sw_csr_row_reduce_bf16(fake, None, fake, fake, 4, 4, b"min",
+                                    None, None)
+    assert rc == -3 and b"'sum' or 'max'" in lib.sw_last_error()
+    rc = lib.sw_csr_rowwise_map_bf16(fake, None, fake, fake, fake, 4, 4, 9,
+                                     None, None)
+    assert rc == -3
+    rc = lib.sw_sddmm_csr_bf16(fake, fake, fake, fake, fake, fake, 4, 4, 4, 4,
+                               7, 1.0, 0.0, None, None)
+    assert rc == -3
+    rc = lib.sw_sparse_attention_bf16(fake, fake, fake, fake, fake, fake, fake,
+                                      fake, fake, fake, -1, 4, 4, 4, 4, 1.0,
+                                      0.0, None, None)
+    assert rc == -2
+    # empty problems never launch
+    assert lib.sw_sparse_attention_bf16(fake, None, None, None, None, None,
+                                        None, None, None, None, 0, 0, 0, 4, 4,
+                                        1.0, 0.0, None, None) == 0
+
+
+def _cpu(*shape, dtype=None):
+    import torch
+    return torch.zeros(shape, dtype=dtype or torch.float32)
+
+
+def test_mirror_rejects_mismatched_shapes():
+    """The Python mirror checks every operand's size against rows, cols,
+    nnz, k, d and dv before it calls the C ABI (a mismatch would otherwise be
+    an out-of-bounds device access)."""
+    import torch
+    i32, bf = torch.int32, torch.bfloat16
+    ro, col = _cpu(5, dtype=i32), _cpu(8, dtype=i32)
+    cases = [
+        ("output must hold rows", lambda: sw.spmv(ro, col, _cpu(8), _cpu(6),
+                                                  _cpu(5))),
+        ("same length", lambda: sw.spmv(ro, col, _cpu(7), _cpu(6), _cpu(4))),
+        ("output [rows, k]", lambda: sw.spmm(ro, col, _cpu(8), _cpu(6, 3),
+                                             _cpu(4, 2))),
+        ("same length", lambda: sw.spmm(ro, col, _cpu(9), _cpu(6, 3),
+                                        _cpu(4, 3))),
+        ("nnzb * block_size^2", lambda: sw.bsr_spmm(
+            _cpu(3, dtype=i32), _cpu(2, dtype=i32), _cpu(7), _cpu(4, 3),
+            _cpu(4, 3), 2)),
+        ("output [rows, k]", lambda: sw.bsr_spmm(
+            _cpu(3, dtype=i32), _cpu(2, dtype=i32), _cpu(8), _cpu(4, 3),
+            _cpu(5, 3), 2)),
+        ("lhs must have rows", lambda: sw.sddmm(
+            ro, col, _cpu(8), _cpu(3, 2), _cpu(2, 6), _cpu(8))),
+        ("one value per stored entry", lambda: sw.sddmm(
+            ro, col, _cpu(8), _cpu(4, 2), _cpu(2, 6), _cpu(7))),
+        ("output must hold rows", lambda: sw.csr_row_reduce(
+            ro, None, _cpu(8), _cpu(3))),
+        ("row values must hold rows", lambda: sw.csr_rowwise_map(
+            ro, None, _cpu(8), _cpu(3), _cpu(8))),
+        ("same length", lambda: sw.csr_rowwise_map(
+            ro, None, _cpu(8), _cpu(4), _cpu(7))),
+        ("query must have rows", lambda: sw.sparse_attention(
+            ro, col, _cpu(8), _cpu(3, 2), _cpu(2, 6), _cpu(6, 2), _cpu(8),
+            _cpu(4), _cpu(4), _cpu(4, 2), 1.0)),
+        ("head-dim rows", lambda: sw.sparse_attention(
+            ro, col, _cpu(8), _cpu(4, 2), _cpu(3, 6), _cpu(6, 2), _cpu(8),
+            _cpu(4), _cpu(4), _cpu(4, 2), 1.0)),
+        ("one row per key", lambda: sw.sparse_attention(
+            ro, col, _cpu(8), _cpu(4, 2), _cpu(2, 6), _cpu(5, 2), _cpu(8),
+            _cpu(4), _cpu(4), _cpu(4, 2), 1.0)),
+        ("one value per stored entry", lambda: sw.sparse_attention(
+            ro, col, _cpu(8), _cpu(4, 2), _cpu(2, 6), _cpu(6, 2), _cpu(9),
+            _cpu(4), _cpu(4), _cpu(4, 2), 1.0)),
+        ("row maximum and row sum", lambda: sw.sparse_attention(
+            ro, col, _cpu(8), _cpu(4, 2), _cpu(2, 6), _cpu(6, 2), _cpu(8),
+            _cpu(3), _cpu(4), _cpu(4, 2), 1.0)),
+        ("output [rows, dv]", lambda: sw.sparse_attention(
+            ro, col, _cpu(8, dtype=bf), _cpu(4, 2, dtype=bf),
+            _cpu(2, 6, dtype=bf), _cpu(6, 2, dtype=bf), _cpu(8, dtype=bf),
+            _cpu(4, dtype=bf), _cpu(4, dtype=bf), _cpu(4, 3, dtype=bf), 1.0)),
+    ]
+    for needle, call in cases:
+        with pytest.raises(ValueError, match=re.escape(needle)):
+            call()
+    # a shape error is also a SparseWaveError carrying the shape status
+    with pytest.raises(sw.SparseWaveError) as e:
+        cases[0][1]()
+    assert e.value.code == -2
+    with pytest.raises(TypeError, match="float32 or bfloat16"):
+        sw.spmm(ro, col, _cpu(8, dtype=torch.float16), _cpu(6, 3),
+                _cpu(4, 3))
+
+
+def test_csr_nnz_limit():
+    """nnz is capped a little below INT32_MAX so that the row loops' int32
+    position arithmetic (which steps past a row's end by less than 2^16)
+    cannot overflow; the entry points reject larger nnz before any launch."""
+    lib = sw.load_library()
+    fake = ctypes.c_void_p(16)
+    limit = 2**31 - 1 - 65536
+    for nnz in (limit + 1, 2**31 - 1):
+        rc = lib.sw_spmv_csr_f32(fake, fake, fake, fake, fake, 4, 4, nnz,
+                                 None, None)
+        assert rc == -2 and b"at most" in lib.sw_last_error()
+        rc = lib.sw_spmm_csr_f32(fake, fake, fake, fake, fake, 4, 4, nnz, 4,
+                                 None, None)
+        assert rc == -2
+        rc = lib.sw_sddmm_csr_bf16(fake, fake, fake, fake, fake, fake, 4, 4,
+                                   nnz, 4, 0, 1.0, 0.0, None, None)
+        assert rc == -2

@@ -463,3 +463,148 @@ def test_multithreaded_spmv_equals_scalar(orc):
     b = orc.spmv(csr.row_offsets, csr.column_indices, csr.values, x,
                  threads=True)
     np.testing.assert_array_equal(a, b)
+
+
+def test_spmm_abs_bound_matches_scipy(orc):
+    """oracle_spmm_abs_bound is |A| @ |B| computed independently (scipy in
+    float64); a bound that drops a term or takes the wrong rhs column must
+    differ."""
+    for k in (1, 3, 8):
+        csr = W.random_csr(150, 110, 9.0, 31 + k, empty_fraction=0.25)
+        rhs = np.random.default_rng(k).uniform(-2, 2, (110, k)).astype(
+            np.float32)
+        bound = orc.spmm_abs_bound(csr.row_offsets, csr.column_indices,
+                                   csr.values, rhs)
+        want = abs(_scipy(csr)) @ np.abs(rhs.astype(np.float64))
+        np.testing.assert_allclose(bound, want, rtol=1e-12, atol=0)
+        # mutation: the signed sum instead of the sum of magnitudes
+        signed = _scipy(csr) @ rhs.astype(np.float64)
+        assert not np.allclose(np.abs(signed), want, rtol=1e-6)
+        if k > 1:  # columns swapped must not match
+            assert not np.allclose(bound[:, ::-1], want, rtol=1e-6)
+
+
+# ---- bf16 ----------------------------------------------------------------
+
+
+def _torch_bf16_bits(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(
+        torch.bfloat16).view(torch.int16).numpy().astype(np.uint16)
+
+
+def test_round_bf16_matches_torch(orc):
+    """oracle_round_bf16 against torch's float32 -> bfloat16 conversion
+    (round to nearest even) over random bit patterns of every exponent,
+    exact ties, subnormals, overflow and non-finite values."""
+    rng = np.random.default_rng(0)
+    bits = rng.integers(0, 2**32, 200000, dtype=np.uint64).astype(np.uint32)
+    ties = (rng.integers(0, 2**16, 20000, dtype=np.uint64).astype(np.uint32)
+            << 16) | 0x8000
+    special = np.array([0, 0x80000000, 0x00000001, 0x807FFFFF, 0x7F7FFFFF,
+                        0x7F7F8000, 0x7F7F7FFF, 0xFF7FFFFF, 0x7F800000,
+                        0xFF800000, 0x7FC00000, 0x7F800001, 0xFFFFFFFF,
+                        0x3F808000, 0x3F818000], np.uint32)
+    x = np.concatenate([bits, ties, special]).view(np.float32)
+    got = orc.round_bf16(x)
+    want = _torch_bf16_bits(x)
+    nan = np.isnan(x)
+    np.testing.assert_array_equal(got[~nan], want[~nan])
+    assert np.all(np.isnan(orc.bf16_to_f32(got[nan])))
+    # widening is exact: the pattern shifted into the upper half
+    h = rng.integers(0, 2**16, 1000, dtype=np.uint64).astype(np.uint16)
+    w = orc.bf16_to_f32(h)
+    np.testing.assert_array_equal(w.view(np.uint32), h.astype(np.uint32) << 16)
+
+
+def test_round_bf16_hand_cases(orc):
+    one = np.float32(1.0)
+    cases = {1 + 2.0**-8: 1.0,             # tie -> even (fraction 0)
+             1 + 3 * 2.0**-8: 1 + 2.0**-6,  # tie -> even (fraction 2)
+             1 + 2.0**-8 + 2.0**-20: 1 + 2.0**-7,  # above the tie
+             -(1 + 2.0**-7): -(1 + 2.0**-7),       # exact
+             3.4e38: float("inf")}                 # overflow
+    for x, want in cases.items():
+        got = orc.as_bf16(np.array([x], np.float32))[0]
+        assert got == np.float32(want), (x, got, want)
+    assert orc.as_bf16(np.array([one]))[0] == one
+
+
+def _dense_attention_bf16_staged(mask, q, kt, v, alpha):
+    """The six ops on bf16 buffers as dense torch algebra: each op's result
+    rounded with torch's bfloat16 conversion (an implementation independent
+    of the oracle's CSR loops, expf and rounding)."""
+    import torch
+    r = lambda t: t.to(torch.bfloat16).to(torch.float32)
+    rows = np.repeat(np.arange(mask.rows), np.diff(mask.row_offsets))
+    cols = mask.column_indices
+    Q = r(torch.from_numpy(q))
+    KT = r(torch.from_numpy(kt))
+    V = r(torch.from_numpy(v))
+    s = r((Q.double() @ KT.double()).float()[rows, cols] * np.float32(alpha))
+    n = mask.rows
+    dense = torch.full((n, mask.cols), -float("inf"))
+    dense[rows, cols] = s
+    mx = dense.max(dim=1).values
+    e = r(torch.exp(s - mx[rows]))
+    rsum = r(torch.zeros(n).index_add_(0, torch.from_numpy(rows), e))
+    p = r(e / rsum[rows])
+    P = torch.zeros(n, mask.cols, dtype=torch.float64)
+    P[rows, cols] = p.double()
+    out = r((P @ V.double()).float())
+    bound = (P.abs() @ V.double().abs()).numpy()
+    return (s.numpy(), mx.numpy(), rsum.numpy(), p.numpy(), out.numpy(),
+            bound)
+
+
+def test_attention_bf16_matches_dense_staged(orc):
+    mask = W.attention_mask(seq=256, block=16, window=3, random_blocks=2,
+                            seed=5)
+    rng = np.random.default_rng(5)
+    q = rng.standard_normal((256, 16)).astype(np.float32)
+    kt = rng.standard_normal((16, 256)).astype(np.float32)
+    v = rng.standard_normal((256, 16)).astype(np.float32)
+    alpha = 0.25
+    sc, mx, rs, out = orc.sparse_attention_bf16(
+        mask.row_offsets, mask.column_indices, mask.values, q, kt, v, alpha)
+    _, wmx, wrs, wp, wout, bound = _dense_attention_bf16_staged(
+        mask, q, kt, v, alpha)
+    # every stored value is a bf16 value
+    for a in (sc, mx, rs, out):
+        np.testing.assert_array_equal(orc.as_bf16(a), a)
+    # results agree up to one bf16 step where fp32 summation order or exp
+    # differ by an ulp across a rounding boundary
+    ulp = lambda a: np.abs(np.asarray(a, np.float64)) * 2.0**-7 + 1e-30
+    assert np.all(np.abs(mx - wmx) <= ulp(wmx))
+    assert np.all(np.abs(rs - wrs) <= ulp(wrs))
+    assert np.all(np.abs(sc - wp) <= 2 * ulp(wp) + 1e-7)
+    assert np.all(np.abs(out - wout) <= 2 * ulp(wout) + 1e-3 * bound)
+    assert np.mean(sc == wp) > 0.95 and np.mean(out == wout) > 0.95
+    # and within the bf16 tolerance of the fp32 chain
+    _, _, _, out32 = orc.sparse_attention(
+        mask.row_offsets, mask.column_indices, mask.values, q, kt, v, alpha)
+    assert rel_l2(out, out32) <= 1e-2
+    # mutation: the same chain with the row sums left unrounded agrees with
+    # the staged dense computation far less often
+    ro, col = mask.row_offsets, mask.column_indices
+    s1 = orc.as_bf16(orc.sddmm(ro, col, mask.values, orc.as_bf16(q),
+                               orc.as_bf16(kt), orc.SDDMM_AFFINE, alpha, 0.0))
+    m1 = orc.row_reduce(ro, s1, orc.REDUCE_MAX)
+    e1 = orc.as_bf16(orc.rowwise_map(ro, s1, m1, orc.MAP_EXP_SUB))
+    r1 = orc.row_reduce(ro, e1, orc.REDUCE_SUM)
+    p1 = orc.as_bf16(orc.rowwise_map(ro, e1, r1, orc.MAP_DIV))
+    assert np.mean(p1 == wp) < 0.9
+
+
+def test_golden_attention_bf16(orc, golden):
+    """The reference's attention golden vector, within bf16 accuracy."""
+    g = golden["attention"]
+    _, _, _, out = orc.sparse_attention_bf16(
+        np.array(g["row_offsets"], np.int32),
+        np.array(g["column_indices"], np.int32),
+        np.array(g["mask_values"], np.float32),
+        np.array(g["query"], np.float32),
+        np.array(g["transposed_key"], np.float32),
+        np.array(g["value"], np.float32), g["alpha"], g["beta"])
+    want = np.array(g["expected"], np.float64)
+    assert np.all(np.abs(out - want) <= 2.0**-7 * np.abs(want) + 1e-4)
