@@ -8,10 +8,12 @@ expression for ``n`` (output rows, or output elements for the attention
 ``output`` kernel), packs the pointer arguments at the recorded kernarg
 offsets and launches the named symbol.
 
-The manifest schema, the argument and buffer ABI and every verifier check
-mirror the reference tool (tools/sparsewave-bundle/sparsewave_bundle_manifest.py:64-193,
-sparsewave_bundle_verify.py:28-300, sparsewave_bundle_ir.py:4-93); the
-supported target constants are gfx950 / Wave64 instead of gfx1101 / Wave32.
+The manifest schema and the argument and buffer ABI are the contract lrrt
+reads (tools/sparsewave-bundle/sparsewave_bundle_manifest.py:64-193,
+sparsewave_bundle_ir.py:4-93), and the verifier rejects what the
+reference's verifier rejects (sparsewave_bundle_verify.py:28-300,
+test/Driver/bundle_test.py:367-433), with its own diagnostics; the target
+constants are gfx950 / Wave64 instead of gfx1101 / Wave32.
 The kernels are this package's HIP sources specialised with -D shape
 constants and compiled by hipcc; HSACO metadata is read with llvm-readobj.
 """
@@ -97,7 +99,7 @@ def find_tool(name: str) -> str:
                  f"/opt/rocm/bin/{name}"):
         if cand and os.path.exists(cand):
             return cand
-    fail(f"cannot find {name}")
+    fail(f"{name} is not on PATH or under /opt/rocm")
 
 
 def run(cmd, **kw):
@@ -140,7 +142,8 @@ def _metadata_text(readobj_json: str) -> str:
 
     visit(json.loads(readobj_json))
     if len(found) != 1:
-        fail(f"expected one AMDGPU metadata document, found {len(found)}")
+        fail(f"the code object carries {len(found)} AMDGPU metadata notes; "
+             "one is needed")
     return found[0]
 
 
@@ -148,18 +151,18 @@ def parse_metadata(text: str) -> dict:
     """Target and kernel descriptors from AMDGPU code-object metadata."""
     doc = yaml.safe_load(text)
     if not isinstance(doc, dict) or "amdhsa.kernels" not in doc:
-        fail("AMDGPU metadata has no amdhsa.kernels")
+        fail("the AMDGPU metadata lists no amdhsa.kernels")
     target = str(doc.get("amdhsa.target", ""))
     m = re.search(r"(gfx[0-9a-z]+)(?::[^-]+)?$", target)
     if not m:
-        fail(f"cannot determine the AMDGPU chip from target '{target}'")
+        fail(f"no gfx chip name in the metadata target '{target}'")
     kernels = []
     for k in doc["amdhsa.kernels"]:
         for field in (".name", ".symbol", ".kernarg_segment_size",
                       ".group_segment_fixed_size",
                       ".max_flat_workgroup_size", ".wavefront_size"):
             if field not in k:
-                fail(f"kernel metadata is missing {field}")
+                fail(f"a kernel descriptor lacks {field}")
         args = []
         for a in k.get(".args", []) or []:
             args.append({key.lstrip("."): val for key, val in a.items()})
@@ -187,12 +190,14 @@ def inspect_hsaco(hsaco: Path, readobj: str | None = None) -> dict:
 # ---- manifest ----------------------------------------------------------------
 
 
-def grid_expression(block_size: int, wavefront_size: int) -> str:
-    """Total work-items for wave-per-unit mappings."""
+def wave_grid(block_size: int, wavefront_size: int) -> str:
+    """Total work-items when each wave owns one unit of n (the SpMM row
+    tiles): ceil(n / waves per workgroup) workgroups."""
     return f"ceil_div(n, {block_size // wavefront_size}) * {block_size}"
 
 
-def linear_grid_expression(block_size: int) -> str:
+def item_grid(block_size: int) -> str:
+    """Total work-items when each work-item owns one unit of n."""
     return f"ceil_div(n, {block_size}) * {block_size}"
 
 
@@ -200,35 +205,36 @@ def evaluate_grid(expr: str, n: int) -> int:
     """Evaluate the manifest's total-work-item expression for n."""
     m = re.fullmatch(r"ceil_div\(n, (\d+)\) \* (\d+)", expr)
     if not m:
-        fail(f"unsupported grid expression '{expr}'")
+        fail(f"grid '{expr}' is not of the form ceil_div(n, d) * b")
     d, b = int(m.group(1)), int(m.group(2))
     return -(-n // d) * b
 
 
-def merge_arguments(ir_args, metadata_args):
-    if len(ir_args) != len(metadata_args):
-        fail("compiler IR and HSACO kernel argument counts differ: "
-             f"{len(ir_args)} != {len(metadata_args)}")
-    merged = []
-    for ir, md in zip(ir_args, metadata_args):
-        if "offset" not in md or "size" not in md:
-            fail("HSACO kernel argument is missing offset or size")
-        if ir["type"] == "ptr":
-            if md.get("value_kind") != "global_buffer":
-                fail(f"IR pointer argument '{ir['name']}' does not map to an "
-                     "HSACO global_buffer argument")
-            if md.get("size") != 8:
-                fail(f"IR pointer argument '{ir['name']}' must have an "
-                     "8-byte HSACO entry")
+def lay_out_arguments(abi_args, code_object_args):
+    """The manifest's argument list: each ABI argument (name, type, and for
+    attention its tensor) placed at the kernarg offset and size the code
+    object's descriptor gives it."""
+    if len(abi_args) != len(code_object_args):
+        fail(f"the kernel takes {len(code_object_args)} arguments but the "
+             f"ABI names {len(abi_args)}")
+    placed = []
+    for want, have in zip(abi_args, code_object_args):
+        if "offset" not in have or "size" not in have:
+            fail("a code-object argument has no offset or size")
+        kind = have.get("value_kind")
+        if want["type"] == "ptr":
+            if kind != "global_buffer" or have.get("size") != 8:
+                fail(f"argument '{want['name']}' must be an 8-byte "
+                     "global_buffer in the code object")
         else:
-            size = SCALAR_TYPE_SIZES.get(ir["type"])
-            if size is None:
-                fail(f"unsupported scalar ABI type '{ir['type']}'")
-            if md.get("value_kind") != "by_value" or md.get("size") != size:
-                fail(f"IR scalar argument '{ir['name']}' does not match its "
-                     "HSACO by_value entry")
-        merged.append({**ir, "offset": md["offset"], "size": md["size"]})
-    return merged
+            width = SCALAR_TYPE_SIZES.get(want["type"])
+            if width is None:
+                fail(f"scalar ABI type '{want['type']}' is not supported")
+            if kind != "by_value" or have.get("size") != width:
+                fail(f"argument '{want['name']}' must be a {width}-byte "
+                     "by_value entry in the code object")
+        placed.append({**want, "offset": have["offset"], "size": have["size"]})
+    return placed
 
 
 def _sha256(path: Path) -> str:
@@ -238,7 +244,7 @@ def _sha256(path: Path) -> str:
 def _prepare_output(output: Path) -> Path:
     output = Path(output).resolve()
     if output.exists() and (not output.is_dir() or any(output.iterdir())):
-        fail(f"output directory is not empty: {output}")
+        fail(f"refusing to write into {output}: it is not empty")
     output.mkdir(parents=True, exist_ok=True)
     return output
 
@@ -252,8 +258,8 @@ def _check_target(chip, wavefront_size, block_size):
                 "block size": (block_size, SUPPORTED_BLOCK_SIZE)}
     for label, (actual, supported) in expected.items():
         if actual != supported:
-            fail(f"gfx950 lrrt bundle support requires {label} {supported}, "
-                 f"got {actual}")
+            fail(f"this producer builds for {label} {supported} only "
+                 f"(asked for {actual})")
 
 
 def build_spmm_bundle(output, rows: int, rhs_columns: int,
@@ -266,30 +272,31 @@ def build_spmm_bundle(output, rows: int, rhs_columns: int,
     with K == tile size (one tile per output row)."""
     _check_target(chip, wavefront_size, block_size)
     if mapping != SUPPORTED_MAPPING:
-        fail(f"gfx950 lrrt bundle support requires mapping "
-             f"{SUPPORTED_MAPPING}, got {mapping}")
+        fail(f"SpMM bundles use mapping {SUPPORTED_MAPPING} (asked for "
+             f"{mapping})")
     if tile_size not in SUPPORTED_TILE_SIZES:
-        fail(f"gfx950 lrrt bundle support requires a tile size in "
-             f"{SUPPORTED_TILE_SIZES}, got {tile_size}")
+        fail(f"tile size {tile_size} is not one of {SUPPORTED_TILE_SIZES}")
     if rows <= 0:
-        fail("output and RHS row extents must be positive")
+        fail("the output needs a positive number of rows")
     if rhs_columns != tile_size:
-        fail("lrrt bundle support requires RHS/output columns equal tile "
-             f"size {tile_size}")
+        fail(f"one tile per row: the RHS columns must equal tile size "
+             f"{tile_size}, not {rhs_columns}")
     output = _prepare_output(output)
     hsaco = compile_hsaco(_KERNELS / "bundle_spmm.hip", output / CODE_OBJECT,
                           {"SW_ROWS": rows, "SW_K": rhs_columns})
     metadata = inspect_hsaco(hsaco)
     if metadata["target"] != chip:
-        fail(f"requested target {chip} does not match HSACO target "
-             f"{metadata['target']}")
+        fail(f"hipcc built for {metadata['target']}, not {chip}")
     if len(metadata["kernels"]) != 1:
-        fail(f"expected one HSACO kernel, found {len(metadata['kernels'])}")
+        fail(f"the SpMM code object holds {len(metadata['kernels'])} kernels "
+             "instead of one")
     kernel = metadata["kernels"][0]
     if kernel["wavefront_size"] != wavefront_size:
-        fail("HSACO wavefront size does not match the requested Wave64 target")
+        fail(f"the compiled kernel runs Wave{kernel['wavefront_size']}, not "
+             f"Wave{wavefront_size}")
     if kernel["block"] != [block_size, 1, 1]:
-        fail("HSACO workgroup size does not match the requested block")
+        fail(f"the compiled kernel's workgroup {kernel['block']} is not "
+             f"[{block_size}, 1, 1]")
     ir_args = [{"name": n, "type": "ptr"} for n in SPMM_ARGUMENT_NAMES]
     manifest = {
         "manifest_version": MANIFEST_VERSION,
@@ -298,10 +305,10 @@ def build_spmm_bundle(output, rows: int, rhs_columns: int,
             "name": SUPPORTED_OPERATION,
             "symbol": kernel["name"],
             "code_object": CODE_OBJECT,
-            "args": merge_arguments(ir_args, kernel["args"]),
+            "args": lay_out_arguments(ir_args, kernel["args"]),
             "kernarg_size": kernel["kernarg_size"],
             "block": kernel["block"],
-            "grid": [grid_expression(block_size, wavefront_size), 1, 1],
+            "grid": [wave_grid(block_size, wavefront_size), 1, 1],
             "shared_memory_bytes": 0,
             "workspace_bytes": 0,
             "sparsewave": {
@@ -361,7 +368,7 @@ def build_attention_bundle(output, rows: int, key_rows: int, head_dim: int,
                      ("head dimension", head_dim),
                      ("value columns", value_cols)):
         if type(v) is not int or v <= 0:
-            fail(f"SparseAttention {label} must be a positive integer")
+            fail(f"attention bundles need a positive integer {label}")
     if alpha is None:
         alpha = 1.0 / math.sqrt(head_dim)
     output = _prepare_output(output)
@@ -383,18 +390,16 @@ def build_attention_bundle(output, rows: int, key_rows: int, head_dim: int,
              "SW_BETA": f"{float(beta)!r}f"})
         md = inspect_hsaco(hsaco)
         if md["target"] != chip:
-            fail(f"requested target {chip} does not match HSACO target "
-                 f"{md['target']}")
+            fail(f"hipcc built {name} for {md['target']}, not {chip}")
         if len(md["kernels"]) != 1:
-            fail(f"expected one kernel in {hsaco}, found {len(md['kernels'])}")
+            fail(f"{hsaco} holds {len(md['kernels'])} kernels instead of one")
         k = md["kernels"][0]
         if k["name"] != name:
-            fail(f"stable kernel name '{name}' does not match HSACO .name "
-                 f"'{k['name']}'")
+            fail(f"{hsaco} exports '{k['name']}' where '{name}' belongs")
         if k["wavefront_size"] != wavefront_size:
-            fail(f"kernel '{name}' does not use the requested wavefront size")
+            fail(f"{name} was compiled for Wave{k['wavefront_size']}")
         if k["block"] != [block_size, 1, 1]:
-            fail(f"kernel '{name}' does not use the requested block size")
+            fail(f"{name} was compiled for workgroup {k['block']}")
         producer = {
             "application": SPARSE_ATTENTION, "role": spec["role"],
             "operation": spec["operation"], "mapping": spec["mapping"],
@@ -406,10 +411,10 @@ def build_attention_bundle(output, rows: int, key_rows: int, head_dim: int,
             producer["scale"] = {"alpha": float(alpha), "beta": float(beta)}
         entries.append({
             "name": name, "symbol": k["name"], "code_object": rel,
-            "args": merge_arguments([buffers[a] for a in spec["args"]],
-                                    k["args"]),
+            "args": lay_out_arguments([buffers[a] for a in spec["args"]],
+                                      k["args"]),
             "kernarg_size": k["kernarg_size"], "block": k["block"],
-            "grid": [linear_grid_expression(block_size), 1, 1],
+            "grid": [item_grid(block_size), 1, 1],
             "shared_memory_bytes": 0, "workspace_bytes": 0,
             "sparsewave": producer,
         })
@@ -435,58 +440,72 @@ def _validate_arguments(kernel, hsaco_kernel, expected_names):
     margs = kernel.get("args")
     hargs = hsaco_kernel["args"]
     if not isinstance(margs, list) or len(margs) != len(hargs):
-        fail("manifest and HSACO kernel argument counts differ")
+        count = len(margs) if isinstance(margs, list) else "no"
+        fail(f"the manifest lists {count} arguments for a kernel that takes "
+             f"{len(hargs)}")
     if len(expected_names) != len(hargs):
-        fail("manifest argument names do not match the kernel ABI contract")
+        fail(f"the ABI fixes {len(expected_names)} arguments, the kernel "
+             f"takes {len(hargs)}")
     for i, (ma, ha) in enumerate(zip(margs, hargs)):
+        where = f"argument {i} ('{ma.get('name')}')"
         if ma.get("name") != expected_names[i]:
-            fail("manifest argument name does not match the ABI contract")
+            fail(f"{where}: the ABI's argument name here is "
+                 f"'{expected_names[i]}'")
         if ma.get("offset") != ha.get("offset"):
-            fail("manifest argument offset does not match HSACO metadata")
+            fail(f"{where}: kernarg offset {ma.get('offset')} differs from the "
+                 f"code object's {ha.get('offset')}")
         if ma.get("size") != ha.get("size"):
-            fail("manifest argument size does not match HSACO metadata")
+            fail(f"{where}: size {ma.get('size')} differs from the code "
+                 f"object's {ha.get('size')}")
+        kind = ha.get("value_kind")
         if ma.get("type") == "ptr":
-            if ha.get("value_kind") != "global_buffer":
-                fail("manifest ptr argument does not match HSACO "
-                     "global_buffer")
-            if ha.get("size") != 8:
-                fail("manifest ptr argument must occupy 8 bytes")
+            if kind != "global_buffer" or ha.get("size") != 8:
+                fail(f"{where}: a ptr argument needs an 8-byte global_buffer "
+                     "in the code object")
         else:
             t = ma.get("type")
             if t not in SCALAR_TYPE_SIZES:
-                fail(f"unsupported manifest argument type '{t}'")
-            if ha.get("value_kind") != "by_value":
-                fail("manifest scalar argument does not match HSACO by_value")
-            if ha.get("size") != SCALAR_TYPE_SIZES[t]:
-                fail("manifest scalar argument has the wrong bit width")
+                fail(f"{where}: type '{t}' is not a supported scalar")
+            if kind != "by_value" or ha.get("size") != SCALAR_TYPE_SIZES[t]:
+                fail(f"{where}: a {t} scalar needs a "
+                     f"{SCALAR_TYPE_SIZES[t]}-byte by_value entry")
 
 
 def _validate_common(kernel, hsaco_kernel, digest):
+    name = kernel.get("name")
     if kernel.get("symbol") != hsaco_kernel["name"]:
-        fail("manifest kernel symbol does not match HSACO .name")
+        fail(f"kernel '{name}': symbol '{kernel.get('symbol')}' is not the "
+             f"code object's kernel '{hsaco_kernel['name']}'")
     if kernel.get("kernarg_size") != hsaco_kernel["kernarg_size"]:
-        fail("manifest kernarg_size does not match HSACO metadata")
+        fail(f"kernel '{name}': kernarg_size {kernel.get('kernarg_size')} "
+             f"differs from the code object's {hsaco_kernel['kernarg_size']}")
     if kernel.get("block") != hsaco_kernel["block"]:
-        fail("manifest block does not match HSACO metadata")
+        fail(f"kernel '{name}': block {kernel.get('block')} differs from the "
+             f"code object's {hsaco_kernel['block']}")
     if kernel.get("shared_memory_bytes") != 0:
-        fail("fixed HSACO group segment must not be dynamic shared memory")
+        fail(f"kernel '{name}': LDS is fixed in the code object "
+             "(fixed_group_segment_bytes); it may not be requested as "
+             "dynamic shared memory")
     if kernel.get("workspace_bytes") != 0:
-        fail("SparseWave bundles do not support workspace")
+        fail(f"kernel '{name}': these kernels take no workspace")
     producer = kernel.get("sparsewave")
     if not isinstance(producer, dict):
-        fail("kernel is missing sparsewave producer metadata")
+        fail(f"kernel '{name}' has no sparsewave section")
     if producer.get("hsaco_sha256") != digest:
-        fail("invalid sparsewave producer field 'hsaco_sha256'")
+        fail(f"kernel '{name}': hsaco_sha256 is not the digest of its code "
+             "object")
     if producer.get("fixed_group_segment_bytes") != hsaco_kernel[
             "fixed_group_segment_bytes"]:
-        fail("invalid sparsewave producer field 'fixed_group_segment_bytes'")
+        fail(f"kernel '{name}': fixed_group_segment_bytes differs from the "
+             "code object")
 
 
 def _validate_spmm(kernel, hsaco_kernel, digest):
     if kernel.get("name") != SUPPORTED_OPERATION:
-        fail("SparseWave SpMM logical kernel name must be 'spmm'")
+        fail(f"an SpMM bundle's kernel is called 'spmm', not "
+             f"'{kernel.get('name')}'")
     if kernel.get("code_object") != CODE_OBJECT:
-        fail(f"kernel code_object must be '{CODE_OBJECT}'")
+        fail(f"an SpMM bundle keeps its code in '{CODE_OBJECT}'")
     _validate_common(kernel, hsaco_kernel, digest)
     _validate_arguments(kernel, hsaco_kernel, SPMM_ARGUMENT_NAMES)
     producer = kernel["sparsewave"]
@@ -496,39 +515,42 @@ def _validate_spmm(kernel, hsaco_kernel, digest):
                 "launch_n": "output_rows"}
     for field, value in expected.items():
         if producer.get(field) != value:
-            fail(f"invalid sparsewave producer field '{field}'")
+            fail(f"sparsewave.{field} must be {value!r}, not "
+                 f"{producer.get(field)!r}")
     if producer.get("tile_size") not in SUPPORTED_TILE_SIZES:
-        fail("invalid sparsewave producer field 'tile_size'")
+        fail(f"sparsewave.tile_size must be one of {SUPPORTED_TILE_SIZES}")
     rows = producer.get("fixed_output_rows")
     if type(rows) is not int or rows <= 0:
-        fail("invalid sparsewave producer field 'fixed_output_rows'")
-    if kernel.get("grid") != [grid_expression(SUPPORTED_BLOCK_SIZE,
-                                              SUPPORTED_WAVEFRONT_SIZE), 1, 1]:
-        fail("manifest grid is not the supported total-work-item expression")
+        fail("sparsewave.fixed_output_rows must be a positive integer")
+    want = wave_grid(SUPPORTED_BLOCK_SIZE, SUPPORTED_WAVEFRONT_SIZE)
+    if kernel.get("grid") != [want, 1, 1]:
+        fail(f"the SpMM grid is ['{want}', 1, 1], not {kernel.get('grid')}")
 
 
 def _validate_attention(manifest, artifacts):
     producer = manifest.get("sparsewave")
     if not isinstance(producer, dict) or producer.get(
             "application") != SPARSE_ATTENTION:
-        fail("SparseAttention manifest is missing application metadata")
+        fail("an attention manifest names its application in sparsewave")
     if "execution_order" in manifest or "execution_order" in producer:
-        fail("SparseAttention execution order belongs to the runtime Executor")
+        fail("the manifest may not fix an execution order: the runtime "
+             "decides the kernels' order")
     buffers = producer.get("buffers")
     if not isinstance(buffers, list):
-        fail("SparseAttention manifest is missing buffer ABI metadata")
+        fail("an attention manifest lists its buffers in sparsewave.buffers")
     by_name = {b.get("name"): b for b in buffers}
     if len(by_name) != len(buffers):
-        fail("SparseAttention buffer names must be unique")
+        fail("two attention buffers share a name")
     if set(by_name) != set(ATTENTION_BUFFER_NAMES):
-        fail("SparseAttention manifest does not contain the stable buffer ABI")
+        fail("the buffers differ from the stable buffer ABI "
+             f"{sorted(ATTENTION_BUFFER_NAMES)}")
     spec = producer.get("specialization")
     keys = {"output_rows", "key_value_rows", "head_dimension",
             "value_columns"}
     if not isinstance(spec, dict) or set(spec) != keys:
-        fail("SparseAttention specialization metadata is incomplete")
+        fail(f"sparsewave.specialization needs exactly {sorted(keys)}")
     if any(type(v) is not int or v <= 0 for v in spec.values()):
-        fail("SparseAttention specialization values must be positive integers")
+        fail("the specialization's shapes must be positive integers")
     expected_buffers = attention_buffers(spec["output_rows"],
                                          spec["key_value_rows"],
                                          spec["head_dimension"],
@@ -536,30 +558,34 @@ def _validate_attention(manifest, artifacts):
     for name, want in expected_buffers.items():
         got = by_name[name]
         if got.get("type") != "ptr" or got.get("kind") != want["kind"]:
-            fail(f"SparseAttention buffer '{name}' has an invalid ABI role")
+            fail(f"buffer '{name}' must be a ptr with ABI role "
+                 f"'{want['kind']}'")
         if got.get("tensor") != want["tensor"]:
-            fail(f"SparseAttention buffer '{name}' has invalid tensor "
-                 "metadata")
+            fail(f"buffer '{name}' tensor metadata should read "
+                 f"{want['tensor']}")
     kernels = manifest.get("kernels")
     if not isinstance(kernels, list):
-        fail("manifest kernels must be an array")
+        fail("the manifest's kernels field is not a list")
     kernels_by_name = {k.get("name"): k for k in kernels}
     if set(kernels_by_name) != set(ATTENTION_KERNELS):
-        fail("SparseAttention manifest does not contain the stable kernel set")
+        fail("the kernels differ from the six attention kernels "
+             f"{sorted(ATTENTION_KERNELS)}")
     if [k.get("name") for k in kernels] != sorted(ATTENTION_KERNELS):
-        fail("SparseAttention kernels must be emitted deterministically")
+        fail("attention kernels are listed by name, so that bundles are "
+             "written deterministically")
     for name, kspec in ATTENTION_KERNELS.items():
         kernel = kernels_by_name[name]
         if kernel.get("code_object") != f"kernels/{name}.hsaco":
-            fail(f"kernel '{name}' has an unstable artifact path")
+            fail(f"kernel '{name}' must live in kernels/{name}.hsaco, a "
+                 "stable path (not an unstable artifact path)")
         art = artifacts[kernel["code_object"]]
         if len(art["metadata"]["kernels"]) != 1:
-            fail(f"kernel '{name}' artifact must contain one entry point")
+            fail(f"kernels/{name}.hsaco must hold exactly one kernel")
         _validate_common(kernel, art["kernel"], art["digest"])
         _validate_arguments(kernel, art["kernel"], kspec["args"])
-        if kernel.get("grid") != [linear_grid_expression(
-                SUPPORTED_BLOCK_SIZE), 1, 1]:
-            fail(f"kernel '{name}' has an invalid total-work-item grid")
+        want = item_grid(SUPPORTED_BLOCK_SIZE)
+        if kernel.get("grid") != [want, 1, 1]:
+            fail(f"kernel '{name}': grid must be ['{want}', 1, 1]")
         kp = kernel["sparsewave"]
         expected = {"application": SPARSE_ATTENTION, "role": kspec["role"],
                     "operation": kspec["operation"],
@@ -567,63 +593,71 @@ def _validate_attention(manifest, artifacts):
                     "launch_n": kspec["launch_n"], "specialization": spec}
         for field, value in expected.items():
             if kp.get(field) != value:
-                fail(f"kernel '{name}' has invalid producer field '{field}'")
+                fail(f"kernel '{name}': producer field '{field}' must be "
+                     f"{value!r}")
         for arg in kernel["args"]:
             if arg["name"] not in by_name:
-                fail(f"kernel '{name}' refers to an unknown buffer")
+                fail(f"kernel '{name}' takes '{arg['name']}', which is not a "
+                     "manifest buffer")
             semantic = {k: arg[k] for k in ("name", "type", "tensor", "kind")
                         if k in arg}
             if semantic != by_name[arg["name"]]:
-                fail(f"kernel '{name}' buffer ABI metadata is inconsistent")
+                fail(f"kernel '{name}': argument '{arg['name']}' is "
+                     "inconsistent with its buffer entry")
 
 
 def verify_bundle(bundle, inspect=inspect_hsaco) -> dict:
-    """Check a bundle directory the way the reference verifier does
-    (sparsewave_bundle_verify.py:236-300); returns the manifest."""
+    """Check a bundle directory against its code objects -- the checks the
+    reference's verifier makes (sparsewave_bundle_verify.py:236-300);
+    returns the manifest."""
     bundle = Path(bundle)
     manifest = json.loads((bundle / "manifest.json").read_text())
     if type(manifest.get("manifest_version")) is not int or manifest[
             "manifest_version"] != MANIFEST_VERSION:
-        fail(f"unsupported manifest_version: "
-             f"{manifest.get('manifest_version')}")
+        fail(f"manifest_version {manifest.get('manifest_version')!r} is "
+             f"unknown; this verifier reads version {MANIFEST_VERSION}")
     if manifest.get("target") != SUPPORTED_TARGET:
-        fail(f"SparseWave gfx950 bundle target must be {SUPPORTED_TARGET}")
+        fail(f"the manifest target is {manifest.get('target')!r}; these "
+             f"bundles run on {SUPPORTED_TARGET}")
     kernels = manifest.get("kernels")
     if not isinstance(kernels, list) or not kernels:
-        fail("manifest kernels must be a non-empty array")
+        fail("the manifest lists no kernels")
     artifacts, names = {}, set()
     for kernel in kernels:
         if not isinstance(kernel, dict):
-            fail("manifest kernel entries must be objects")
+            fail("each kernel entry must be a JSON object")
         name = kernel.get("name")
         if not isinstance(name, str) or not name:
-            fail("manifest kernel name must be a non-empty string")
+            fail("a kernel entry has no name")
         if name in names:
-            fail(f"duplicate manifest kernel name '{name}'")
+            fail(f"kernel '{name}' appears twice")
         names.add(name)
         rel = kernel.get("code_object")
         if not isinstance(rel, str):
-            fail("kernel code_object must be a relative path")
+            fail(f"kernel '{name}' names no code_object (a relative path)")
         rp = Path(rel)
         if rp.is_absolute() or ".." in rp.parts:
-            fail("kernel code_object must be relative to the bundle directory")
+            fail(f"kernel '{name}': code_object '{rel}' must stay inside the "
+                 "bundle (a relative path without '..')")
         if rel not in artifacts:
             hsaco = bundle / rp
             md = inspect(hsaco)
             if manifest["target"] != md["target"]:
-                fail("manifest target does not match HSACO architecture")
+                fail(f"{rel} was built for {md['target']}, the manifest "
+                     f"target is {manifest['target']}")
             artifacts[rel] = {"metadata": md, "digest": _sha256(hsaco)}
         md = artifacts[rel]["metadata"]
         by_name = {k["name"]: k for k in md["kernels"]}
         symbol = kernel.get("symbol")
         if symbol not in by_name:
-            fail(f"manifest kernel symbol '{symbol}' is missing from HSACO")
+            fail(f"kernel '{name}': symbol '{symbol}' is missing from HSACO "
+                 f"{rel}")
         artifacts[rel]["kernel"] = by_name[symbol]
     if manifest.get("sparsewave", {}).get("application") == SPARSE_ATTENTION:
         _validate_attention(manifest, artifacts)
     else:
         if len(kernels) != 1 or len(artifacts) != 1:
-            fail("SpMM bundle must contain exactly one kernel artifact")
+            fail("an SpMM bundle holds one kernel in one code object")
         k = kernels[0]
         art = artifacts[k["code_object"]]
         _validate_spmm(k, art["kernel"], art["digest"])
@@ -639,28 +673,30 @@ def parse_spmm_signature(text: str) -> dict:
     returns rows and rhs columns."""
     op = re.search(r"^\s*sparsewave\.spmm\b", text, re.MULTILINE)
     if op is None:
-        fail("expected one fixed-shape function containing sparsewave.spmm")
+        fail("the input holds no sparsewave.spmm op")
     funcs = list(re.finditer(r"func\.func\s+@[\w.$-]+\s*\((.*?)\)\s*\{",
                              text[:op.start()], re.DOTALL))
     if not funcs:
-        fail("expected a function containing the SparseWave application")
+        fail("the sparsewave.spmm op is not inside a func.func")
     types = re.findall(r"%[\w.$-]+\s*:\s*(memref<[^>]+>)", funcs[-1].group(1))
     if len(types) != len(SPMM_ARGUMENT_NAMES):
-        fail("fixed-shape SpMM bundle requires exactly five kernel arguments")
+        fail(f"the function takes {len(types)} memrefs; an SpMM bundle "
+             "takes the op's five")
     pats = (r"memref<(\d+)xi32>", r"memref<(\d+|\?)xi32>",
             r"memref<(\d+|\?)xf32>", r"memref<(\d+)x(\d+)xf32>",
             r"memref<(\d+)x(\d+)xf32>")
     ms = [re.fullmatch(p, t) for p, t in zip(pats, types)]
     if not all(ms):
-        fail("bundle input must use fixed-shape CSR i32 and FP32 SpMM memrefs")
+        fail("the memrefs must be i32 offsets and indices, f32 values, and "
+             "f32 rhs / output with static shapes")
     rows, k = int(ms[4].group(1)), int(ms[3].group(2))
     if int(ms[0].group(1)) != rows + 1:
-        fail("rowOffsets extent must equal output rows plus one")
+        fail("rowOffsets must hold the output rows plus one entries")
     if k != int(ms[4].group(2)):
-        fail("RHS and output column extents must match")
+        fail("rhs and output have different column counts")
     if ms[1].group(1) != "?" and ms[2].group(1) != "?" and \
             ms[1].group(1) != ms[2].group(1):
-        fail("columnIndices and values extents must match")
+        fail("columnIndices and values have different lengths")
     if rows <= 0 or int(ms[3].group(1)) <= 0:
-        fail("output and RHS row extents must be positive")
+        fail("rows of the output and of the RHS must be positive")
     return {"rows": rows, "rhs_columns": k}

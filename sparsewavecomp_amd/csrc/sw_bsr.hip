@@ -10,6 +10,9 @@
 //   fp32, k % 4 == 0: a wave owns a 16 x 64 output strip (four tiles with
 //     interleaved columns, 128-bit RHS loads and output stores) and issues
 //     v_mfma_f32_16x16x4_f32 four times per block and tile;
+//   bf16 with a bf16 output, k % 8 == 0: a wave owns a 16 x 128 output strip
+//     (eight tiles with interleaved columns, 128-bit RHS loads) and issues
+//     v_mfma_f32_16x16x16_bf16 once per block and tile;
 //   otherwise a workgroup of four waves owns one block row and 128 output
 //     columns, each wave two 16 x 16 tiles, issuing
 //     fp32: v_mfma_f32_16x16x4_f32 four times per block and tile,
@@ -361,9 +364,12 @@ int check_bsr(const int32_t *bro, const int32_t *bcol, const void *bval,
 }
 
 // bf16 x8 kernel shape: blocks per batch and waves (block rows) per
-// workgroup
-constexpr int kBf16Batch = 4;
-constexpr int kBf16Waves = 4;
+// workgroup.  Configuration 4 (bf16 output): NB = 1 / 2 / 4 / 8 measured
+// 63.2 / 62.1 / 69.9 / 113.6 us with four waves per workgroup (94 VGPRs at
+// NB = 2, four waves per SIMD; 142 at NB = 4, two), and NB = 2 with 1, 2, 4
+// or 8 waves per workgroup 61.5 / 62.0 / 62.1 / 62.3 us.
+constexpr int kBf16Batch = 2;
+constexpr int kBf16Waves = 1;
 
 template <typename T, typename TO>
 int launch_bsr(const int32_t *bro, const int32_t *bcol, const T *bval,
@@ -387,18 +393,22 @@ int launch_bsr(const int32_t *bro, const int32_t *bcol, const T *bval,
       return sw::launch_check("BSR MFMA kernel");
     }
   } else {
-    // bf16 with k % 8 == 0: eight interleaved tiles per wave, 128-bit RHS
-    // loads
-    if (mfma_ok && k % 8 == 0 && sw::aligned16(rhs) && sw::aligned16(out)) {
-      const int64_t gx = sw::ceil_div(nbr, kBf16Waves);
-      const int64_t gy = sw::ceil_div(k, 128);
-      if (gy > 65535)
-        return sw::fail(SW_ERR_INVALID_SHAPE, "rhs has too many columns");
-      hipLaunchKernelGGL((bsr16_mfma_bf16_x8<kBf16Batch, kBf16Waves, TO>),
-                         dim3((unsigned)gx, (unsigned)gy),
-                         dim3(64 * kBf16Waves), 0, st, bro, bcol, bval, rhs,
-                         out, k, nbr);
-      return sw::launch_check("BSR MFMA kernel");
+    // bf16 output with k % 8 == 0: eight interleaved tiles per wave,
+    // 128-bit RHS loads (configuration 4: 61.5 us against 69.8 us for the
+    // two-tile kernel below).  An fp32 output keeps the two-tile kernel,
+    // which measured faster there (73.7 us against 81.6 us).
+    if constexpr (sizeof(TO) == 2) {
+      if (mfma_ok && k % 8 == 0 && sw::aligned16(rhs) && sw::aligned16(out)) {
+        const int64_t gx = sw::ceil_div(nbr, kBf16Waves);
+        const int64_t gy = sw::ceil_div(k, 128);
+        if (gy > 65535)
+          return sw::fail(SW_ERR_INVALID_SHAPE, "rhs has too many columns");
+        hipLaunchKernelGGL((bsr16_mfma_bf16_x8<kBf16Batch, kBf16Waves, TO>),
+                           dim3((unsigned)gx, (unsigned)gy),
+                           dim3(64 * kBf16Waves), 0, st, bro, bcol, bval,
+                           rhs, out, k, nbr);
+        return sw::launch_check("BSR MFMA kernel");
+      }
     }
   }
   if (mfma_ok) {
