@@ -381,11 +381,15 @@ def main():
                             "spmm-positions-per-lane=8 spmm-block-size=256"),
                         (4, "spmm-mapping=wave-per-row-tile spmm-tile-size=4 "
                             "spmm-block-size=64"),
+                        (4, "spmm-mapping=wave-per-row-tile-lds "
+                            "spmm-tile-size=4"),
                         (64, "spmm-mapping=wave-per-position "
                              "spmm-positions-per-lane=16 spmm-block-size=64"),
                         (64, "spmm-mapping=wave-per-row-tile "
                              "spmm-tile-size=32 spmm-lanes-per-row=64 "
-                             "spmm-block-size=64")]:
+                             "spmm-block-size=64"),
+                        (64, "spmm-mapping=wave-per-row-tile-lds "
+                             "spmm-tile-size=32")]:
             rhs = T(W.config3_rhs(m, k, seed=0))
             out = torch.empty((n, k), device=dev)
             o = sw.Options.parse(opts)

@@ -57,9 +57,10 @@ typedef struct sw_options {
   int64_t position_block_size;      /* position-parallel init kernels, default 256 */
   char spmm_mapping[32];            /* thread-per-output | wave-per-row-tile |
                                        thread-per-position | wave-per-position |
-                                       row-tile-mfma | wave-per-row-balanced
-                                       (the last three are Wave64
-                                       extensions) */
+                                       row-tile-mfma | wave-per-row-balanced |
+                                       wave-per-row-tile-lds (the last four
+                                       are Wave64 extensions; -lds stages the
+                                       RHS rows in LDS) */
   int64_t spmm_block_size;          /* 1..1024, default 256 */
   int64_t spmm_tile_size;           /* 1..32, default 4 */
   int64_t spmm_position_chunk_size; /* default 1 */

@@ -222,12 +222,14 @@ int sw_validate_options(const sw_options *o) {
                     o->spmv_mapping);
   if (spmm != "thread-per-output" && spmm != "wave-per-row-tile" &&
       spmm != "thread-per-position" && spmm != "wave-per-position" &&
-      spmm != "row-tile-mfma" && spmm != "wave-per-row-balanced")
+      spmm != "row-tile-mfma" && spmm != "wave-per-row-balanced" &&
+      spmm != "wave-per-row-tile-lds")
     return sw::fail(SW_ERR_INVALID_OPTION,
                     "unsupported SpMM mapping strategy '%s'; expected "
                     "'thread-per-output', 'wave-per-row-tile', "
                     "'thread-per-position', 'wave-per-position', "
-                    "'row-tile-mfma', or 'wave-per-row-balanced'",
+                    "'row-tile-mfma', 'wave-per-row-balanced', or "
+                    "'wave-per-row-tile-lds'",
                     o->spmm_mapping);
   std::string sddmm(o->sddmm_mapping);
   if (sddmm != "thread-per-row" && sddmm != "wave-per-row" &&
@@ -258,7 +260,8 @@ int sw_validate_options(const sw_options *o) {
   const int64_t w = o->wavefront_size;
   bool wave_spmm = spmm == "wave-per-row-tile" ||
                    spmm == "wave-per-position" || spmm == "row-tile-mfma" ||
-                   spmm == "wave-per-row-balanced";
+                   spmm == "wave-per-row-balanced" ||
+                   spmm == "wave-per-row-tile-lds";
   bool wave_spmv = spmv == "wave-per-row" || spmv == "block-per-row" ||
                    spmv == "wave-per-position";
   if ((wave_spmm || wave_spmv) && w != 64)

@@ -747,6 +747,78 @@ __global__ __launch_bounds__(64 * W) void spmm_tile_mfma_bf16(
       spmm_row_wave(ro, col, val, rhs, out, r, k);
 }
 
+// wave-per-row-tile with the RHS rows staged in LDS (Wave64 extension
+// wave-per-row-tile-lds; fp32, k % 4 == 0, tile % 4 == 0, rhs 16-byte
+// aligned): the "dense RHS tiles in LDS" form of the row tile.  A wave owns
+// one (row, tile) unit, its lanes split into PL = 64 / CL position groups of
+// CL column lanes (4 columns each).  Per step every group takes U
+// positions; the 16-byte RHS slices of all of them go from global memory
+// straight into LDS with global_load_lds_dwordx4 (lane l's bytes land in
+// slot l of the step's 1 KB), so no VGPR holds them in flight.  After the
+// wave's loads complete, each lane reads its slots back and accumulates; the
+// groups' partial sums meet in an xor butterfly.  Configuration 3 measured it
+// slower than the register form: the RHS rows are gathered at random and
+// each is used once, so LDS adds a round trip and no reuse.
+constexpr int kLdsTileSteps = 4;
+
+template <int CL>
+__global__ __launch_bounds__(256) void spmm_row_tile_lds(
+    const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
+    const float *__restrict__ val, const float *__restrict__ rhs,
+    float *__restrict__ out, int64_t rows, int64_t k, int32_t tile,
+    int64_t tiles_per_row) {
+  constexpr int PL = kWave / CL, U = kLdsTileSteps;
+  __shared__ v4f stage[4][U][kWave];
+  const int wave = threadIdx.x / kWave, l = lane_id();
+  const int64_t unit = (int64_t)blockIdx.x * 4 + wave;
+  if (unit >= rows * tiles_per_row)
+    return; // wave-uniform; the kernel has no workgroup barrier
+  const int64_t r = unit / tiles_per_row;
+  const int64_t c0 = (unit - r * tiles_per_row) * tile;
+  const int pl = l / CL, cl = l % CL;
+  const int64_t cb = c0 + 4 * cl;
+  const bool col_ok = cb + 4 <= std::min<int64_t>(c0 + tile, k);
+  // lanes past the tile load (and ignore) the tile's first columns
+  const int64_t cload = col_ok ? cb : c0;
+  v4f acc = {0.f, 0.f, 0.f, 0.f};
+  const int32_t s = ro[r], e = ro[r + 1];
+  for (int32_t p0 = s; p0 < e; p0 += PL * U) {
+    float v[U];
+    int64_t cc[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int32_t q = p0 + pl + u * PL;
+      const int32_t qc = q < e ? q : e - 1; // always a position of the row
+      const float x = val[qc];
+      v[u] = q < e ? x : 0.0f;
+      cc[u] = col[qc];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      __builtin_amdgcn_global_load_lds(
+          (const void *)(rhs + cc[u] * k + cload),
+          (void __attribute__((address_space(3))) *)&stage[wave][u][0], 16,
+          0, 0);
+    __builtin_amdgcn_s_waitcnt(0); // the LDS-direct loads have landed
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      acc += v[u] * stage[wave][u][l];
+    __builtin_amdgcn_wave_barrier(); // slots read before the next step
+  }
+#pragma unroll
+  for (int off = CL; off < kWave; off <<= 1) {
+    acc.x += __shfl_xor(acc.x, off, kWave);
+    acc.y += __shfl_xor(acc.y, off, kWave);
+    acc.z += __shfl_xor(acc.z, off, kWave);
+    acc.w += __shfl_xor(acc.w, off, kWave);
+  }
+  if (pl == 0 && col_ok)
+    st4_nt(out + r * k + cb, acc);
+}
+
 // Row-owner SpMM for wide rhs (Wave64 extension, k % 4 == 0).
 //
 // The nonzeros are cut into chunks of `chunk` positions; wave w owns the
@@ -967,7 +1039,31 @@ bool launch_spmm_rows(const int32_t *ro, const int32_t *col, const T *val,
     *rc = launch_check("row-owner SpMM kernel");
     return true;
   }
-  const bool row_tile = streq(o.spmm_mapping, "wave-per-row-tile");
+  if constexpr (sizeof(T) == 4) {
+    const int64_t Tt = o.spmm_tile_size;
+    if (streq(o.spmm_mapping, "wave-per-row-tile-lds") && k % 4 == 0 &&
+        Tt % 4 == 0 && aligned16(rhs) && aligned16(out)) {
+      const int64_t tpr = ceil_div(k, Tt);
+      const int64_t grid = std::max<int64_t>(ceil_div(rows * tpr, 4), 1);
+      *rc = check_grid(grid, what);
+      if (*rc)
+        return true;
+      const int CL = next_pow2((int)(Tt / 4));
+#define SW_LDS_TILE(CC)                                                       \
+  case CC:                                                                    \
+    hipLaunchKernelGGL(spmm_row_tile_lds<CC>, dim3((unsigned)grid),           \
+                       dim3(256), 0, st, ro, col, val, rhs, out, rows, k,     \
+                       (int32_t)Tt, tpr);                                     \
+    break;
+      switch (CL) { SW_LDS_TILE(1) SW_LDS_TILE(2) SW_LDS_TILE(4) SW_LDS_TILE(8) }
+#undef SW_LDS_TILE
+      *rc = launch_check("LDS-staged row-tile SpMM kernel");
+      return true;
+    }
+  }
+  // wave-per-row-tile-lds outside its shapes takes the register row tile
+  const bool row_tile = streq(o.spmm_mapping, "wave-per-row-tile") ||
+                        streq(o.spmm_mapping, "wave-per-row-tile-lds");
   if (!row_tile && sizeof(T) == 4)
     return false; // fp32: the position schedule
   // wave-per-row-tile (bf16 also for the shapes the mappings above decline)

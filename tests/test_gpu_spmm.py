@@ -34,6 +34,10 @@ MAPPINGS = [
     "spmm-mapping=wave-per-position spmm-positions-per-lane=16 "
     "spmm-block-size=128",
     "spmm-mapping=row-tile-mfma",
+    "spmm-mapping=wave-per-row-tile-lds",
+    "spmm-mapping=wave-per-row-tile-lds spmm-tile-size=32",
+    "spmm-mapping=wave-per-row-tile-lds spmm-tile-size=12",
+    "spmm-mapping=wave-per-row-tile-lds spmm-tile-size=3",
     "spmm-mapping=wave-per-row-balanced",
     "spmm-mapping=wave-per-row-balanced spmm-positions-per-lane=1 "
     "spmm-block-size=64",
