@@ -418,3 +418,72 @@ def test_bf16_bsr_config4_sample(dev, orc, out_dtype):
                          16)
     assert rel_l2(got[rows], ref32) <= BF16_REL_L2
     assert np.all(np.isfinite(got))
+
+
+# ---- misaligned operands: the vector fallbacks ---------------------------
+
+
+def _b16_misaligned(a):
+    """A bf16 device view of a that starts 2 bytes past an aligned address,
+    so every 8- and 16-byte alignment check fails."""
+    a = np.asarray(a, np.float32)
+    flat = torch.empty(a.size + 1, dtype=BF, device=G.DEV)
+    view = flat[1:].view(a.shape)
+    view.copy_(b16(a))
+    return view
+
+
+def test_bf16_misaligned_operands(dev, orc):
+    """bf16 SDDMM, SpMM, BSR and the fused attention options with operands
+    that miss the matrix-core paths' alignment: the vector kernels run and
+    keep the same results."""
+    from tests.test_gpu_bsr_attention import _tile_structure_csr
+    csr = _tile_structure_csr()
+    rng = np.random.default_rng(11)
+    d = dv = 64
+    q = rng.standard_normal((csr.rows, d)).astype(np.float32)
+    kt = rng.standard_normal((d, csr.cols)).astype(np.float32)
+    v = rng.standard_normal((csr.cols, dv)).astype(np.float32)
+    G.say("bf16 misaligned sddmm / spmm / attention")
+    out = nan_b16(csr.nnz)
+    sw.sddmm(G.t(csr.row_offsets), G.t(csr.column_indices),
+             b16(csr.values), _b16_misaligned(q), b16(kt), out,
+             sw.SDDMM_AFFINE, 0.125, 0.5,
+             options="sddmm-mapping=row-tile-mfma")
+    torch.cuda.synchronize()
+    _sddmm_check(orc, csr, csr.values, q, kt, sw.SDDMM_AFFINE, 0.125, 0.5,
+                 host(out))
+    o = nan_b16(csr.rows, dv)
+    sw.spmm(G.t(csr.row_offsets), G.t(csr.column_indices), b16(csr.values),
+            _b16_misaligned(v), o, options="spmm-mapping=row-tile-mfma")
+    torch.cuda.synchronize()
+    vb, rb = orc.as_bf16(csr.values), orc.as_bf16(v)
+    ref = orc.spmm(csr.row_offsets, csr.column_indices, vb, rb)
+    bound = orc.spmm_abs_bound(csr.row_offsets, csr.column_indices, vb, rb)
+    assert_bf16_within_bound(host(o), ref, bound)
+    scores, rmax, rsum = nan_b16(csr.nnz), nan_b16(csr.rows), nan_b16(
+        csr.rows)
+    att = nan_b16(csr.rows, dv)
+    sw.sparse_attention(G.t(csr.row_offsets), G.t(csr.column_indices),
+                        b16(csr.values), _b16_misaligned(q), b16(kt),
+                        _b16_misaligned(v), scores, rmax, rsum, att, 0.125,
+                        0.5, options=FUSED)
+    torch.cuda.synchronize()
+    _check_attention_bf16(orc, csr, csr.values, q, kt, v, 0.125, 0.5,
+                          (host(scores), host(rmax), host(rsum), host(att)),
+                          exact_frac=0.9)
+    bsr = W.bsr_banded(seed=5, rows=16 * 64, block_size=16, blocks_per_row=6,
+                       band=3, band_blocks=3, value_std=0.5)
+    rhs = rng.standard_normal((bsr.cols, 128)).astype(np.float32)
+    ob = nan_b16(bsr.rows, 128)
+    G.say("bf16 misaligned bsr")
+    sw.bsr_spmm(G.t(bsr.block_row_offsets), G.t(bsr.block_column_indices),
+                b16(bsr.block_values), _b16_misaligned(rhs), ob, 16,
+                options="bsr-use-mfma=1")
+    torch.cuda.synchronize()
+    vb, rb = orc.as_bf16(bsr.block_values), orc.as_bf16(rhs)
+    ref = orc.bsr_spmm(bsr.block_row_offsets, bsr.block_column_indices, vb,
+                       rb, 16)
+    bound = orc.bsr_abs_bound(bsr.block_row_offsets, bsr.block_column_indices,
+                              vb, rb, 16)
+    assert_bf16_within_bound(host(ob), ref, bound)

@@ -41,6 +41,9 @@ MAPPINGS = [
     "spmm-mapping=wave-per-row-balanced",
     "spmm-mapping=wave-per-row-balanced spmm-positions-per-lane=1 "
     "spmm-block-size=64",
+    # block sizes above the row-owner kernel's 256-thread launch bound
+    "spmm-mapping=wave-per-row-balanced spmm-block-size=512",
+    "spmm-mapping=wave-per-row-balanced spmm-block-size=1024",
 ]
 
 
