@@ -184,26 +184,27 @@ __global__ __launch_bounds__(256) void bsr16_mfma_bf16(
 }
 
 // Column-interleaved bf16 kernel (k % 8 == 0, rhs and output 16-byte
-// aligned).  A wave owns one block row and a 128-column strip as eight
+// aligned).  A workgroup owns one block row and a 128-column strip as eight
 // 16 x 16 tiles whose columns interleave -- tile t's MFMA column j is strip
 // column 8j + t -- so one 128-bit load of an RHS row gives a lane its eight
 // columns' values, one per tile: per block a lane issues one 64-bit A load
 // and four 128-bit B loads (the block's 16 x 128 RHS slab in four wave
 // instructions), then eight v_mfma_f32_16x16x16_bf16.  The B operand of tile
 // t is element t of the four loaded rows (lane group g: rows 4g .. 4g+3).
-// Each lane ends with eight consecutive columns of four output rows: one
-// 128-bit (bf16) or two 128-bit (fp32) stores per row.  Blocks are taken in
-// batches of NB, all loads of a batch before its MFMAs; waves of a
-// workgroup take consecutive block rows, workgroups in XCD-contiguous order.
-template <int NB, int WPB, typename TO>
-__global__ __launch_bounds__(64 * WPB) void bsr16_mfma_bf16_x8(
+// The block row's blocks are split over the SPL waves of the workgroup
+// (wave w takes blocks w NB .. w NB + NB - 1, then every NB SPL-th batch),
+// which shortens each wave's chain of memory trips; the waves' partial
+// tiles are summed in LDS by wave 0.  Each lane ends with eight consecutive
+// columns of four output rows: one 128-bit (bf16) or two 128-bit (fp32)
+// stores per row.  Workgroups run in XCD-contiguous block-row order.
+template <int NB, int SPL, typename TO>
+__global__ __launch_bounds__(64 * SPL) void bsr16_mfma_bf16_x8(
     const int32_t *__restrict__ bro, const int32_t *__restrict__ bcol,
     const uint16_t *__restrict__ bval, const uint16_t *__restrict__ rhs,
     TO *__restrict__ out, int64_t k, int nbr) {
-  const int64_t br = xcd_contiguous(blockIdx.x, gridDim.x) * WPB +
-                     threadIdx.x / kWave;
-  if (br >= nbr)
-    return; // wave-uniform; the kernel has no barrier
+  __shared__ float red[SPL > 1 ? SPL - 1 : 1][8][4][kWave];
+  const int64_t br = xcd_contiguous(blockIdx.x, gridDim.x);
+  const int sp = threadIdx.x / kWave;
   const int l = lane_id();
   const int j = l & 15, g = l >> 4;
   const int64_t cb = (int64_t)blockIdx.y * 128 + 8 * j;
@@ -213,7 +214,7 @@ __global__ __launch_bounds__(64 * WPB) void bsr16_mfma_bf16_x8(
   for (int t = 0; t < 8; ++t)
     acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
   const int32_t s = bro[br], e = bro[br + 1];
-  for (int32_t b0 = s; b0 < e; b0 += NB) {
+  for (int32_t b0 = s + sp * NB; b0 < e; b0 += NB * SPL) {
     const int nb = e - b0 < NB ? e - b0 : NB; // wave-uniform
     const int bcl = l < nb ? bcol[b0 + l] : 0;
     v2u a[NB];
@@ -249,6 +250,24 @@ __global__ __launch_bounds__(64 * WPB) void bsr16_mfma_bf16_x8(
       }
     }
   }
+  if constexpr (SPL > 1) {
+    if (sp > 0)
+#pragma unroll
+      for (int t = 0; t < 8; ++t)
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          red[sp - 1][t][v][l] = acc[t][v];
+    __syncthreads();
+    if (sp > 0)
+      return; // after the only barrier
+#pragma unroll
+    for (int w = 0; w < SPL - 1; ++w)
+#pragma unroll
+      for (int t = 0; t < 8; ++t)
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          acc[t][v] += red[w][t][v][l];
+  }
   if (ok) {
     TO *o = out + (br * 16 + g * 4) * k + cb;
 #pragma unroll
@@ -275,24 +294,33 @@ __global__ __launch_bounds__(64 * WPB) void bsr16_mfma_bf16_x8(
 // tiles, and one 128-bit store writes its four results of an output row.
 // Per block and strip a lane issues one A load and four B loads instead of
 // one A load and sixteen scalar B loads.
-template <int NB>
-__global__ __launch_bounds__(256) void bsr16_mfma_f32_x4(
+//
+// A workgroup covers one block row and up to kF32Strips strips; SPL waves per
+// strip split the block row's blocks (wave sp takes batches sp, sp + SPL, ...)
+// so that more loads are in flight per block row, and the SPL partial tiles
+// are summed through LDS by wave 0 of each strip.
+constexpr int kF32Strips = 2;
+
+template <int NB, int SPL>
+__global__ __launch_bounds__(64 * kF32Strips * SPL) void bsr16_mfma_f32_x4(
     const int32_t *__restrict__ bro, const int32_t *__restrict__ bcol,
     const float *__restrict__ bval, const float *__restrict__ rhs,
     float *__restrict__ out, int64_t k, int nbr) {
+  __shared__ float red[kF32Strips][SPL > 1 ? SPL - 1 : 1][4][4][kWave];
   const int br = xcd_block_row(blockIdx.x, nbr);
-  const int strips = blockDim.x / kWave;
+  const int strips = blockDim.x / (kWave * SPL);
+  const int wv = threadIdx.x / kWave;
+  const int strip = wv % strips, sp = wv / strips;
   const int l = lane_id();
   const int i = l & 15, g = l >> 4;
-  const int64_t cb =
-      ((int64_t)blockIdx.y * strips + threadIdx.x / kWave) * 64 + 4 * i;
+  const int64_t cb = ((int64_t)blockIdx.y * strips + strip) * 64 + 4 * i;
   const bool ok = cb < k; // k % 4 == 0: all four columns or none
   v4f acc[4];
 #pragma unroll
   for (int t = 0; t < 4; ++t)
     acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
   const int32_t s = bro[br], e = bro[br + 1];
-  for (int32_t b0 = s; b0 < e; b0 += NB) {
+  for (int32_t b0 = s + sp * NB; b0 < e; b0 += NB * SPL) {
     const int nb = e - b0 < NB ? e - b0 : NB; // wave-uniform
     const int bcl = l < nb ? bcol[b0 + l] : 0;
     v4f a[NB], bv[NB][4];
@@ -326,6 +354,25 @@ __global__ __launch_bounds__(256) void bsr16_mfma_f32_x4(
       }
     }
   }
+  if constexpr (SPL > 1) {
+    if (sp > 0) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          red[strip][sp - 1][t][v][l] = acc[t][v];
+    }
+    __syncthreads();
+    if (sp > 0)
+      return;
+#pragma unroll
+    for (int w = 0; w < SPL - 1; ++w)
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          acc[t][v] += red[strip][w][t][v][l];
+  }
   if (ok) {
     float *o = out + ((int64_t)br * 16 + g * 4) * k + cb;
 #pragma unroll
@@ -335,6 +382,12 @@ __global__ __launch_bounds__(256) void bsr16_mfma_f32_x4(
                                   reinterpret_cast<v4f *>(o + v * k));
   }
 }
+
+// fp32 x4 kernel shape: blocks per batch and waves per strip. Configuration
+// 4, two strips per workgroup: 1 wave x 4-block batches 134.0 us, 2 x 2
+// 127.5 us, 2 x 1 128.3 us, 2 x 4 144.2 us, 4 x 2 130.3 us, 4 x 1 124.0 us.
+constexpr int kF32Batch = 1;
+constexpr int kF32Split = 4;
 
 int check_bsr(const int32_t *bro, const int32_t *bcol, const void *bval,
               const void *rhs, const void *out, int64_t rows, int64_t cols,
@@ -363,13 +416,13 @@ int check_bsr(const int32_t *bro, const int32_t *bcol, const void *bval,
   return SW_OK;
 }
 
-// bf16 x8 kernel shape: blocks per batch and waves (block rows) per
-// workgroup.  Configuration 4 (bf16 output): NB = 1 / 2 / 4 / 8 measured
-// 63.2 / 62.1 / 69.9 / 113.6 us with four waves per workgroup (94 VGPRs at
-// NB = 2, four waves per SIMD; 142 at NB = 4, two), and NB = 2 with 1, 2, 4
-// or 8 waves per workgroup 61.5 / 62.0 / 62.1 / 62.3 us.
-constexpr int kBf16Batch = 2;
-constexpr int kBf16Waves = 1;
+// bf16 x8 kernel shape: blocks per batch and waves per block row.
+// Configuration 4 (bf16 output), one wave per block row: batches of
+// 1 / 2 / 4 / 8 blocks 63.2 / 62.1 / 69.9 / 113.6 us (94 VGPRs at 2, 142 at
+// 4); the block row split over waves: 2 waves x 2-block batches 60.8 us,
+// 2 x 1 58.3 us, 4 x 1 56.6 us, 4 x 2 62.8 us, 8 x 1 98.2 us.
+constexpr int kBf16Batch = 1;
+constexpr int kBf16Split = 4;
 
 template <typename T, typename TO>
 int launch_bsr(const int32_t *bro, const int32_t *bcol, const T *bval,
@@ -381,31 +434,32 @@ int launch_bsr(const int32_t *bro, const int32_t *bcol, const T *bval,
   const int nbr = (int)(rows / 16);
   if constexpr (sizeof(T) == 4) {
     // fp32 with k % 4 == 0 takes the column-interleaved kernel (measured on
-    // configuration 4: 167 us against 189 us)
+    // configuration 4: 167 us against 189 us for the one-column-per-lane
+    // kernel below, before the block row was split over waves)
     if (mfma_ok && k % 4 == 0 && sw::aligned16(rhs) && sw::aligned16(out)) {
-      const int64_t strips = std::min<int64_t>(4, sw::ceil_div(k, 64));
+      const int64_t strips =
+          std::min<int64_t>(kF32Strips, sw::ceil_div(k, 64));
       const int64_t gy = sw::ceil_div(k, 64 * strips);
       if (gy > 65535)
         return sw::fail(SW_ERR_INVALID_SHAPE, "rhs has too many columns");
-      hipLaunchKernelGGL(bsr16_mfma_f32_x4<4>, dim3((unsigned)nbr, (unsigned)gy),
-                         dim3((unsigned)(64 * strips)), 0, st, bro, bcol, bval,
-                         rhs, out, k, nbr);
+      hipLaunchKernelGGL((bsr16_mfma_f32_x4<kF32Batch, kF32Split>),
+                         dim3((unsigned)nbr, (unsigned)gy),
+                         dim3((unsigned)(64 * strips * kF32Split)), 0, st, bro,
+                         bcol, bval, rhs, out, k, nbr);
       return sw::launch_check("BSR MFMA kernel");
     }
   } else {
-    // bf16 output with k % 8 == 0: eight interleaved tiles per wave,
-    // 128-bit RHS loads (configuration 4: 61.5 us against 69.8 us for the
-    // two-tile kernel below).  An fp32 output keeps the two-tile kernel,
-    // which measured faster there (73.7 us against 81.6 us).
-    if constexpr (sizeof(TO) == 2) {
+    // k % 8 == 0: eight interleaved tiles per workgroup, 128-bit RHS loads
+    // (configuration 4: bf16 output 57.1 us against 69.8 us for the two-tile
+    // kernel below; fp32 output 74.3 against 73.7 us)
+    {
       if (mfma_ok && k % 8 == 0 && sw::aligned16(rhs) && sw::aligned16(out)) {
-        const int64_t gx = sw::ceil_div(nbr, kBf16Waves);
         const int64_t gy = sw::ceil_div(k, 128);
         if (gy > 65535)
           return sw::fail(SW_ERR_INVALID_SHAPE, "rhs has too many columns");
-        hipLaunchKernelGGL((bsr16_mfma_bf16_x8<kBf16Batch, kBf16Waves, TO>),
-                           dim3((unsigned)gx, (unsigned)gy),
-                           dim3(64 * kBf16Waves), 0, st, bro, bcol, bval,
+        hipLaunchKernelGGL((bsr16_mfma_bf16_x8<kBf16Batch, kBf16Split, TO>),
+                           dim3((unsigned)nbr, (unsigned)gy),
+                           dim3(64 * kBf16Split), 0, st, bro, bcol, bval,
                            rhs, out, k, nbr);
         return sw::launch_check("BSR MFMA kernel");
       }

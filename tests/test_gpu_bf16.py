@@ -388,6 +388,28 @@ def test_bf16_bsr(dev, orc, opts, k, out_dtype):
 
 
 @pytest.mark.parametrize("out_dtype", [BF, torch.float32])
+@pytest.mark.parametrize("k", [128, 64, 200, 40])
+def test_bf16_bsr_ragged_block_rows(dev, orc, k, out_dtype):
+    """Block rows of 0 to 9 blocks through the bf16 MFMA kernels, which split
+    a block row's blocks over several waves."""
+    from tests._check import assert_within_bound
+    from tests.test_gpu_bsr_attention import _ragged_bsr
+    bsr = _ragged_bsr(k)
+    rhs = np.random.default_rng(k + 1).standard_normal(
+        (bsr.cols, k)).astype(np.float32)
+    got = _bsr_bf16(bsr, rhs, "bsr-use-mfma=1", out_dtype)
+    vb, rb = orc.as_bf16(bsr.block_values), orc.as_bf16(rhs)
+    ref = orc.bsr_spmm(bsr.block_row_offsets, bsr.block_column_indices, vb,
+                       rb, 16)
+    bound = orc.bsr_abs_bound(bsr.block_row_offsets, bsr.block_column_indices,
+                              vb, rb, 16)
+    if out_dtype == BF:
+        assert_bf16_within_bound(got, ref, bound)
+    else:
+        assert_within_bound(got, ref, bound)
+
+
+@pytest.mark.parametrize("out_dtype", [BF, torch.float32])
 def test_bf16_bsr_config4_sample(dev, orc, out_dtype):
     """Configuration 4 at full size (262,144 rows, 131,072 blocks, k = 128)
     in bf16; 400 block rows (first, last, random) checked against the

@@ -112,6 +112,36 @@ def test_bsr_bf16(dev, orc, opts, k):
     assert_within_bound(out, ref_b, bound)
 
 
+def _ragged_bsr(seed, b=16):
+    """Block rows of 0 to 9 blocks: the MFMA kernels split a block row's
+    blocks over several waves, so rows with fewer blocks than waves, empty
+    rows and rows whose count is not a multiple of the split all occur."""
+    rng = np.random.default_rng(seed)
+    counts = np.array([0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 0, 1, 0, 5] * 4)
+    nbr = counts.size
+    cols = [np.sort(rng.choice(nbr, c, replace=False)) for c in counts]
+    bro = np.zeros(nbr + 1, np.int32)
+    np.cumsum(counts, out=bro[1:])
+    bcol = np.concatenate(cols).astype(np.int32)
+    vals = rng.standard_normal(bcol.size * b * b).astype(np.float32)
+    return W.BSR(rows=nbr * b, cols=nbr * b, block_size=b,
+                 block_row_offsets=bro, block_column_indices=bcol,
+                 block_values=vals)
+
+
+@pytest.mark.parametrize("k", [128, 64, 200, 36])
+def test_bsr_ragged_block_rows(dev, orc, k):
+    bsr = _ragged_bsr(k)
+    rhs = np.random.default_rng(k + 1).standard_normal(
+        (bsr.cols, k)).astype(np.float32)
+    out = _bsr_run(bsr, rhs, "bsr-use-mfma=1")
+    ref = orc.bsr_spmm(bsr.block_row_offsets, bsr.block_column_indices,
+                       bsr.block_values, rhs, 16)
+    bound = orc.bsr_abs_bound(bsr.block_row_offsets, bsr.block_column_indices,
+                              bsr.block_values, rhs, 16)
+    assert_within_bound(out, ref, bound)
+
+
 def test_bsr_config4_sample(dev, orc):
     bsr, rhs = W.config4(seed=0)
     out = _bsr_run(bsr, rhs, "bsr-use-mfma=1")
