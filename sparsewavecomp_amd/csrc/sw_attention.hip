@@ -510,6 +510,31 @@ __device__ __forceinline__ void attention_row_softmax(
   }
 }
 
+// Four consecutive mask values at position e as one vector load.  The
+// target takes unaligned vector loads (a position is only element-aligned);
+// amax = nnz - 4 keeps the 4-element window inside the buffer: a window that
+// would pass the end is read from amax and shifted, so that value v is that
+// of position e + v whenever e + v < nnz (the others are past the last row
+// and never used).
+__device__ __forceinline__ v4f ld_window4(const float *p, uint32_t e,
+                                         uint32_t amax) {
+  const uint32_t a = e < amax ? e : amax;
+  v4f w;
+  __builtin_memcpy(&w, p + a, sizeof w);
+  const uint32_t d = e - a;
+  return v4f{d == 0 ? w.x : d == 1 ? w.y : d == 2 ? w.z : w.w,
+             d == 0 ? w.y : d == 1 ? w.z : w.w, d == 0 ? w.z : w.w, w.w};
+}
+
+__device__ __forceinline__ uint64_t ld_window4(const uint16_t *p, uint32_t e,
+                                               uint32_t amax) {
+  const uint32_t a = e < amax ? e : amax;
+  uint64_t w;
+  __builtin_memcpy(&w, p + a, sizeof w);
+  const uint32_t d = e - a;
+  return d < 4 ? w >> (16 * d) : 0ull;
+}
+
 // The attention chain fused over 16-row tiles (d = 64 * KB, dv % 16 == 0):
 // scores = alpha * Q K^T + beta * mask on the mask's positions, the row
 // softmax (rowMaximum, rowSum and the normalised scores written as the
@@ -537,7 +562,8 @@ constexpr int kFusedWaves = 8;
 constexpr int kFusedChunks = kFusedCols / (16 * kFusedWaves);
 
 // The host guarantees that the byte offsets into mask / scores (positions),
-// K^T (kdim * cols) and V (cols * dv) fit 32 bits.
+// K^T (kdim * cols) and V (cols * dv) fit 32 bits and that nnz >= 4
+// (amax = nnz - 4, the last 4-entry window of the mask).
 template <int KB, int W>
 __global__ __launch_bounds__(64 * W) void attention_tile_fused(
     const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
@@ -545,7 +571,7 @@ __global__ __launch_bounds__(64 * W) void attention_tile_fused(
     const float *__restrict__ kt, const float *__restrict__ value,
     float *scores, float *__restrict__ rmax, float *__restrict__ rsum,
     float *__restrict__ out, int32_t rows, int64_t cols, int32_t kdim,
-    int64_t dv, float alpha, float beta) {
+    int64_t dv, float alpha, float beta, uint32_t amax) {
   static_assert(W == 8 && kFusedCols == 8 * kWave && kFusedChunks == 4,
                 "check layout");
   __shared__ float part[W][4][4][kWave]; // [wave][n tile][v][lane]
@@ -663,17 +689,13 @@ __global__ __launch_bounds__(64 * W) void attention_tile_fused(
     float s0[4] = {0.f, 0.f, 0.f, 0.f}, s1[4] = {0.f, 0.f, 0.f, 0.f};
     v4f acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
     if (one) {
+      // row i's mask values at entries t0 + 4g .. t0 + 4g + 3 (and t1 ...)
+      const v4f x0 = ld_window4(mask, rbase + t0 + 4 * g, amax);
+      const v4f x1 = ld_window4(mask, rbase + t1 + 4 * g, amax);
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        // a chunk exists, so the last row is not empty and its first
-        // position bl is a valid index
-        const bool in0 = valid(2 * it, v), in1 = valid(2 * it + 1, v);
-        const float x0 =
-            *at_bytes(mask, 4u * (in0 ? rbase + t0 + 4 * g + v : bl));
-        const float x1 =
-            *at_bytes(mask, 4u * (in1 ? rbase + t1 + 4 * g + v : bl));
-        s0[v] = in0 ? x0 : 0.0f;
-        s1[v] = in1 ? x1 : 0.0f;
+        s0[v] = valid(2 * it, v) ? x0[v] : 0.0f;
+        s1[v] = valid(2 * it + 1, v) ? x1[v] : 0.0f;
       }
       // K^T[kb 64 + 16g + st][cj]: the wave-uniform row kb 64 + st plus the
       // lane's byte offset (16g rows and cj columns on)
@@ -772,15 +794,23 @@ __global__ __launch_bounds__(64 * W) void attention_tile_fused(
     for (int w = 1; w < W; ++w)
       sum += wred[1][w][i];
 #pragma unroll
-    for (int k = 0; k < kFusedChunks; ++k)
+    for (int k = 0; k < kFusedChunks; ++k) {
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const bool in = valid(k, v);
-        const float p = in ? sv[k][v] / sum : 0.0f;
-        if (in) // the wave-uniform entry t0(k) + v, lane offset rbase + 4g
-          *at_bytes(scores + chunk_t0(k) + v, 4u * (rbase + 4 * g)) = p;
-        sv[k][v] = p; // zero past the row: the P V product adds nothing
+      for (int v = 0; v < 4; ++v) // zero past the row: P V adds nothing
+        sv[k][v] = valid(k, v) ? sv[k][v] / sum : 0.0f;
+      // entries t0(k) + 4g .. + 3 of row i: one (unaligned) vector store
+      // when all four are the row's, else the row's ones one by one
+      float *dst = scores + rbase + chunk_t0(k) + 4 * g;
+      if (valid(k, 3)) {
+        const v4f x = v4f{sv[k][0], sv[k][1], sv[k][2], sv[k][3]};
+        __builtin_memcpy(dst, &x, sizeof x);
+      } else {
+#pragma unroll
+        for (int v = 0; v < 3; ++v)
+          if (valid(k, v))
+            dst[v] = sv[k][v];
       }
+    }
     if (wave == 0 && g == 0 && i < nt) {
       rmax[r0 + i] = m;
       rsum[r0 + i] = sum;
@@ -976,8 +1006,8 @@ __global__ __launch_bounds__(64 * W) void sddmm_tile_mfma_bf16(
 // dv % 64 == 0): the fp32 attention_tile_fused's tiles, waves, chunks,
 // structure check and fallbacks, with the products on bf16 matrix cores.
 // The host guarantees that the byte offsets into mask / scores (2 * nnz),
-// K^T (2 * d * cols) and V (2 * cols * dv) fit 32 bits and that Q is 16-byte
-// and V 8-byte aligned.
+// K^T (2 * d * cols) and V (2 * cols * dv) fit 32 bits, that nnz >= 4
+// (amax = nnz - 4) and that Q is 16-byte and V 8-byte aligned.
 template <int KB, int W>
 __global__ __launch_bounds__(64 * W) void attention_tile_fused_bf16(
     const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
@@ -985,7 +1015,7 @@ __global__ __launch_bounds__(64 * W) void attention_tile_fused_bf16(
     const uint16_t *__restrict__ kt, const uint16_t *__restrict__ value,
     uint16_t *scores, uint16_t *__restrict__ rmax, uint16_t *__restrict__ rsum,
     uint16_t *__restrict__ out, int32_t rows, int64_t cols, int32_t kdim,
-    int64_t dv, float alpha, float beta) {
+    int64_t dv, float alpha, float beta, uint32_t amax) {
   static_assert(W == 8 && kFusedCols == 8 * kWave && kFusedChunks == 4,
                 "check layout");
   constexpr int S = 2 * KB;
@@ -1090,15 +1120,14 @@ __global__ __launch_bounds__(64 * W) void attention_tile_fused_bf16(
     float s0[4] = {0.f, 0.f, 0.f, 0.f}, s1[4] = {0.f, 0.f, 0.f, 0.f};
     v4f acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
     if (one) {
+      const uint64_t x0 = ld_window4(mask, rbase + t0 + 4 * g, amax);
+      const uint64_t x1 = ld_window4(mask, rbase + t1 + 4 * g, amax);
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const bool in0 = valid(2 * it, v), in1 = valid(2 * it + 1, v);
-        const float x0 = tof(
-            *at_bytes(mask, 2u * (in0 ? rbase + t0 + 4 * g + v : bl)));
-        const float x1 = tof(
-            *at_bytes(mask, 2u * (in1 ? rbase + t1 + 4 * g + v : bl)));
-        s0[v] = in0 ? x0 : 0.0f;
-        s1[v] = in1 ? x1 : 0.0f;
+        s0[v] = valid(2 * it, v) ? bf16_to_f32((uint16_t)(x0 >> (16 * v)))
+                                 : 0.0f;
+        s1[v] = valid(2 * it + 1, v) ? bf16_to_f32((uint16_t)(x1 >> (16 * v)))
+                                     : 0.0f;
       }
       const uint32_t ko0 = 2u * cj0 + 8u * g * row_bytes;
       const uint32_t ko1 = 2u * cj1 + 8u * g * row_bytes;
@@ -1182,16 +1211,22 @@ __global__ __launch_bounds__(64 * W) void attention_tile_fused_bf16(
       sum += wred[1][w][i];
     sum = as_stored<uint16_t>(sum);
 #pragma unroll
-    for (int k = 0; k < kFusedChunks; ++k)
+    for (int k = 0; k < kFusedChunks; ++k) {
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const bool in = valid(k, v);
-        const float p = in ? as_stored<uint16_t>(sv[k][v] / sum) : 0.0f;
-        if (in)
-          *at_bytes(scores + chunk_t0(k) + v, 2u * (rbase + 4 * g)) =
-              f32_to_bf16(p);
-        sv[k][v] = p;
+      for (int v = 0; v < 4; ++v)
+        sv[k][v] = valid(k, v) ? as_stored<uint16_t>(sv[k][v] / sum) : 0.0f;
+      uint16_t *dst = scores + rbase + chunk_t0(k) + 4 * g;
+      if (valid(k, 3)) {
+        const v2u x = v2u{pack_bf16x2(sv[k][0], sv[k][1]),
+                          pack_bf16x2(sv[k][2], sv[k][3])};
+        __builtin_memcpy(dst, &x, sizeof x);
+      } else {
+#pragma unroll
+        for (int v = 0; v < 3; ++v)
+          if (valid(k, v))
+            dst[v] = f32_to_bf16(sv[k][v]);
       }
+    }
     if (wave == 0 && g == 0 && i < nt) {
       stv(rmax + r0 + i, m);
       stv(rsum + r0 + i, sum);
@@ -1490,7 +1525,7 @@ bool launch_fused_attention(const int32_t *ro, const int32_t *col,
                             int64_t rows, int64_t cols, int64_t nnz,
                             int64_t d, int64_t dv, float alpha, float beta,
                             hipStream_t st, int *rc) {
-  if (!((d == 64 || d == 128) && dv > 0 && dv % 16 == 0 &&
+  if (!((d == 64 || d == 128) && dv > 0 && dv % 16 == 0 && nnz >= 4 &&
         narrow_offsets(nnz, 1) && narrow_offsets(cols, d) &&
         narrow_offsets(cols, dv)))
     return false;
@@ -1502,7 +1537,8 @@ bool launch_fused_attention(const int32_t *ro, const int32_t *col,
   hipLaunchKernelGGL((attention_tile_fused<KB, kFusedWaves>),                 \
                      dim3((unsigned)grid), dim3(64 * kFusedWaves), 0, st, ro, \
                      col, mask, q, kt, v, scores, rmax, rsum, out,            \
-                     (int32_t)rows, cols, (int32_t)d, dv, alpha, beta)
+                     (int32_t)rows, cols, (int32_t)d, dv, alpha, beta,     \
+                     (uint32_t)(nnz - 4))
   if (d == 64)
     SW_FUSED(1);
   else
@@ -1519,7 +1555,8 @@ bool launch_fused_attention(const int32_t *ro, const int32_t *col,
                             uint16_t *out, int64_t rows, int64_t cols,
                             int64_t nnz, int64_t d, int64_t dv, float alpha,
                             float beta, hipStream_t st, int *rc) {
-  if (!((d == 64 || d == 128) && dv > 0 && dv % 64 == 0 && aligned16(q) &&
+  if (!((d == 64 || d == 128) && dv > 0 && dv % 64 == 0 && nnz >= 4 &&
+        aligned16(q) &&
         (reinterpret_cast<uintptr_t>(v) & 7u) == 0 &&
         (reinterpret_cast<uintptr_t>(out) & 7u) == 0 &&
         narrow_offsets(nnz, 1) && narrow_offsets(cols, d) &&
@@ -1533,7 +1570,8 @@ bool launch_fused_attention(const int32_t *ro, const int32_t *col,
   hipLaunchKernelGGL((attention_tile_fused_bf16<KB, kFusedWaves>),            \
                      dim3((unsigned)grid), dim3(64 * kFusedWaves), 0, st, ro, \
                      col, mask, q, kt, v, scores, rmax, rsum, out,            \
-                     (int32_t)rows, cols, (int32_t)d, dv, alpha, beta)
+                     (int32_t)rows, cols, (int32_t)d, dv, alpha, beta,     \
+                     (uint32_t)(nnz - 4))
   if (d == 64)
     SW_FUSED(1);
   else

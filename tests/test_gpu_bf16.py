@@ -320,6 +320,22 @@ def test_bf16_attention_fused_paths(dev, orc, shape, d, dv):
                           exact_frac=0.9)
 
 
+@pytest.mark.parametrize("nnz", [1, 2, 3, 4, 5, 6])
+def test_bf16_attention_few_entries(dev, orc, nnz):
+    """Matrices of one to six entries under the fused options: the bf16
+    kernel's 4-entry mask windows near the buffer's end (nnz >= 4) and the
+    op chain below that."""
+    from tests.test_gpu_bsr_attention import _few_entries_csr
+    csr = _few_entries_csr(nnz)
+    rng = np.random.default_rng(nnz)
+    q = rng.standard_normal((csr.rows, 64)).astype(np.float32)
+    kt = rng.standard_normal((64, csr.cols)).astype(np.float32)
+    v = rng.standard_normal((csr.cols, 64)).astype(np.float32)
+    got = _attention_bf16(csr, csr.values, q, kt, v, 0.125, 0.5, FUSED)
+    _check_attention_bf16(orc, csr, csr.values, q, kt, v, 0.125, 0.5, got,
+                          exact_frac=0.9)
+
+
 @pytest.mark.parametrize("opts", [FUSED] + ATT_OPTS[:2])
 def test_bf16_attention_non_finite_value_rows(dev, orc, opts):
     """inf / NaN in V rows that a tile's last row includes and its shorter

@@ -445,6 +445,29 @@ def test_attention_fused_paths(dev, orc, shape, d, dv):
     _check_attention(orc, csr, *_attention_case(orc, csr, d, dv, FUSED))
 
 
+def _few_entries_csr(nnz):
+    """Five rows holding nnz entries in all (one to six), rows of one, two
+    and three entries and empty rows: with nnz >= 4 the fused kernel reads
+    every 4-entry mask window from inside the buffer, shifting the windows
+    that would pass its end; below 4 the options fall back to the op chain."""
+    lengths = {1: [0, 1, 0, 0, 0], 2: [1, 0, 1, 0, 0], 3: [0, 2, 0, 1, 0],
+               4: [1, 3, 0, 0, 0], 5: [0, 2, 0, 0, 3], 6: [3, 0, 1, 0, 2]}[nnz]
+    rng = np.random.default_rng(nnz)
+    ro = np.zeros(6, np.int32)
+    np.cumsum(lengths, out=ro[1:])
+    col = np.concatenate([np.sort(rng.choice(8, n, replace=False))
+                          for n in lengths]).astype(np.int32)
+    val = rng.uniform(-1, 1, nnz).astype(np.float32)
+    return W.CSR(5, 8, ro, col, val)
+
+
+@pytest.mark.parametrize("nnz", [1, 2, 3, 4, 5, 6])
+def test_attention_few_entries(dev, orc, nnz):
+    csr = _few_entries_csr(nnz)
+    G.say(f"fused attention few entries nnz={nnz}")
+    _check_attention(orc, csr, *_attention_case(orc, csr, 64, 64, FUSED))
+
+
 @pytest.mark.parametrize("opts", [FUSED] + ATT_OPTS[:2])
 def test_attention_masked_out_entries(dev, orc, opts):
     """Mask values of -inf with beta = 1 (entries masked out) follow IEEE
