@@ -510,31 +510,6 @@ __device__ __forceinline__ void attention_row_softmax(
   }
 }
 
-// Four consecutive mask values at position e as one vector load.  The
-// target takes unaligned vector loads (a position is only element-aligned);
-// amax = nnz - 4 keeps the 4-element window inside the buffer: a window that
-// would pass the end is read from amax and shifted, so that value v is that
-// of position e + v whenever e + v < nnz (the others are past the last row
-// and never used).
-__device__ __forceinline__ v4f ld_window4(const float *p, uint32_t e,
-                                         uint32_t amax) {
-  const uint32_t a = e < amax ? e : amax;
-  v4f w;
-  __builtin_memcpy(&w, p + a, sizeof w);
-  const uint32_t d = e - a;
-  return v4f{d == 0 ? w.x : d == 1 ? w.y : d == 2 ? w.z : w.w,
-             d == 0 ? w.y : d == 1 ? w.z : w.w, d == 0 ? w.z : w.w, w.w};
-}
-
-__device__ __forceinline__ uint64_t ld_window4(const uint16_t *p, uint32_t e,
-                                               uint32_t amax) {
-  const uint32_t a = e < amax ? e : amax;
-  uint64_t w;
-  __builtin_memcpy(&w, p + a, sizeof w);
-  const uint32_t d = e - a;
-  return d < 4 ? w >> (16 * d) : 0ull;
-}
-
 // The attention chain fused over 16-row tiles (d = 64 * KB, dv % 16 == 0):
 // scores = alpha * Q K^T + beta * mask on the mask's positions, the row
 // softmax (rowMaximum, rowSum and the normalised scores written as the
@@ -549,14 +524,24 @@ __device__ __forceinline__ uint64_t ld_window4(const uint16_t *p, uint32_t e,
 //      the P V product takes;
 //   B. the row maxima, then the row sums, are reduced over the four lanes of
 //      a row in each wave and over the waves through LDS (two barriers);
-//      every final score, row maximum and row sum is written once.  The V
-//      rows of each wave's first two chunks are loaded before the first
-//      barrier, so their latency overlaps the softmax;
+//      every final score, row maximum and row sum is written once;
 //   C. output = P V from those registers against the gathered V rows, the
 //      waves' partial output tiles summed through LDS.
 // The scores thus cross HBM once (written) instead of five times, and the
 // chain is one launch.  Other tiles run row by row: each wave computes a row's
 // scores, softmax and output in global memory.
+//
+// The loads are batched so that the chain of dependent memory trips is
+// short: (1) the tile's row offsets (one load, spread to the lanes by
+// permutes) and its Q rows; (2) the rows' column indices for the structure
+// check; (3) the K^T gathers and mask windows of chunks 0-1, then of chunks
+// 2-3; the V rows of chunks 0-1 fly over the softmax.  Entries past the last row read the last row's
+// final column, so no load is guarded; their scores are never used and
+// their P is zero.  A V row that is inf or NaN makes the tile's output
+// non-finite wherever it is read (0 * inf); such tiles are recomputed row by
+// row from the stored scores, adding exactly each row's own entries.
+// Scheduling barriers keep each batch of loads together and in order, so
+// that waiting for one batch leaves the later ones in flight.
 constexpr int kFusedCols = 512;
 constexpr int kFusedWaves = 8;
 constexpr int kFusedChunks = kFusedCols / (16 * kFusedWaves);
@@ -570,8 +555,9 @@ constexpr int kFusedChunks = kFusedCols / (16 * kFusedWaves);
 // output column 4j + n of the block -- so that one 128-bit load of a V row
 // gives a lane its values for all four tiles, and one 128-bit store writes
 // four outputs of a row.
+// (at most 128 VGPRs: the two workgroups of a CU need four waves per SIMD)
 template <int KB, int W, bool IL>
-__global__ __launch_bounds__(64 * W) void attention_tile_fused(
+__global__ __launch_bounds__(64 * W, 4) void attention_tile_fused(
     const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
     const float *__restrict__ mask, const float *__restrict__ q,
     const float *__restrict__ kt, const float *__restrict__ value,
@@ -583,32 +569,51 @@ __global__ __launch_bounds__(64 * W) void attention_tile_fused(
   __shared__ float part[W][4][4][kWave]; // [wave][n tile][v][lane]
   __shared__ float wred[2][W][16];       // [max, sum][wave][row]
   __shared__ int32_t lcol[kFusedCols];   // the last row's columns
-  __shared__ int verdict;
-  __shared__ int v_nonfinite; // a V value of the tile is inf or NaN
+  __shared__ int wshared[W]; // each wave's rows share the last row's columns
+  __shared__ int v_nonfinite; // an output of the tile is inf or NaN
   const int r0 = blockIdx.x * 16;
   const int nt = std::min(16, rows - r0);
   const int wave = threadIdx.x / kWave;
   const int l = lane_id(), i = l & 15, g = l >> 4;
-  // loads are unconditional from clamped, valid addresses, their values
-  // selected afterwards (a guarded load becomes a branch that waits for it
-  // on the spot)
-  const int ic = i < nt ? i : nt - 1;
-  // row i of the tile: its first position and its length (0 past nt)
-  const int32_t rbase = ro[r0 + ic];
-  const int32_t la = i < nt ? ro[r0 + ic + 1] - rbase : 0;
+  // 1. lanes 0..nt hold ro[r0 .. r0 + nt]; Q row r0 + i, elements
+  //    kb 64 + 16 g + st (the B operand of step st)
+  const int32_t my_ro = ro[r0 + (l < nt ? l : nt)];
   float qa[16 * KB];
   const int64_t qrow = (int64_t)std::min(r0 + i, rows - 1) * kdim;
 #pragma unroll
   for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-    for (int st = 0; st < 16; ++st) {
-      const float x = q[qrow + kb * 64 + 16 * g + st];
-      qa[kb * 16 + st] = i < nt ? x : 0.0f;
+    for (int u = 0; u < 4; ++u) {
+      v4f x;
+      __builtin_memcpy(&x, q + qrow + kb * 64 + 16 * g + 4 * u, sizeof x);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        qa[kb * 16 + 4 * u + e] = i < nt ? x[e] : 0.0f;
     }
-  // lanes 0..nt of every wave hold ro[r0 .. r0+nt]
-  const int32_t my_ro = ro[r0 + (l < nt ? l : nt)];
+  __builtin_amdgcn_sched_barrier(0);
+  // row i's first position and length (0 past nt); the permutes run on
+  // every lane, as a permute reads zero from a lane that is switched off
+  const int ic = i < nt ? i : nt - 1;
+  const int32_t rbase = __builtin_amdgcn_ds_bpermute(ic << 2, my_ro);
+  const int32_t rnext = __builtin_amdgcn_ds_bpermute((ic + 1) << 2, my_ro);
+  const int32_t la = i < nt ? rnext - rbase : 0;
   const int32_t bl = __builtin_amdgcn_readlane(my_ro, nt - 1);
   const int32_t len_last = __builtin_amdgcn_readlane(my_ro, nt) - bl;
+  // first entry of this wave's chunk k (entries past len_last: no chunk)
+  auto chunk_t0 = [&](int k) __attribute__((always_inline)) {
+    return 16 * (wave + W * k);
+  };
+  // entry (k, v) of lane (i, g): row i, entry chunk_t0(k) + 4g + v
+  auto valid = [&](int k, int v) __attribute__((always_inline)) {
+    return chunk_t0(k) + 4 * g + v < la;
+  };
+  // row i's mask values at entries t0(k) + 4g .. + 3: the raw window, read
+  // from position min(e, amax) for the window's first position e and
+  // shifted by e - min(e, amax) where the values are used
+  auto window_at = [&](int k) __attribute__((always_inline)) {
+    const uint32_t e = rbase + chunk_t0(k) + 4 * g;
+    return e < amax ? e : amax;
+  };
   // The structure check and the LDS copy of the last row's column indices
   // share one batch of loads: wave w compares rows w and w + W (at most two,
   // nt <= 16 = 2W) against the last row, a row of at most kFusedCols entries
@@ -616,10 +621,8 @@ __global__ __launch_bounds__(64 * W) void attention_tile_fused(
   // row to LDS, where both products read their K / V row indices.
   bool ok = len_last <= kFusedCols; // workgroup-uniform
   if (ok) {
-    if (threadIdx.x == 0) {
-      verdict = 1;
+    if (threadIdx.x == 0)
       v_nonfinite = 0;
-    }
     int32_t x[2][8], yl[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
@@ -639,30 +642,33 @@ __global__ __launch_bounds__(64 * W) void attention_tile_fused(
         x[h][u] = col[len > 0 ? b + std::min(t, len - 1) : 0];
       }
     }
+    // without branches: a compare inside a branch would pull its loads
+    // into the branch
     bool mine = true;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int rr = wave + h * W;
-      if (rr < nt - 1) { // wave-uniform
-        const int32_t b = __builtin_amdgcn_readlane(my_ro, rr);
-        const int32_t len = __builtin_amdgcn_readlane(my_ro, rr + 1) - b;
-        mine &= len <= len_last;
+      const int rc = rr < nt - 1 ? rr : 0;
+      const int32_t b = __builtin_amdgcn_readlane(my_ro, rc);
+      const int32_t len = __builtin_amdgcn_readlane(my_ro, rc + 1) - b;
+      bool same = len <= len_last;
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
-          if (l + u * kWave < len)
-            mine &= x[h][u] == yl[u];
-      }
+      for (int u = 0; u < 8; ++u)
+        same &= (l + u * kWave >= len) | (x[h][u] == yl[u]);
+      mine &= (rr >= nt - 1) | same;
     }
     // wave w stores the last row's entries 64w .. 64w + 63
 #pragma unroll
     for (int u = 0; u < 8; ++u)
       if (u == wave && l + u * kWave < len_last)
         lcol[l + u * kWave] = yl[u];
-    __syncthreads(); // verdict initialised before any wave clears it
-    if (__builtin_amdgcn_ballot_w64(!mine) != 0 && l == 0)
-      verdict = 0;
+    const bool shared_cols = __builtin_amdgcn_ballot_w64(!mine) == 0;
+    if (l == 0)
+      wshared[wave] = shared_cols;
     __syncthreads();
-    ok = verdict != 0;
+#pragma unroll
+    for (int w = 0; w < W; ++w)
+      ok &= wshared[w] != 0;
   }
   if (!ok) { // workgroup-uniform
     for (int r = r0 + wave; r < r0 + nt; r += W) {
@@ -675,104 +681,107 @@ __global__ __launch_bounds__(64 * W) void attention_tile_fused(
     }
     return;
   }
-  // first entry of this wave's chunk k (entries past len_last: no chunk)
-  auto chunk_t0 = [&](int k) __attribute__((always_inline)) {
-    return 16 * (wave + W * k);
+  // 3. the gathers; entries past the last row read its final column
+  const int32_t last = std::max(len_last - 1, 0);
+  // K_chunk rows (A operand of step kb 16 + st): K^T[kb 64 + 16 g + st][c]
+  // for the column c of entry t0 + i -- the wave-uniform row kb 64 + st
+  // plus the lane's byte offset (16 g rows and c columns on)
+  auto gather_k = [&](int k, float (&a)[16 * KB])
+      __attribute__((always_inline)) {
+    const uint32_t cj = lcol[std::min(chunk_t0(k) + i, last)];
+    const uint32_t ko = 4u * (16u * g * (uint32_t)cols + cj);
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+      for (int st = 0; st < 16; ++st)
+        a[kb * 16 + st] = *at_bytes(kt + (int64_t)(kb * 64 + st) * cols, ko);
   };
-  // entry (k, v) of lane (i, g): row i, entry chunk_t0(k) + 4g + v
-  auto valid = [&](int k, int v) __attribute__((always_inline)) {
-    return chunk_t0(k) + 4 * g + v < la;
-  };
-  // A. S^T per chunk, two chunks per step: sv[k][v] = score (i, t0(k)+4g+v)
-  float sv[kFusedChunks][4];
-#pragma unroll
-  for (int it = 0; it < kFusedChunks / 2; ++it) {
-    const int32_t t0 = chunk_t0(2 * it), t1 = chunk_t0(2 * it + 1);
-    const bool one = t0 < len_last, two = t1 < len_last; // wave-uniform
-    const int32_t last = std::max(len_last - 1, 0);
-    const uint32_t cj0 = lcol[std::min(t0 + i, last)];
-    const uint32_t cj1 = lcol[std::min(two ? t1 + i : t0 + i, last)];
-    float s0[4] = {0.f, 0.f, 0.f, 0.f}, s1[4] = {0.f, 0.f, 0.f, 0.f};
-    v4f acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-    if (one) {
-      // row i's mask values at entries t0 + 4g .. t0 + 4g + 3 (and t1 ...)
-      const v4f x0 = ld_window4(mask, rbase + t0 + 4 * g, amax);
-      const v4f x1 = ld_window4(mask, rbase + t1 + 4 * g, amax);
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        s0[v] = valid(2 * it, v) ? x0[v] : 0.0f;
-        s1[v] = valid(2 * it + 1, v) ? x1[v] : 0.0f;
-      }
-      // K^T[kb 64 + 16g + st][cj]: the wave-uniform row kb 64 + st plus the
-      // lane's byte offset (16g rows and cj columns on)
-      const uint32_t ko0 = 4u * (16u * g * (uint32_t)cols + cj0);
-      const uint32_t ko1 = 4u * (16u * g * (uint32_t)cols + cj1);
-#pragma unroll
-      for (int kb = 0; kb < KB; ++kb) {
-        float bv0[16], bv1[16];
-#pragma unroll
-        for (int st = 0; st < 16; ++st) {
-          const float *krow = kt + (int64_t)(kb * 64 + st) * cols;
-          bv0[st] = *at_bytes(krow, ko0);
-          bv1[st] = *at_bytes(krow, ko1);
-        }
-#pragma unroll
-        for (int st = 0; st < 16; ++st) {
-          acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(
-              bv0[st], qa[kb * 16 + st], acc0, 0, 0, 0);
-          if (two)
-            acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(
-                bv1[st], qa[kb * 16 + st], acc1, 0, 0, 0);
-        }
-      }
-    }
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      sv[2 * it][v] =
-          combine_sddmm(SW_SDDMM_AFFINE, s0[v], acc0[v], alpha, beta);
-      sv[2 * it + 1][v] =
-          combine_sddmm(SW_SDDMM_AFFINE, s1[v], acc1[v], alpha, beta);
-    }
-  }
-  // C's V rows for chunks 2 it and 2 it + 1: lane (j, g) takes
-  // V[c_t][nb + 16n + j] for t = t0(k) + 4g + st (chunks past len_last and
-  // output tiles past dv read a valid address and hold zeros)
-  auto load_v = [&](int it, int64_t nb, float (&bv)[2][4][4])
+  // V rows (B operand of P V, [n tile][st]): for t = t0(k) + 4g + st, lane
+  // (j, g) takes V[c_t][nb + 4j + n] (IL) or V[c_t][nb + 16n + j]; tiles
+  // n >= ntiles read tile 0 again -- their outputs are never stored, so
+  // their values need no select (a select on the wave-uniform n < ntiles
+  // would become a branch around each load)
+  auto load_v = [&](int k, int64_t nb, float (&bv)[4][4])
       __attribute__((always_inline)) {
     const int ntiles = (int)std::min<int64_t>(4, (dv - nb) / 16);
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+    for (int st = 0; st < 4; ++st) {
+      const int32_t t = chunk_t0(k) + 4 * g + st;
+      const uint32_t c = lcol[std::min(t, last)];
+      if constexpr (IL) {
+        const uint32_t vo = 4u * (c * (uint32_t)dv + 4u * (uint32_t)i);
+        const v4f x = *reinterpret_cast<const v4f *>(at_bytes(value + nb, vo));
 #pragma unroll
-      for (int st = 0; st < 4; ++st) {
-        const int32_t t = chunk_t0(2 * it + h) + 4 * g + st;
-        const uint32_t c = lcol[std::max(std::min(t, len_last - 1), 0)];
-        if constexpr (IL) {
-          // V[c][nb + 4j .. nb + 4j + 3], tile n taking element n
-          const uint32_t vo =
-              4u * ((t < len_last ? c * (uint32_t)dv : 0u) + 4u * (uint32_t)i);
-          const v4f x = *reinterpret_cast<const v4f *>(at_bytes(value + nb, vo));
-#pragma unroll
-          for (int n = 0; n < 4; ++n)
-            bv[h][n][st] = t < len_last ? x[n] : 0.0f;
-          continue;
-        }
-        // V[c][nb + 16n + j]: the wave-uniform column nb + 16n plus the
-        // lane's byte offset (row c, column j; row 0 past len_last).  Tiles
-        // n >= ntiles read tile 0 again: their outputs are never stored, so
-        // their values need no select (a select on the wave-uniform n <
-        // ntiles would become a branch around each load).
-        const uint32_t vo =
-            4u * ((t < len_last ? c * (uint32_t)dv : 0u) + (uint32_t)i);
+        for (int n = 0; n < 4; ++n)
+          bv[n][st] = x[n];
+      } else {
+        const uint32_t vo = 4u * (c * (uint32_t)dv + (uint32_t)i);
 #pragma unroll
         for (int n = 0; n < 4; ++n) {
           const int nn = n < ntiles ? n : 0; // wave-uniform
-          const float x = *at_bytes(value + nb + 16 * nn, vo);
-          bv[h][n][st] = t < len_last ? x : 0.0f;
+          bv[n][st] = *at_bytes(value + nb + 16 * nn, vo);
         }
       }
+    }
   };
-  float bv[2][4][4];
-  load_v(0, 0, bv); // in flight over the softmax
+  // A. S^T per chunk: sv[k][v] = score (i, t0(k) + 4g + v)
+  float sv[kFusedChunks][4];
+  auto sddmm_chunk = [&](int k, const float (&a)[16 * KB], const v4f &w)
+      __attribute__((always_inline)) {
+    v4f acc = {0.f, 0.f, 0.f, 0.f};
+    if (chunk_t0(k) < len_last) { // wave-uniform
+#pragma unroll
+      for (int st = 0; st < 16 * KB; ++st)
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[st], qa[st], acc, 0, 0,
+                                                   0);
+    }
+    const uint32_t d = rbase + chunk_t0(k) + 4 * g - window_at(k);
+    const v4f x = {d == 0 ? w.x : d == 1 ? w.y : d == 2 ? w.z : w.w,
+                   d == 0 ? w.y : d == 1 ? w.z : w.w, d == 0 ? w.z : w.w, w.w};
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+      sv[k][v] = combine_sddmm(SW_SDDMM_AFFINE, valid(k, v) ? x[v] : 0.0f,
+                               acc[v], alpha, beta);
+  };
+  float bv[kFusedChunks][4][4];
+  // two chunks' K^T gathers and mask windows per batch; a chunk past the
+  // last row's entries loads nothing (each branch holds its loads and the
+  // products that take them, so no branch waits for a load it does not use)
+#pragma unroll
+  for (int k0 = 0; k0 < kFusedChunks; k0 += 2) {
+    if (chunk_t0(k0 + 1) < len_last) { // wave-uniform
+      float a[2][16 * KB];
+      v4f w[2];
+      gather_k(k0, a[0]);
+      gather_k(k0 + 1, a[1]);
+      __builtin_memcpy(&w[0], mask + window_at(k0), sizeof(v4f));
+      __builtin_memcpy(&w[1], mask + window_at(k0 + 1), sizeof(v4f));
+      __builtin_amdgcn_sched_barrier(0);
+      sddmm_chunk(k0, a[0], w[0]);
+      sddmm_chunk(k0 + 1, a[1], w[1]);
+    } else {
+      if (chunk_t0(k0) < len_last) {
+        float a[16 * KB];
+        v4f w;
+        gather_k(k0, a);
+        __builtin_memcpy(&w, mask + window_at(k0), sizeof(v4f));
+        __builtin_amdgcn_sched_barrier(0);
+        sddmm_chunk(k0, a, w);
+      } else {
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          sv[k0][v] = 0.0f;
+      }
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        sv[k0 + 1][v] = 0.0f;
+    }
+  }
+  // in flight over the softmax (the V rows of chunks 2-3 are loaded after
+  // it: holding all four chunks' rows over it would take more registers
+  // than four waves per SIMD leave)
+  load_v(0, 0, bv[0]);
+  load_v(1, 0, bv[1]);
   // B. row softmax: lanes (i, 0..3) of every wave hold row i's entries
   {
     float m = -INFINITY;
@@ -834,25 +843,16 @@ __global__ __launch_bounds__(64 * W) void attention_tile_fused(
   }
   // C. output = P V with P from sv (lane (i, g) holds P[i][t0(k)+4g+st],
   // the A operand of step st); the waves' partial tiles are summed in LDS
-  auto mfma_pair = [&](int it, const float (&b)[2][4][4], v4f (&acc)[4])
+  auto mfma_chunk = [&](int k, const float (&b)[4][4], v4f (&acc)[4])
       __attribute__((always_inline)) {
+    if (chunk_t0(k) < len_last) // wave-uniform
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
-      if (chunk_t0(2 * it + h) < len_last) // wave-uniform
+      for (int n = 0; n < 4; ++n)
 #pragma unroll
-        for (int n = 0; n < 4; ++n)
-#pragma unroll
-          for (int st = 0; st < 4; ++st)
-            acc[n] = __builtin_amdgcn_mfma_f32_16x16x4f32(
-                sv[2 * it + h][st], b[h][n][st], acc[n], 0, 0, 0);
+        for (int st = 0; st < 4; ++st)
+          acc[n] = __builtin_amdgcn_mfma_f32_16x16x4f32(sv[k][st], b[n][st],
+                                                        acc[n], 0, 0, 0);
   };
-  // The rows of a tile share each MFMA's V operand, so an inf or NaN in a V
-  // row that a shorter row of the tile leaves out would reach that row as
-  // 0 * inf.  The tile's last row holds every entry, so such a value makes
-  // some output of the tile non-finite: a tile with a non-finite output
-  // has it recomputed row by row from the stored scores, adding exactly
-  // each row's own entries (the same values wherever the MFMA result was
-  // right).
   bool nonfinite = false;
   for (int64_t nb = 0; nb < dv; nb += 64) {
     const int ntiles = (int)std::min<int64_t>(4, (dv - nb) / 16);
@@ -860,16 +860,18 @@ __global__ __launch_bounds__(64 * W) void attention_tile_fused(
 #pragma unroll
     for (int n = 0; n < 4; ++n)
       acc[n] = v4f{0.f, 0.f, 0.f, 0.f};
-    if (nb > 0)
-      load_v(0, nb, bv);
-    // keep the loads ahead of the MFMAs that take them
-    __builtin_amdgcn_sched_barrier(0);
-    mfma_pair(0, bv, acc);
-    if (chunk_t0(2) < len_last) { // wave-uniform
-      load_v(1, nb, bv);
-      __builtin_amdgcn_sched_barrier(0);
-      mfma_pair(1, bv, acc);
+    if (nb > 0) {
+#pragma unroll
+      for (int k = 0; k < kFusedChunks; ++k)
+        load_v(k, nb, bv[k]);
+    } else {
+      load_v(2, 0, bv[2]);
+      load_v(3, 0, bv[3]);
     }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < kFusedChunks; ++k)
+      mfma_chunk(k, bv[k], acc);
 #pragma unroll
     for (int n = 0; n < 4; ++n)
 #pragma unroll
@@ -1044,11 +1046,24 @@ __global__ __launch_bounds__(64 * W) void sddmm_tile_mfma_bf16(
 // The attention chain fused over 16-row tiles, bf16 (d = 64 * KB,
 // dv % 64 == 0): the fp32 attention_tile_fused's tiles, waves, chunks,
 // structure check and fallbacks, with the products on bf16 matrix cores.
+// Its loads are batched so that the chain of dependent memory trips is short:
+//   1. the tile's row offsets (one load, spread to the lanes by permutes) and
+//      its Q rows;
+//   2. the rows' column indices for the structure check, with every chunk's
+//      mask window in flight over the check and its barriers;
+//   3. the K^T gathers of all four chunks (d = 64; chunks 0-1, then 2-3 for
+//      d = 128) with the V rows of chunks 0-1; the V rows of chunks 2-3 fly
+//      over the softmax.
+// Entries past the last row read the last row's final column, so no load is
+// guarded; their scores are never used and their P is zero.  A V row that
+// is inf or NaN makes the tile's output non-finite wherever it is read
+// (0 * inf), and such tiles are recomputed row by row, as in the fp32 kernel.
 // The host guarantees that the byte offsets into mask / scores (2 * nnz),
 // K^T (2 * d * cols) and V (2 * cols * dv) fit 32 bits, that nnz >= 4
 // (amax = nnz - 4) and that Q is 16-byte and V 8-byte aligned.
+// (at most 128 VGPRs: the two workgroups of a CU need four waves per SIMD)
 template <int KB, int W>
-__global__ __launch_bounds__(64 * W) void attention_tile_fused_bf16(
+__global__ __launch_bounds__(64 * W, 4) void attention_tile_fused_bf16(
     const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
     const uint16_t *__restrict__ mask, const uint16_t *__restrict__ q,
     const uint16_t *__restrict__ kt, const uint16_t *__restrict__ value,
@@ -1061,16 +1076,15 @@ __global__ __launch_bounds__(64 * W) void attention_tile_fused_bf16(
   __shared__ float part[W][4][4][kWave]; // [wave][n tile][v][lane]
   __shared__ float wred[2][W][16];       // [max, sum][wave][row]
   __shared__ int32_t lcol[kFusedCols];   // the last row's columns
-  __shared__ int verdict;
+  __shared__ int wshared[W]; // each wave's rows share the last row's columns
   __shared__ int v_nonfinite;
   const int r0 = blockIdx.x * 16;
   const int nt = std::min(16, rows - r0);
   const int wave = threadIdx.x / kWave;
   const int l = lane_id(), i = l & 15, g = l >> 4;
-  const int ic = i < nt ? i : nt - 1;
-  const int32_t rbase = ro[r0 + ic];
-  const int32_t la = i < nt ? ro[r0 + ic + 1] - rbase : 0;
-  // B operand of S^T = K_chunk Q^T: Q row r0 + i, elements 32 s + 8 g .. + 7
+  // 1. lanes 0..nt hold ro[r0 .. r0 + nt]; Q row r0 + i, elements
+  //    32 s + 8 g .. + 7 (the B operand of S^T = K_chunk Q^T)
+  const int32_t my_ro = ro[r0 + (l < nt ? l : nt)];
   v4u qb[S];
   const int64_t qrow = (int64_t)std::min(r0 + i, rows - 1) * kdim;
 #pragma unroll
@@ -1078,15 +1092,35 @@ __global__ __launch_bounds__(64 * W) void attention_tile_fused_bf16(
     const v4u x = *reinterpret_cast<const v4u *>(q + qrow + 32 * s + 8 * g);
     qb[s] = i < nt ? x : v4u{0u, 0u, 0u, 0u};
   }
-  const int32_t my_ro = ro[r0 + (l < nt ? l : nt)];
+  // (scheduling barriers keep each batch of loads together and in order,
+  // so that waiting for one batch leaves the later ones in flight)
+  __builtin_amdgcn_sched_barrier(0);
+  // row i's first position and length (0 past nt); the permutes run on
+  // every lane, as a permute reads zero from a lane that is switched off
+  const int ic = i < nt ? i : nt - 1;
+  const int32_t rbase = __builtin_amdgcn_ds_bpermute(ic << 2, my_ro);
+  const int32_t rnext = __builtin_amdgcn_ds_bpermute((ic + 1) << 2, my_ro);
+  const int32_t la = i < nt ? rnext - rbase : 0;
   const int32_t bl = __builtin_amdgcn_readlane(my_ro, nt - 1);
   const int32_t len_last = __builtin_amdgcn_readlane(my_ro, nt) - bl;
+  auto chunk_t0 = [&](int k) __attribute__((always_inline)) {
+    return 16 * (wave + W * k);
+  };
+  auto valid = [&](int k, int v) __attribute__((always_inline)) {
+    return chunk_t0(k) + 4 * g + v < la;
+  };
+  // 2. row i's mask values at entries t0(k) + 4g .. + 3: the raw 8-byte
+  //    window, read from position min(e, amax) for the window's first
+  //    position e and shifted by e - min(e, amax) where the values are used
+  auto window_at = [&](int k) __attribute__((always_inline)) {
+    const uint32_t e = rbase + chunk_t0(k) + 4 * g;
+    return e < amax ? e : amax;
+  };
+  uint64_t mw[kFusedChunks];
   bool ok = len_last <= kFusedCols; // workgroup-uniform
   if (ok) {
-    if (threadIdx.x == 0) {
-      verdict = 1;
+    if (threadIdx.x == 0)
       v_nonfinite = 0;
-    }
     int32_t x[2][8], yl[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
@@ -1105,29 +1139,37 @@ __global__ __launch_bounds__(64 * W) void attention_tile_fused_bf16(
         x[h][u] = col[len > 0 ? b + std::min(t, len - 1) : 0];
       }
     }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < kFusedChunks; ++k)
+      __builtin_memcpy(&mw[k], mask + window_at(k), sizeof(uint64_t));
+    __builtin_amdgcn_sched_barrier(0);
+    // without branches: a compare inside a branch would pull its loads
+    // into the branch, behind the mask windows
     bool mine = true;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int rr = wave + h * W;
-      if (rr < nt - 1) { // wave-uniform
-        const int32_t b = __builtin_amdgcn_readlane(my_ro, rr);
-        const int32_t len = __builtin_amdgcn_readlane(my_ro, rr + 1) - b;
-        mine &= len <= len_last;
+      const int rc = rr < nt - 1 ? rr : 0;
+      const int32_t b = __builtin_amdgcn_readlane(my_ro, rc);
+      const int32_t len = __builtin_amdgcn_readlane(my_ro, rc + 1) - b;
+      bool same = len <= len_last;
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
-          if (l + u * kWave < len)
-            mine &= x[h][u] == yl[u];
-      }
+      for (int u = 0; u < 8; ++u)
+        same &= (l + u * kWave >= len) | (x[h][u] == yl[u]);
+      mine &= (rr >= nt - 1) | same;
     }
 #pragma unroll
     for (int u = 0; u < 8; ++u)
       if (u == wave && l + u * kWave < len_last)
         lcol[l + u * kWave] = yl[u];
+    const bool shared_cols = __builtin_amdgcn_ballot_w64(!mine) == 0;
+    if (l == 0)
+      wshared[wave] = shared_cols;
     __syncthreads();
-    if (__builtin_amdgcn_ballot_w64(!mine) != 0 && l == 0)
-      verdict = 0;
-    __syncthreads();
-    ok = verdict != 0;
+#pragma unroll
+    for (int w = 0; w < W; ++w)
+      ok &= wshared[w] != 0;
   }
   if (!ok) { // workgroup-uniform
     for (int r = r0 + wave; r < r0 + nt; r += W) {
@@ -1140,78 +1182,90 @@ __global__ __launch_bounds__(64 * W) void attention_tile_fused_bf16(
     }
     return;
   }
-  auto chunk_t0 = [&](int k) __attribute__((always_inline)) {
-    return 16 * (wave + W * k);
-  };
-  auto valid = [&](int k, int v) __attribute__((always_inline)) {
-    return chunk_t0(k) + 4 * g + v < la;
-  };
-  // A. S^T per chunk: sv[k][v] = score (i, t0(k) + 4g + v), rounded to bf16
+  // 3. the gathers; entries past the last row read its final column
+  const int32_t last = std::max(len_last - 1, 0);
   const uint32_t row_bytes = 2u * (uint32_t)cols;
-  float sv[kFusedChunks][4];
+  // K_chunk rows (A operand): K^T[32 s + 8 g .. + 7][column of entry t0 + i]
+  auto gather_k = [&](int k, v4u (&a)[S]) __attribute__((always_inline)) {
+    const uint32_t cj = lcol[std::min(chunk_t0(k) + i, last)];
+    const uint32_t ko = 2u * cj + 8u * g * row_bytes;
 #pragma unroll
-  for (int it = 0; it < kFusedChunks / 2; ++it) {
-    const int32_t t0 = chunk_t0(2 * it), t1 = chunk_t0(2 * it + 1);
-    const bool one = t0 < len_last, two = t1 < len_last; // wave-uniform
-    const int32_t last = std::max(len_last - 1, 0);
-    const uint32_t cj0 = lcol[std::min(t0 + i, last)];
-    const uint32_t cj1 = lcol[std::min(two ? t1 + i : t0 + i, last)];
-    float s0[4] = {0.f, 0.f, 0.f, 0.f}, s1[4] = {0.f, 0.f, 0.f, 0.f};
-    v4f acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-    if (one) {
-      const uint64_t x0 = ld_window4(mask, rbase + t0 + 4 * g, amax);
-      const uint64_t x1 = ld_window4(mask, rbase + t1 + 4 * g, amax);
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        s0[v] = valid(2 * it, v) ? bf16_to_f32((uint16_t)(x0 >> (16 * v)))
-                                 : 0.0f;
-        s1[v] = valid(2 * it + 1, v) ? bf16_to_f32((uint16_t)(x1 >> (16 * v)))
-                                     : 0.0f;
-      }
-      const uint32_t ko0 = 2u * cj0 + 8u * g * row_bytes;
-      const uint32_t ko1 = 2u * cj1 + 8u * g * row_bytes;
-      v4u a0[S], a1[S];
-#pragma unroll
-      for (int s = 0; s < S; ++s) {
-        const uint16_t *base = kt + (int64_t)(32 * s) * cols;
-        a0[s] = gather_kt8(base, row_bytes, ko0);
-        a1[s] = gather_kt8(base, row_bytes, ko1);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int s = 0; s < S; ++s) {
-        acc0 = mfma_16x16x32_bf16(a0[s], qb[s], acc0);
-        if (two)
-          acc1 = mfma_16x16x32_bf16(a1[s], qb[s], acc1);
-      }
-    }
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      sv[2 * it][v] = as_stored<uint16_t>(
-          combine_sddmm(SW_SDDMM_AFFINE, s0[v], acc0[v], alpha, beta));
-      sv[2 * it + 1][v] = as_stored<uint16_t>(
-          combine_sddmm(SW_SDDMM_AFFINE, s1[v], acc1[v], alpha, beta));
-    }
-  }
-  // C's V rows for chunks 2 it and 2 it + 1: lane (j, g) takes
-  // V[c_t][nb + 4j .. nb + 4j + 3] for t = t0(k) + 4g + st (zero past
-  // len_last, read from row 0)
-  auto load_v = [&](int it, int64_t nb, v2u (&bv)[2][4])
+    for (int s = 0; s < S; ++s)
+      a[s] = gather_kt8(kt + (int64_t)(32 * s) * cols, row_bytes, ko);
+  };
+  // V rows (B operand of P V): lane (j, g) takes V[c_t][nb + 4j .. + 3] for
+  // t = t0(k) + 4g + st, tile n taking element n
+  auto load_v = [&](int k, int64_t nb, v2u (&bv)[4])
       __attribute__((always_inline)) {
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int st = 0; st < 4; ++st) {
-        const int32_t t = chunk_t0(2 * it + h) + 4 * g + st;
-        const uint32_t c = lcol[std::max(std::min(t, len_last - 1), 0)];
-        const uint32_t vo =
-            2u * ((t < len_last ? c * (uint32_t)dv : 0u) + 4u * (uint32_t)i);
-        const v2u x = *reinterpret_cast<const v2u *>(at_bytes(value + nb, vo));
-        bv[h][st] = t < len_last ? x : v2u{0u, 0u};
-      }
+    for (int st = 0; st < 4; ++st) {
+      const int32_t t = chunk_t0(k) + 4 * g + st;
+      const uint32_t c = lcol[std::min(t, last)];
+      const uint32_t vo = 2u * (c * (uint32_t)dv + 4u * (uint32_t)i);
+      bv[st] = *reinterpret_cast<const v2u *>(at_bytes(value + nb, vo));
+    }
   };
-  v2u bv[2][4];
-  load_v(0, 0, bv); // in flight over the softmax
+  // A. S^T per chunk: sv[k][v] = score (i, t0(k) + 4g + v), rounded to bf16
+  float sv[kFusedChunks][4];
+  auto sddmm_chunk = [&](int k, const v4u (&a)[S])
+      __attribute__((always_inline)) {
+    v4f acc = {0.f, 0.f, 0.f, 0.f};
+    if (chunk_t0(k) < len_last) { // wave-uniform
+#pragma unroll
+      for (int s = 0; s < S; ++s)
+        acc = mfma_16x16x32_bf16(a[s], qb[s], acc);
+    }
+    const uint32_t d = rbase + chunk_t0(k) + 4 * g - window_at(k);
+    const uint64_t w = d < 4 ? mw[k] >> (16 * d) : 0ull;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const float x = valid(k, v) ? bf16_to_f32((uint16_t)(w >> (16 * v)))
+                                  : 0.0f;
+      sv[k][v] = as_stored<uint16_t>(
+          combine_sddmm(SW_SDDMM_AFFINE, x, acc[v], alpha, beta));
+    }
+  };
+  // two chunks' K^T gathers per batch; a chunk past the last row's entries
+  // loads nothing (each branch holds its loads and the products that take
+  // them, so no branch waits for a load it does not use)
+  auto batch = [&](int k0) __attribute__((always_inline)) {
+    if (chunk_t0(k0 + 1) < len_last) { // wave-uniform
+      v4u a[2][S];
+      gather_k(k0, a[0]);
+      gather_k(k0 + 1, a[1]);
+      __builtin_amdgcn_sched_barrier(0);
+      sddmm_chunk(k0, a[0]);
+      sddmm_chunk(k0 + 1, a[1]);
+    } else {
+      if (chunk_t0(k0) < len_last) {
+        v4u a[S];
+        gather_k(k0, a);
+        __builtin_amdgcn_sched_barrier(0);
+        sddmm_chunk(k0, a);
+      } else {
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          sv[k0][v] = 0.0f;
+      }
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        sv[k0 + 1][v] = 0.0f;
+    }
+  };
+  v2u bv[kFusedChunks][4];
+  batch(0);
+  if constexpr (KB == 1) { // in flight over the second batch and the softmax
+    load_v(0, 0, bv[0]);
+    load_v(1, 0, bv[1]);
+  }
+  batch(2);
+  if constexpr (KB == 1) { // in flight over the softmax
+    load_v(2, 0, bv[2]);
+    load_v(3, 0, bv[3]);
+  } else {
+    load_v(0, 0, bv[0]);
+    load_v(1, 0, bv[1]);
+  }
   // B. row softmax on the stored (bf16) scores, each op's result rounded
   {
     float m = -INFINITY;
@@ -1272,22 +1326,18 @@ __global__ __launch_bounds__(64 * W) void attention_tile_fused_bf16(
     }
   }
   // C. output = P V: P from sv (lane (i, g) holds P[i][t0(k) + 4g + st])
-  auto mfma_pair = [&](int it, const v2u (&b)[2][4], v4f (&acc)[4])
+  auto mfma_chunk = [&](int k, const v2u (&b)[4], v4f (&acc)[4])
       __attribute__((always_inline)) {
+    if (chunk_t0(k) < len_last) { // wave-uniform
+      const v2u a = v2u{pack_bf16x2(sv[k][0], sv[k][1]),
+                        pack_bf16x2(sv[k][2], sv[k][3])};
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
-      if (chunk_t0(2 * it + h) < len_last) { // wave-uniform
-        const int k = 2 * it + h;
-        const v2u a = v2u{pack_bf16x2(sv[k][0], sv[k][1]),
-                          pack_bf16x2(sv[k][2], sv[k][3])};
-#pragma unroll
-        for (int n = 0; n < 4; ++n) {
-          const v2u bn =
-              v2u{bf16_half(b[h][0], n) | (bf16_half(b[h][1], n) << 16),
-                  bf16_half(b[h][2], n) | (bf16_half(b[h][3], n) << 16)};
-          acc[n] = mfma_16x16x16_bf16(a, bn, acc[n]);
-        }
+      for (int n = 0; n < 4; ++n) {
+        const v2u bn = v2u{bf16_half(b[0], n) | (bf16_half(b[1], n) << 16),
+                           bf16_half(b[2], n) | (bf16_half(b[3], n) << 16)};
+        acc[n] = mfma_16x16x16_bf16(a, bn, acc[n]);
       }
+    }
   };
   bool nonfinite = false;
   for (int64_t nb = 0; nb < dv; nb += 64) {
@@ -1295,15 +1345,18 @@ __global__ __launch_bounds__(64 * W) void attention_tile_fused_bf16(
 #pragma unroll
     for (int n = 0; n < 4; ++n)
       acc[n] = v4f{0.f, 0.f, 0.f, 0.f};
-    if (nb > 0)
-      load_v(0, nb, bv);
-    __builtin_amdgcn_sched_barrier(0);
-    mfma_pair(0, bv, acc);
-    if (chunk_t0(2) < len_last) { // wave-uniform
-      load_v(1, nb, bv);
-      __builtin_amdgcn_sched_barrier(0);
-      mfma_pair(1, bv, acc);
+    if (nb > 0) {
+#pragma unroll
+      for (int k = 0; k < kFusedChunks; ++k)
+        load_v(k, nb, bv[k]);
+    } else if constexpr (KB != 1) {
+      load_v(2, 0, bv[2]);
+      load_v(3, 0, bv[3]);
     }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < kFusedChunks; ++k)
+      mfma_chunk(k, bv[k], acc);
 #pragma unroll
     for (int n = 0; n < 4; ++n)
 #pragma unroll
