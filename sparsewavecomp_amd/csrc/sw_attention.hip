@@ -1075,7 +1075,6 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused_bf16(
   constexpr int S = 2 * KB;
   __shared__ float part[W][4][4][kWave]; // [wave][n tile][v][lane]
   __shared__ float wred[2][W][16];       // [max, sum][wave][row]
-  __shared__ int32_t lcol[kFusedCols];   // the last row's columns
   __shared__ int wshared[W]; // each wave's rows share the last row's columns
   __shared__ int v_nonfinite;
   const int r0 = blockIdx.x * 16;
@@ -1117,78 +1116,27 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused_bf16(
     return e < amax ? e : amax;
   };
   uint64_t mw[kFusedChunks];
+  // The structure check and the products run together: each wave checks its
+  // rows against the last row and computes its chunks with the last row's
+  // columns right away; the verdict is read at the softmax's first barrier,
+  // before anything is stored, and a tile that fails it is redone row by
+  // row.  The last row's column indices stay in registers: lane j of yl[u]
+  // holds entry 64u + j (clamped to the last entry), and a lane takes the
+  // column of an entry from there with a permute.
   bool ok = len_last <= kFusedCols; // workgroup-uniform
-  if (ok) {
-    if (threadIdx.x == 0)
-      v_nonfinite = 0;
-    int32_t x[2][8], yl[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int32_t t = l + u * kWave;
-      yl[u] = col[len_last > 0 ? bl + std::min(t, len_last - 1) : 0];
-    }
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int rr = wave + h * W;
-      const int rc = rr < nt - 1 ? rr : 0;
-      const int32_t b = __builtin_amdgcn_readlane(my_ro, rc);
-      const int32_t len = __builtin_amdgcn_readlane(my_ro, rc + 1) - b;
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int32_t t = l + u * kWave;
-        x[h][u] = col[len > 0 ? b + std::min(t, len - 1) : 0];
-      }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int k = 0; k < kFusedChunks; ++k)
-      __builtin_memcpy(&mw[k], mask + window_at(k), sizeof(uint64_t));
-    __builtin_amdgcn_sched_barrier(0);
-    // without branches: a compare inside a branch would pull its loads
-    // into the branch, behind the mask windows
-    bool mine = true;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int rr = wave + h * W;
-      const int rc = rr < nt - 1 ? rr : 0;
-      const int32_t b = __builtin_amdgcn_readlane(my_ro, rc);
-      const int32_t len = __builtin_amdgcn_readlane(my_ro, rc + 1) - b;
-      bool same = len <= len_last;
-#pragma unroll
-      for (int u = 0; u < 8; ++u)
-        same &= (l + u * kWave >= len) | (x[h][u] == yl[u]);
-      mine &= (rr >= nt - 1) | same;
-    }
-#pragma unroll
-    for (int u = 0; u < 8; ++u)
-      if (u == wave && l + u * kWave < len_last)
-        lcol[l + u * kWave] = yl[u];
-    const bool shared_cols = __builtin_amdgcn_ballot_w64(!mine) == 0;
-    if (l == 0)
-      wshared[wave] = shared_cols;
-    __syncthreads();
-#pragma unroll
-    for (int w = 0; w < W; ++w)
-      ok &= wshared[w] != 0;
-  }
-  if (!ok) { // workgroup-uniform
-    for (int r = r0 + wave; r < r0 + nt; r += W) {
-      sddmm_row_wave(ro, col, mask, q, kt, scores, r, cols, kdim,
-                     SW_SDDMM_AFFINE, alpha, beta);
-      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
-      attention_row_softmax(ro, scores, rmax, rsum, r);
-      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
-      attention_row_output(ro, col, scores, value, out, r, dv);
-    }
-    return;
-  }
-  // 3. the gathers; entries past the last row read its final column
-  const int32_t last = std::max(len_last - 1, 0);
-  const uint32_t row_bytes = 2u * (uint32_t)cols;
+  if (threadIdx.x == 0)
+    v_nonfinite = 0;
+  // yk[k]: the yl register holding chunk k's entries 16 (w + 8k) .. + 15,
+  // in lanes 16 (w & 3) .. + 15
+  int32_t yk[kFusedChunks];
+  auto col_of = [&](int k, int off) __attribute__((always_inline)) {
+    return (uint32_t)__builtin_amdgcn_ds_bpermute(
+        (16 * (wave & 3) + off) << 2, yk[k]);
+  };
   // K_chunk rows (A operand): K^T[32 s + 8 g .. + 7][column of entry t0 + i]
+  const uint32_t row_bytes = 2u * (uint32_t)cols;
   auto gather_k = [&](int k, v4u (&a)[S]) __attribute__((always_inline)) {
-    const uint32_t cj = lcol[std::min(chunk_t0(k) + i, last)];
-    const uint32_t ko = 2u * cj + 8u * g * row_bytes;
+    const uint32_t ko = 2u * col_of(k, i) + 8u * g * row_bytes;
 #pragma unroll
     for (int s = 0; s < S; ++s)
       a[s] = gather_kt8(kt + (int64_t)(32 * s) * cols, row_bytes, ko);
@@ -1199,8 +1147,7 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused_bf16(
       __attribute__((always_inline)) {
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
-      const int32_t t = chunk_t0(k) + 4 * g + st;
-      const uint32_t c = lcol[std::min(t, last)];
+      const uint32_t c = col_of(k, 4 * g + st);
       const uint32_t vo = 2u * (c * (uint32_t)dv + 4u * (uint32_t)i);
       bv[st] = *reinterpret_cast<const v2u *>(at_bytes(value + nb, vo));
     }
@@ -1253,21 +1200,66 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused_bf16(
     }
   };
   v2u bv[kFusedChunks][4];
-  batch(0);
-  if constexpr (KB == 1) { // in flight over the second batch and the softmax
-    load_v(0, 0, bv[0]);
-    load_v(1, 0, bv[1]);
-  }
-  batch(2);
-  if constexpr (KB == 1) { // in flight over the softmax
-    load_v(2, 0, bv[2]);
-    load_v(3, 0, bv[3]);
-  } else {
-    load_v(0, 0, bv[0]);
-    load_v(1, 0, bv[1]);
-  }
-  // B. row softmax on the stored (bf16) scores, each op's result rounded
-  {
+  if (ok) {
+    int32_t x[2][8], yl[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int32_t t = l + u * kWave;
+      yl[u] = col[len_last > 0 ? bl + std::min(t, len_last - 1) : 0];
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int rr = wave + h * W;
+      const int rc = rr < nt - 1 ? rr : 0;
+      const int32_t b = __builtin_amdgcn_readlane(my_ro, rc);
+      const int32_t len = __builtin_amdgcn_readlane(my_ro, rc + 1) - b;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int32_t t = l + u * kWave;
+        x[h][u] = col[len > 0 ? b + std::min(t, len - 1) : 0];
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < kFusedChunks; ++k)
+      __builtin_memcpy(&mw[k], mask + window_at(k), sizeof(uint64_t));
+    __builtin_amdgcn_sched_barrier(0);
+    // without branches: a compare inside a branch would pull its loads
+    // into the branch, behind the mask windows
+    bool mine = true;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int rr = wave + h * W;
+      const int rc = rr < nt - 1 ? rr : 0;
+      const int32_t b = __builtin_amdgcn_readlane(my_ro, rc);
+      const int32_t len = __builtin_amdgcn_readlane(my_ro, rc + 1) - b;
+      bool same = len <= len_last;
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        same &= (l + u * kWave >= len) | (x[h][u] == yl[u]);
+      mine &= (rr >= nt - 1) | same;
+    }
+    const bool shared_cols = __builtin_amdgcn_ballot_w64(!mine) == 0;
+    if (l == 0)
+      wshared[wave] = shared_cols;
+#pragma unroll
+    for (int k = 0; k < kFusedChunks; ++k)
+      yk[k] = wave >= 4 ? yl[2 * k + 1] : yl[2 * k];
+    batch(0);
+    if constexpr (KB == 1) { // in flight over the second batch and softmax
+      load_v(0, 0, bv[0]);
+      load_v(1, 0, bv[1]);
+    }
+    batch(2);
+    if constexpr (KB == 1) { // in flight over the softmax
+      load_v(2, 0, bv[2]);
+      load_v(3, 0, bv[3]);
+    } else {
+      load_v(0, 0, bv[0]);
+      load_v(1, 0, bv[1]);
+    }
+    // B. row softmax on the stored (bf16) scores, each op's result rounded:
+    // this wave's row maxima
     float m = -INFINITY;
 #pragma unroll
     for (int k = 0; k < kFusedChunks; ++k)
@@ -1279,8 +1271,26 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused_bf16(
     m = maximumf(m, shfl_xor32(m));
     if (g == 0)
       wred[0][wave][i] = m;
-    __syncthreads();
-    m = wred[0][0][i];
+  }
+  __syncthreads();
+  if (ok) {
+#pragma unroll
+    for (int w = 0; w < W; ++w)
+      ok &= wshared[w] != 0;
+  }
+  if (!ok) { // workgroup-uniform; nothing has been stored yet
+    for (int r = r0 + wave; r < r0 + nt; r += W) {
+      sddmm_row_wave(ro, col, mask, q, kt, scores, r, cols, kdim,
+                     SW_SDDMM_AFFINE, alpha, beta);
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+      attention_row_softmax(ro, scores, rmax, rsum, r);
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+      attention_row_output(ro, col, scores, value, out, r, dv);
+    }
+    return;
+  }
+  {
+    float m = wred[0][0][i];
 #pragma unroll
     for (int w = 1; w < W; ++w)
       m = maximumf(m, wred[0][w][i]);
