@@ -800,15 +800,21 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused(
 #pragma unroll
     for (int w = 1; w < W; ++w)
       m = maximumf(m, wred[0][w][i]);
+    // per chunk of entries (a chunk past the last row is skipped whole),
+    // each entry's value computed unconditionally and selected afterwards:
+    // no branch per entry
     float sum = 0.0f;
 #pragma unroll
-    for (int k = 0; k < kFusedChunks; ++k)
+    for (int k = 0; k < kFusedChunks; ++k) {
+      if (chunk_t0(k) < len_last) { // wave-uniform
 #pragma unroll
-      for (int v = 0; v < 4; ++v)
-        if (valid(k, v)) {
-          sv[k][v] = expf(sv[k][v] - m);
+        for (int v = 0; v < 4; ++v) {
+          const float e = expf(sv[k][v] - m);
+          sv[k][v] = valid(k, v) ? e : 0.0f;
           sum += sv[k][v];
         }
+      }
+    }
     sum += swizzle_xor16(sum);
     sum += shfl_xor32(sum);
     if (g == 0)
@@ -820,9 +826,17 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused(
       sum += wred[1][w][i];
 #pragma unroll
     for (int k = 0; k < kFusedChunks; ++k) {
+      if (chunk_t0(k) >= len_last) { // wave-uniform
 #pragma unroll
-      for (int v = 0; v < 4; ++v) // zero past the row: P V adds nothing
-        sv[k][v] = valid(k, v) ? sv[k][v] / sum : 0.0f;
+        for (int v = 0; v < 4; ++v)
+          sv[k][v] = 0.0f;
+        continue;
+      }
+#pragma unroll
+      for (int v = 0; v < 4; ++v) { // zero past the row: P V adds nothing
+        const float p = sv[k][v] / sum;
+        sv[k][v] = valid(k, v) ? p : 0.0f;
+      }
       // entries t0(k) + 4g .. + 3 of row i: one (unaligned) vector store
       // when all four are the row's, else the row's ones one by one
       float *dst = scores + rbase + chunk_t0(k) + 4 * g;
