@@ -1064,14 +1064,17 @@ __global__ __launch_bounds__(64 * W) void sddmm_tile_mfma_bf16(
 //   1. the tile's row offsets (one load, spread to the lanes by permutes) and
 //      its Q rows;
 //   2. the rows' column indices for the structure check, with every chunk's
-//      mask window in flight over the check and its barriers;
-//   3. the K^T gathers of all four chunks (d = 64; chunks 0-1, then 2-3 for
-//      d = 128) with the V rows of chunks 0-1; the V rows of chunks 2-3 fly
-//      over the softmax.
-// Entries past the last row read the last row's final column, so no load is
-// guarded; their scores are never used and their P is zero.  A V row that
-// is inf or NaN makes the tile's output non-finite wherever it is read
-// (0 * inf), and such tiles are recomputed row by row, as in the fp32 kernel.
+//      mask window in flight over the check;
+//   3. the K^T gathers of chunks 0-1, then of chunks 2-3 (none for chunks
+//      past the last row); the V rows of chunks 0-1 fly over the second
+//      batch (d = 64) or the softmax, those of chunks 2-3 over the softmax
+//      (d = 64) or are loaded after it.
+// The products do not wait for the structure check: its verdict is read at
+// the softmax's first barrier, before anything is stored.  Entries past the
+// last row read the last row's final column, so no load is guarded; their
+// scores are never used and their P is zero.  A V row that is inf or NaN
+// makes the tile's output non-finite wherever it is read (0 * inf), and such
+// tiles are recomputed row by row, as in the fp32 kernel.
 // The host guarantees that the byte offsets into mask / scores (2 * nnz),
 // K^T (2 * d * cols) and V (2 * cols * dv) fit 32 bits, that nnz >= 4
 // (amax = nnz - 4) and that Q is 16-byte and V 8-byte aligned.
