@@ -238,6 +238,26 @@ __device__ __forceinline__ uint32_t bf16_half(v2u w, int n) {
   return (n & 1) ? d >> 16 : d & 0xFFFFu;
 }
 
+// Raw buffer descriptor (stride 0) over the n bytes at the wave-uniform p.
+// A buffer load adds a 32-bit lane offset and a wave-uniform SGPR offset to
+// the descriptor's base, so a lane's address costs no vector instruction.
+// Word 3 is the gfx9-family format word of a raw 32-bit buffer.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *p,
+                                                              uint32_t n) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, (int)n,
+                                           0x00020000);
+}
+
+// the float at byte lane_off + uniform_off of the buffer (lane_off < n, the
+// descriptor's size, or the load reads zero)
+__device__ __forceinline__ float buffer_load_f32(__amdgpu_buffer_rsrc_t r,
+                                                 uint32_t lane_off,
+                                                 uint32_t uniform_off) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)lane_off,
+                                                  (int)uniform_off, 0));
+}
+
 // p advanced by b bytes.  With p wave-uniform this is the form the global
 // memory instructions take directly (base in SGPRs, one 32-bit VGPR offset),
 // so a lane's address costs no 64-bit arithmetic; the caller guarantees that
