@@ -142,11 +142,24 @@ __global__ __launch_bounds__(1024) void spmv_block_per_row(
   const int64_t r = blockIdx.x;
   const int t = threadIdx.x;
   const int B = blockDim.x;
-  float acc = 0.0f;
-  if (r < rows) {
-    int32_t s = ro[r], e = ro[r + 1];
-    acc = strided_dot<NARROW>(col, val, x, s + t, e, B, 0.0f);
+  if (r >= rows)
+    return; // block-uniform: no barrier follows for this block
+  const int32_t s = ro[r], e = ro[r + 1];
+  if (e - s <= kWave) { // block-uniform
+    // A row of at most one wave's positions: only wave 0 holds products,
+    // each thread one, and the other waves' partial sums are zeros.  Wave
+    // 0 alone gives the same sum -- its butterfly, plus the zeros the full
+    // reduction would add (which turns a -0 into +0) -- without the LDS
+    // exchange and the barrier.
+    if (t >= kWave)
+      return;
+    const float w = wave_sum(strided_dot<NARROW>(col, val, x, s + t, e, B,
+                                                 0.0f));
+    if (t == 0)
+      y[r] = w + 0.0f;
+    return;
   }
+  float acc = strided_dot<NARROW>(col, val, x, s + t, e, B, 0.0f);
   // blockDim.x is a multiple of 64 (validated), so every wave is full
   float w = wave_sum(acc);
   const int wave = t / kWave;
@@ -157,7 +170,7 @@ __global__ __launch_bounds__(1024) void spmv_block_per_row(
     const int waves = B / kWave;
     float v = lane_id() < waves ? partial[lane_id()] : 0.0f;
     v = wave_sum(v);
-    if (t == 0 && r < rows)
+    if (t == 0)
       y[r] = v;
   }
 }
