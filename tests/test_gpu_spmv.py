@@ -272,6 +272,32 @@ def test_row_recovery_bit_exact(dev, orc, config2):
             out.cpu().numpy(), orc.rows_at_positions(csr.row_offsets, pos))
 
 
+@pytest.mark.parametrize("block", [64, 256, 1024])
+def test_block_per_row_short_and_long_rows(dev, orc, block):
+    """block-per-row takes a shortcut for rows of at most 64 entries (wave 0
+    alone, no LDS exchange): rows of 0, 1, 63, 64, 65, 200 and 3000 entries
+    against the oracle, and a row of -0.0 products, whose sum the full
+    reduction (and the reference's zero-initialised accumulator) makes +0."""
+    rng = np.random.default_rng(block)
+    lengths = [0, 1, 63, 64, 65, 200, 3000, 5, 64, 0, 17]
+    cols = 4000
+    ro = np.zeros(len(lengths) + 1, np.int32)
+    np.cumsum(lengths, out=ro[1:])
+    col = np.concatenate([np.sort(rng.choice(cols, n, replace=False))
+                          for n in lengths]).astype(np.int32)
+    val = rng.uniform(-1, 1, col.size).astype(np.float32)
+    x = rng.uniform(-1, 1, cols).astype(np.float32)
+    # row 7: five products -0.0 * x > 0
+    z = slice(ro[7], ro[8])
+    val[z] = -0.0
+    x[col[z]] = np.abs(x[col[z]]) + 0.5
+    csr = W.CSR(len(lengths), cols, ro, col, val)
+    y = G.spmv(csr, x, f"spmv-mapping=block-per-row spmv-block-size={block}")
+    _check(orc, csr, x, y)
+    assert y[7] == 0.0 and not np.signbit(y[7])
+    assert y[0] == 0.0 and not np.signbit(y[0])
+
+
 def test_repeat_is_stable(dev, orc):
     """Position mappings zero the output on every call (no accumulation
     across calls)."""
