@@ -445,6 +445,43 @@ def test_attention_fused_paths(dev, orc, shape, d, dv):
     _check_attention(orc, csr, *_attention_case(orc, csr, d, dv, FUSED))
 
 
+def _f32_offset(a):
+    """A float32 device view of a that starts one element (4 bytes) past an
+    aligned address, so every 16-byte alignment check fails."""
+    a = np.asarray(a, np.float32)
+    flat = torch.empty(a.size + 1, dtype=torch.float32, device=G.DEV)
+    view = flat[1:].view(a.shape)
+    view.copy_(G.t(a))
+    return view
+
+
+@pytest.mark.parametrize("dv", [64, 80])
+def test_attention_fused_misaligned_operands(dev, orc, dv):
+    """The fp32 fused kernel with every value buffer one element off a
+    16-byte boundary: the non-interleaved output tiles, element-aligned Q
+    and mask windows, and K^T gathers through a descriptor whose base is
+    only 4-byte aligned."""
+    csr = _tile_structure_csr()
+    d = 64
+    rng = np.random.default_rng(dv)
+    q = rng.standard_normal((csr.rows, d)).astype(np.float32)
+    kt = rng.standard_normal((d, csr.cols)).astype(np.float32)
+    v = rng.standard_normal((csr.cols, dv)).astype(np.float32)
+    G.say(f"fused attention misaligned operands dv={dv}")
+    scores = _f32_offset(np.full(csr.nnz, np.nan, np.float32))
+    rmax = _f32_offset(np.full(csr.rows, np.nan, np.float32))
+    rsum = _f32_offset(np.full(csr.rows, np.nan, np.float32))
+    out = _f32_offset(np.full((csr.rows, dv), np.nan, np.float32))
+    sw.sparse_attention(G.t(csr.row_offsets), G.t(csr.column_indices),
+                        _f32_offset(csr.values), _f32_offset(q),
+                        _f32_offset(kt), _f32_offset(v), scores, rmax, rsum,
+                        out, 0.125, 0.5, options=FUSED)
+    torch.cuda.synchronize()
+    refs = orc.sparse_attention(csr.row_offsets, csr.column_indices,
+                                csr.values, q, kt, v, 0.125, 0.5)
+    _check_attention(orc, csr, scores, rmax, rsum, out, refs, v)
+
+
 def _few_entries_csr(nnz):
     """Five rows holding nnz entries in all (one to six), rows of one, two
     and three entries and empty rows: with nnz >= 4 the fused kernel reads
