@@ -66,6 +66,16 @@ __device__ __forceinline__ float as_stored(float v) {
     return bf16_to_f32(f32_to_bf16(v));
 }
 
+// exp(x) in the fused chains, as the hardware base-2 exponential of
+// x log2 e (v_exp_f32): rounding the product adds at most
+// 2^-24 |x log2 e| ln 2 relative error (1.2e-6 at x = -20, beside
+// v_exp_f32's own ulp), about 2 instructions instead of the library expf's
+// 10.  A softmax's arguments are x = s - max <= 0, so nothing overflows;
+// -inf gives 0 and NaN stays NaN, as with expf.
+__device__ __forceinline__ float exp_by_exp2(float x) {
+  return __builtin_amdgcn_exp2f(x * 1.44269504088896341f);
+}
+
 __device__ __forceinline__ float map_value(int kind, float v, float rv) {
   switch (kind) {
   case SW_MAP_EXP_SUB:
@@ -814,7 +824,7 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused(
       if (chunk_t0(k) < len_last) { // wave-uniform
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-          const float e = expf(sv[k][v] - m);
+          const float e = exp_by_exp2(sv[k][v] - m);
           sv[k][v] = valid(k, v) ? e : 0.0f;
           sum += sv[k][v];
         }
@@ -829,6 +839,9 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused(
 #pragma unroll
     for (int w = 1; w < W; ++w)
       sum += wred[1][w][i];
+    // one correctly rounded reciprocal per row, one multiply per entry
+    // (within 1.5 ulp of the quotient)
+    const float rsum_i = 1.0f / sum;
 #pragma unroll
     for (int k = 0; k < kFusedChunks; ++k) {
       if (chunk_t0(k) >= len_last) { // wave-uniform
@@ -839,7 +852,7 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused(
       }
 #pragma unroll
       for (int v = 0; v < 4; ++v) { // zero past the row: P V adds nothing
-        const float p = sv[k][v] / sum;
+        const float p = sv[k][v] * rsum_i;
         sv[k][v] = valid(k, v) ? p : 0.0f;
       }
       // entries t0(k) + 4g .. + 3 of row i: one (unaligned) vector store
@@ -1322,7 +1335,7 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused_bf16(
 #pragma unroll
       for (int v = 0; v < 4; ++v)
         if (valid(k, v)) {
-          sv[k][v] = as_stored<uint16_t>(expf(sv[k][v] - m));
+          sv[k][v] = as_stored<uint16_t>(exp_by_exp2(sv[k][v] - m));
           sum += sv[k][v];
         }
     sum += swizzle_xor16(sum);
@@ -1335,11 +1348,14 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused_bf16(
     for (int w = 1; w < W; ++w)
       sum += wred[1][w][i];
     sum = as_stored<uint16_t>(sum);
+    // one correctly rounded reciprocal per row, one multiply per entry
+    // (within 1.5 ulp of the quotient before the bf16 rounding)
+    const float rsum_i = 1.0f / sum;
 #pragma unroll
     for (int k = 0; k < kFusedChunks; ++k) {
 #pragma unroll
       for (int v = 0; v < 4; ++v)
-        sv[k][v] = valid(k, v) ? as_stored<uint16_t>(sv[k][v] / sum) : 0.0f;
+        sv[k][v] = valid(k, v) ? as_stored<uint16_t>(sv[k][v] * rsum_i) : 0.0f;
       uint16_t *dst = scores + rbase + chunk_t0(k) + 4 * g;
       if (valid(k, 3)) {
         const v2u x = v2u{pack_bf16x2(sv[k][0], sv[k][1]),

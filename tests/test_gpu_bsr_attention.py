@@ -411,12 +411,11 @@ def _long_prefix_csr():
     return W.CSR(len(rows_cols), cols, ro, col, val)
 
 
-def _attention_case(orc, csr, d, dv, options):
+def _attention_case(orc, csr, d, dv, options, alpha=0.125, beta=0.5):
     rng = np.random.default_rng(d + dv)
     q = rng.standard_normal((csr.rows, d)).astype(np.float32)
     kt = rng.standard_normal((d, csr.cols)).astype(np.float32)
     v = rng.standard_normal((csr.cols, dv)).astype(np.float32)
-    alpha, beta = 0.125, 0.5
     nan = float("nan")
     scores = torch.full((csr.nnz,), nan, device=G.DEV)
     rmax = torch.full((csr.rows,), nan, device=G.DEV)
@@ -443,6 +442,23 @@ def test_attention_fused_paths(dev, orc, shape, d, dv):
     G.say(f"fused attention {shape} rows={csr.rows} nnz={csr.nnz} d={d} "
           f"dv={dv}")
     _check_attention(orc, csr, *_attention_case(orc, csr, d, dv, FUSED))
+
+
+@pytest.mark.parametrize("opts", ATT_OPTS)
+def test_attention_wide_score_range(dev, orc, opts):
+    """Scores spread over about 70 below their row's maximum (alpha = 1 on
+    N(0, 1) operands, d = 64), so the exponentials run over a wide range of
+    arguments: the fused kernel's exp2 of the score times log2 e and its
+    reciprocal row sums against the oracle's expf and division.  (An fp32
+    sequential SDDMM alone moves these probabilities by up to 1.4e-5
+    relative against exact arithmetic; the score tolerance is 1e-4.)"""
+    mask, _, _, _, _ = W.config5(seed=0, seq=1024)
+    G.say(f"attention wide score range opts='{opts}'")
+    scores, rmax, rsum, out, refs, v = _attention_case(orc, mask, 64, 64, opts,
+                                                       alpha=1.0, beta=0.0)
+    s_ref = refs[0]
+    assert float(np.log(s_ref[s_ref > 0]).min()) < -40.0
+    _check_attention(orc, mask, scores, rmax, rsum, out, refs, v)
 
 
 def _f32_offset(a):
