@@ -45,13 +45,10 @@ __device__ __forceinline__ float combine_sddmm(int kind, float sample,
   return dot;
 }
 
-// arith.maximumf: NaN propagates, +0 is above -0.
+// arith.maximumf: NaN propagates, +0 is above -0 -- the IEEE 754-2019
+// maximum, which gfx950 computes in one v_maximum3_f32 (llvm.maximum)
 __device__ __forceinline__ float maximumf(float a, float b) {
-  if (a != a || b != b)
-    return __builtin_nanf("");
-  if (a == b)
-    return __float_as_int(a) < 0 ? b : a;
-  return a > b ? a : b;
+  return __builtin_elementwise_maximum(a, b);
 }
 
 // A result as its op stores it: unchanged in fp32, rounded to bf16 (and

@@ -327,6 +327,17 @@ def test_row_reduce_and_map(dev, orc, golden, opts):
                              zip(csr.row_offsets[:-1], csr.row_offsets[1:])])
             assert np.all(np.abs(got[ok] - ref[ok]) <= 1e-5 * absb[ok] + 0)
             del lens
+    # the sign of a zero maximum: +0 is above -0 in either order
+    zs = np.array([-0.0, 0.0, 0.0, -0.0, -0.0, -0.0, -0.0, 0.0], np.float32)
+    zro = np.array([0, 2, 4, 6, 7, 8], np.int32)
+    zout = torch.empty(5, device=G.DEV)
+    sw.csr_row_reduce(G.t(zro), None, G.t(zs), zout, "max", options=opts)
+    torch.cuda.synchronize()
+    zref = orc.row_reduce(zro, zs, orc.REDUCE_MAX)
+    np.testing.assert_array_equal(np.signbit(zout.cpu().numpy()),
+                                  np.signbit(zref))
+    np.testing.assert_array_equal(np.signbit(zref),
+                                  [False, False, True, True, False])
     rowv = np.random.default_rng(1).uniform(0.5, 2, csr.rows).astype(
         np.float32)
     for kind in (sw.MAP_EXP_SUB, sw.MAP_DIV, sw.MAP_SUB, sw.MAP_MUL):
