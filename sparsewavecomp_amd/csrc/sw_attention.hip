@@ -664,10 +664,12 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused(
         same &= (l + u * kWave >= len) | (x[h][u] == yl[u]);
       mine &= (rr >= nt - 1) | same;
     }
-    // wave w stores the last row's entries 64w .. 64w + 63
+    // wave w stores the last row's entries 64w .. 64w + 63; those past the
+    // row hold its final column (the clamped loads above), so that the
+    // gathers read lcol without clamping an index
 #pragma unroll
     for (int u = 0; u < 8; ++u)
-      if (u == wave && l + u * kWave < len_last)
+      if (u == wave)
         lcol[l + u * kWave] = yl[u];
     const bool shared_cols = __builtin_amdgcn_ballot_w64(!mine) == 0;
     if (l == 0)
@@ -689,7 +691,6 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused(
     return;
   }
   // 3. the gathers; entries past the last row read its final column
-  const int32_t last = std::max(len_last - 1, 0);
   // K_chunk rows (A operand of step kb 16 + st): K^T[kb 64 + 16 g + st][c]
   // for the column c of entry t0 + i -- the lane's byte offset (16 g rows
   // and c columns on) plus the wave-uniform offset of row kb 64 + st, as
@@ -699,7 +700,7 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused(
       buffer_rsrc(kt, 4u * (uint32_t)kdim * (uint32_t)cols);
   auto gather_k = [&](int k, float (&a)[16 * KB])
       __attribute__((always_inline)) {
-    const uint32_t cj = lcol[std::min(chunk_t0(k) + i, last)];
+    const uint32_t cj = lcol[chunk_t0(k) + i];
     const uint32_t ko = 4u * (16u * g * (uint32_t)cols + cj);
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb)
@@ -719,7 +720,7 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused(
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
       const int32_t t = chunk_t0(k) + 4 * g + st;
-      const uint32_t c = lcol[std::min(t, last)];
+      const uint32_t c = lcol[t];
       if constexpr (IL) {
         const uint32_t vo = 4u * (c * (uint32_t)dv + 4u * (uint32_t)i);
         const v4f x = *reinterpret_cast<const v4f *>(at_bytes(value + nb, vo));

@@ -336,6 +336,23 @@ def test_bf16_attention_few_entries(dev, orc, nnz):
                           exact_frac=0.9)
 
 
+def test_bf16_attention_fused_empty_tile(dev, orc):
+    """A tile of 16 empty rows between populated tiles under the fused
+    options: the identities in its rows (row maximum -inf, row sum 0,
+    output 0)."""
+    from tests.test_gpu_bsr_attention import _empty_tile_csr
+    csr = _empty_tile_csr()
+    rng = np.random.default_rng(5)
+    q = rng.standard_normal((csr.rows, 64)).astype(np.float32)
+    kt = rng.standard_normal((64, csr.cols)).astype(np.float32)
+    v = rng.standard_normal((csr.cols, 64)).astype(np.float32)
+    got = _attention_bf16(csr, csr.values, q, kt, v, 0.125, 0.5, FUSED)
+    _check_attention_bf16(orc, csr, csr.values, q, kt, v, 0.125, 0.5, got)
+    _, rmax, rsum, out = got
+    assert np.all(np.isneginf(rmax[16:32])) and np.all(rsum[16:32] == 0)
+    assert np.all(out[16:32] == 0)
+
+
 @pytest.mark.parametrize("opts", [FUSED] + ATT_OPTS[:2])
 def test_bf16_attention_non_finite_value_rows(dev, orc, opts):
     """inf / NaN in V rows that a tile's last row includes and its shorter

@@ -525,6 +525,43 @@ def _few_entries_csr(nnz):
     return W.CSR(5, 8, ro, col, val)
 
 
+def _empty_tile_csr():
+    """40 rows: a prefix-structured 16-row tile, a tile of 16 empty rows
+    (its last row is empty, so the structure check passes with no entries
+    at all) and a partial tile of 8 rows."""
+    rng = np.random.default_rng(17)
+    cols = 96
+    rows_cols = []
+    for nt, width in ((16, 70), (16, 0), (8, 40)):
+        base = np.sort(rng.choice(cols, max(width, 1), replace=False))
+        lens = np.sort(rng.integers(1, width + 1, nt)) if width else \
+            np.zeros(nt, np.int64)
+        if width:
+            lens[-1] = width
+        rows_cols += [base[:n].copy() for n in lens]
+    lengths = np.array([len(c) for c in rows_cols])
+    ro = np.zeros(len(rows_cols) + 1, np.int32)
+    np.cumsum(lengths, out=ro[1:])
+    col = np.concatenate(rows_cols).astype(np.int32)
+    val = rng.uniform(-1, 1, col.size).astype(np.float32)
+    return W.CSR(len(rows_cols), cols, ro, col, val)
+
+
+@pytest.mark.parametrize("dv", [64, 80])
+def test_attention_fused_empty_tile(dev, orc, dv):
+    """A tile whose rows are all empty takes the fused path with no entry:
+    its outputs are the identities (row maximum -inf, row sum 0, output 0)
+    and the V rows it reads are valid ones."""
+    csr = _empty_tile_csr()
+    assert np.all(np.diff(csr.row_offsets)[16:32] == 0)
+    G.say(f"fused attention empty tile dv={dv}")
+    got = _attention_case(orc, csr, 64, dv, FUSED)
+    _check_attention(orc, csr, *got)
+    rmax, rsum, out = got[1].cpu().numpy(), got[2].cpu().numpy(), got[3]
+    assert np.all(np.isneginf(rmax[16:32])) and np.all(rsum[16:32] == 0)
+    assert np.all(out.cpu().numpy()[16:32] == 0)
+
+
 @pytest.mark.parametrize("nnz", [1, 2, 3, 4, 5, 6])
 def test_attention_few_entries(dev, orc, nnz):
     csr = _few_entries_csr(nnz)
