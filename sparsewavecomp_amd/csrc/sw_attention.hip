@@ -1233,6 +1233,7 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused_bf16(
     }
   };
   v2u bv[kFusedChunks][4];
+  v2u pk[kFusedChunks]; // P as bf16 pairs: entries 4g, 4g + 1 | 4g + 2, 4g + 3
   if (ok) {
     int32_t x[2][8], yl[8];
 #pragma unroll
@@ -1349,21 +1350,23 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused_bf16(
     // one correctly rounded reciprocal per row, one multiply per entry
     // (within 1.5 ulp of the quotient before the bf16 rounding)
     const float rsum_i = 1.0f / sum;
+    // P rounded to bf16 once, as pairs: the stored scores and the A operand
+    // of P V are the same bits
 #pragma unroll
     for (int k = 0; k < kFusedChunks; ++k) {
+      float p[4];
 #pragma unroll
       for (int v = 0; v < 4; ++v)
-        sv[k][v] = valid(k, v) ? as_stored<uint16_t>(sv[k][v] * rsum_i) : 0.0f;
+        p[v] = valid(k, v) ? sv[k][v] * rsum_i : 0.0f;
+      pk[k] = v2u{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3])};
       uint16_t *dst = scores + rbase + chunk_t0(k) + 4 * g;
       if (valid(k, 3)) {
-        const v2u x = v2u{pack_bf16x2(sv[k][0], sv[k][1]),
-                          pack_bf16x2(sv[k][2], sv[k][3])};
-        __builtin_memcpy(dst, &x, sizeof x);
+        __builtin_memcpy(dst, &pk[k], sizeof pk[k]);
       } else {
 #pragma unroll
         for (int v = 0; v < 3; ++v)
           if (valid(k, v))
-            dst[v] = f32_to_bf16(sv[k][v]);
+            dst[v] = (uint16_t)(pk[k][v >> 1] >> (16 * (v & 1)));
       }
     }
     if (wave == 0 && g == 0 && i < nt) {
@@ -1371,17 +1374,14 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused_bf16(
       stv(rsum + r0 + i, sum);
     }
   }
-  // C. output = P V: P from sv (lane (i, g) holds P[i][t0(k) + 4g + st])
+  // C. output = P V: P from pk (lane (i, g) holds P[i][t0(k) + 4g + st])
   auto mfma_chunk = [&](int k, const v2u (&b)[4], v4f (&acc)[4])
       __attribute__((always_inline)) {
     if (chunk_t0(k) < len_last) { // wave-uniform
-      const v2u a = v2u{pack_bf16x2(sv[k][0], sv[k][1]),
-                        pack_bf16x2(sv[k][2], sv[k][3])};
 #pragma unroll
       for (int n = 0; n < 4; ++n) {
-        const v2u bn = v2u{bf16_half(b[0], n) | (bf16_half(b[1], n) << 16),
-                           bf16_half(b[2], n) | (bf16_half(b[3], n) << 16)};
-        acc[n] = mfma_16x16x16_bf16(a, bn, acc[n]);
+        const v2u bn = v2u{bf16_pair(b[0], b[1], n), bf16_pair(b[2], b[3], n)};
+        acc[n] = mfma_16x16x16_bf16(pk[k], bn, acc[n]);
       }
     }
   };

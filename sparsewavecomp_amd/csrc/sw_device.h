@@ -232,10 +232,12 @@ __device__ __forceinline__ v4f mfma_16x16x16_bf16(v2u a, v2u b, v4f c) {
   return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
       __builtin_bit_cast(v4s, a), __builtin_bit_cast(v4s, b), c, 0, 0, 0);
 }
-// Half n (0..3) of a 4-element bf16 vector held as two dwords.
-__device__ __forceinline__ uint32_t bf16_half(v2u w, int n) {
-  const uint32_t d = (n & 2) ? w.y : w.x;
-  return (n & 1) ? d >> 16 : d & 0xFFFFu;
+// Element n (0..3) of two 4-element bf16 vectors, each held as two dwords, as
+// one bf16 pair with a's in the low half: one byte permute (v_perm_b32 picks
+// bytes of {hi: db, lo: da}).
+__device__ __forceinline__ uint32_t bf16_pair(v2u a, v2u b, int n) {
+  const uint32_t da = (n & 2) ? a.y : a.x, db = (n & 2) ? b.y : b.x;
+  return __builtin_amdgcn_perm(db, da, (n & 1) ? 0x07060302u : 0x05040100u);
 }
 
 // Raw buffer descriptor (stride 0) over the n bytes at the wave-uniform p.

@@ -706,9 +706,8 @@ __global__ __launch_bounds__(64 * W) void spmm_tile_mfma_bf16(
       for (int h = 0; h < CH; ++h)
 #pragma unroll
         for (int n = 0; n < 4; ++n) {
-          const v2u bn =
-              v2u{bf16_half(bq[h][0], n) | (bf16_half(bq[h][1], n) << 16),
-                  bf16_half(bq[h][2], n) | (bf16_half(bq[h][3], n) << 16)};
+          const v2u bn = v2u{bf16_pair(bq[h][0], bq[h][1], n),
+                             bf16_pair(bq[h][2], bq[h][3], n)};
           acc[n] = mfma_16x16x16_bf16(a[h], bn, acc[n]);
         }
     }
