@@ -1328,15 +1328,21 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused_bf16(
 #pragma unroll
     for (int w = 1; w < W; ++w)
       m = maximumf(m, wred[0][w][i]);
+    // per chunk of entries (a chunk past the last row is skipped whole),
+    // each entry's value computed unconditionally and selected afterwards:
+    // no branch per entry (adding the zeros leaves the sum's bits as they are)
     float sum = 0.0f;
 #pragma unroll
-    for (int k = 0; k < kFusedChunks; ++k)
+    for (int k = 0; k < kFusedChunks; ++k) {
+      if (chunk_t0(k) < len_last) { // wave-uniform
 #pragma unroll
-      for (int v = 0; v < 4; ++v)
-        if (valid(k, v)) {
-          sv[k][v] = as_stored<uint16_t>(exp_by_exp2(sv[k][v] - m));
+        for (int v = 0; v < 4; ++v) {
+          const float e = as_stored<uint16_t>(exp_by_exp2(sv[k][v] - m));
+          sv[k][v] = valid(k, v) ? e : 0.0f;
           sum += sv[k][v];
         }
+      }
+    }
     sum += swizzle_xor16(sum);
     sum += shfl_xor32(sum);
     if (g == 0)
