@@ -70,6 +70,12 @@ def parse():
                          "headline mapping of that workload)")
     ap.add_argument("--k", type=int, default=4,
                     help="rhs columns for --profile spmm")
+    ap.add_argument("--x-entries", type=int, default=0,
+                    help="for --profile spmv / floor: redraw configuration "
+                         "2's columns uniformly over an x of this many "
+                         "entries (sorted within each row), to see how the "
+                         "gathers' speed depends on x's size against the "
+                         "L2 (default: configuration 2 itself)")
     return ap.parse_args()
 
 
@@ -105,7 +111,17 @@ def profile(args):
             dst.copy_(src)
     elif w in ("spmv", "floor", "coo", "spmm"):
         csr, x = W.config2(seed=0)
-        ro, col, val = T(csr.row_offsets), T(csr.column_indices), T(csr.values)
+        cols = csr.column_indices
+        if args.x_entries > 0 and w in ("spmv", "floor"):
+            nx = args.x_entries
+            rng = np.random.default_rng(1)
+            rows = np.repeat(np.arange(csr.rows, dtype=np.int64),
+                             np.diff(csr.row_offsets))
+            key = np.sort(rows * nx + rng.integers(0, nx, csr.nnz))
+            cols = (key % nx).astype(np.int32)
+            x = rng.uniform(-1.0, 1.0, nx).astype(np.float32)
+            log(f"columns redrawn over {nx} x entries")
+        ro, col, val = T(csr.row_offsets), T(cols), T(csr.values)
         if w == "spmv":
             o = sw.Options.parse(args.opts or HEADLINE_SPMV)
             xv, y = T(x), torch.empty(csr.rows, device=dev)
