@@ -238,14 +238,14 @@ __global__ __launch_bounds__(64 * SPL) void bsr16_mfma_bf16_x8(
       if (u < nb) {
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
-          // element t of the four rows: dword t / 2, half t % 2
-          const int d = t >> 1, sh = 16 * (t & 1);
-          const uint32_t e0 = (q[u][0][d] >> sh) & 0xFFFFu;
-          const uint32_t e1 = (q[u][1][d] >> sh) & 0xFFFFu;
-          const uint32_t e2 = (q[u][2][d] >> sh) & 0xFFFFu;
-          const uint32_t e3 = (q[u][3][d] >> sh) & 0xFFFFu;
-          acc[t] = mfma_16x16x16_bf16(a[u], v2u{e0 | (e1 << 16), e2 | (e3 << 16)},
-                                      acc[t]);
+          // element t of the four rows (dword t / 2, half t % 2), paired by
+          // byte permutes
+          const int d = t >> 1;
+          const uint32_t sel = (t & 1) ? 0x07060302u : 0x05040100u;
+          const v2u bt = v2u{
+              __builtin_amdgcn_perm(q[u][1][d], q[u][0][d], sel),
+              __builtin_amdgcn_perm(q[u][3][d], q[u][2][d], sel)};
+          acc[t] = mfma_16x16x16_bf16(a[u], bt, acc[t]);
         }
       }
     }
