@@ -580,7 +580,8 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused(
   __shared__ int v_nonfinite; // an output of the tile is inf or NaN
   const int r0 = blockIdx.x * 16;
   const int nt = std::min(16, rows - r0);
-  const int wave = threadIdx.x / kWave;
+  // wave-uniform, so in a scalar register: the tests on it are scalar
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int l = lane_id(), i = l & 15, g = l >> 4;
   // 1. lanes 0..nt hold ro[r0 .. r0 + nt]; Q row r0 + i, elements
   //    kb 64 + 16 g + st (the B operand of step st)
@@ -1112,7 +1113,8 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused_bf16(
   __shared__ int v_nonfinite;
   const int r0 = blockIdx.x * 16;
   const int nt = std::min(16, rows - r0);
-  const int wave = threadIdx.x / kWave;
+  // wave-uniform, so in a scalar register: the tests on it are scalar
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int l = lane_id(), i = l & 15, g = l >> 4;
   // 1. lanes 0..nt hold ro[r0 .. r0 + nt]; Q row r0 + i, elements
   //    32 s + 8 g .. + 7 (the B operand of S^T = K_chunk Q^T)
