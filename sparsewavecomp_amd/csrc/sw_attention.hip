@@ -194,7 +194,7 @@ __global__ __launch_bounds__(256) void sddmm_wave_per_row(
     const T *__restrict__ rhs, T *__restrict__ out, int32_t rows,
     int64_t cols, int32_t kdim, int kind, float alpha, float beta) {
   const int64_t r = (int64_t)blockIdx.x * (blockDim.x / kWave) +
-                    threadIdx.x / kWave;
+                    wave_in_group();
   if (r >= rows)
     return; // wave-uniform
   sddmm_row_wave(ro, col, val, lhs, rhs, out, r, cols, kdim, kind, alpha,
@@ -224,7 +224,7 @@ __global__ __launch_bounds__(64 * W) void sddmm_tile_mfma(
     int64_t cols, int32_t kdim, int kind, float alpha, float beta) {
   const int r0 = blockIdx.x * 16;
   const int nt = std::min(16, rows - r0);
-  const int wave = threadIdx.x / kWave;
+  const int wave = wave_in_group();
   const int l = lane_id(), i = l & 15, g = l >> 4;
   // loads are unconditional from clamped, valid addresses, their values
   // selected afterwards (a guarded load becomes a branch that waits for it
@@ -358,7 +358,7 @@ __global__ __launch_bounds__(256) void row_reduce_wave(
     const int32_t *__restrict__ ro, const T *__restrict__ val,
     T *__restrict__ out, int32_t rows) {
   const int64_t r = (int64_t)blockIdx.x * (blockDim.x / kWave) +
-                    threadIdx.x / kWave;
+                    wave_in_group();
   if (r >= rows)
     return;
   const int l = lane_id();
@@ -401,7 +401,7 @@ __global__ __launch_bounds__(256) void rowwise_map_wave(
     const int32_t *__restrict__ ro, const T *val,
     const T *__restrict__ rowv, T *out, int32_t rows, int kind) {
   const int64_t r = (int64_t)blockIdx.x * (blockDim.x / kWave) +
-                    threadIdx.x / kWave;
+                    wave_in_group();
   if (r >= rows)
     return;
   const float rv = ldv(rowv + r);
@@ -422,7 +422,7 @@ __global__ __launch_bounds__(256) void row_softmax_wave(
     const int32_t *__restrict__ ro, T *scores, T *__restrict__ rmax,
     T *__restrict__ rsum, int32_t rows) {
   const int64_t r = (int64_t)blockIdx.x * (blockDim.x / kWave) +
-                    threadIdx.x / kWave;
+                    wave_in_group();
   if (r >= rows)
     return;
   const int l = lane_id();
@@ -580,8 +580,7 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused(
   __shared__ int v_nonfinite; // an output of the tile is inf or NaN
   const int r0 = blockIdx.x * 16;
   const int nt = std::min(16, rows - r0);
-  // wave-uniform, so in a scalar register: the tests on it are scalar
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int wave = wave_in_group();
   const int l = lane_id(), i = l & 15, g = l >> 4;
   // 1. lanes 0..nt hold ro[r0 .. r0 + nt]; Q row r0 + i, elements
   //    kb 64 + 16 g + st (the B operand of step st)
@@ -996,7 +995,7 @@ __global__ __launch_bounds__(64 * W) void sddmm_tile_mfma_bf16(
   constexpr int S = 2 * KB; // 32-deep K steps
   const int r0 = blockIdx.x * 16;
   const int nt = std::min(16, rows - r0);
-  const int wave = threadIdx.x / kWave;
+  const int wave = wave_in_group();
   const int l = lane_id(), i = l & 15, g = l >> 4;
   int32_t rb[4], rl[4];
   {
@@ -1113,8 +1112,7 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused_bf16(
   __shared__ int v_nonfinite;
   const int r0 = blockIdx.x * 16;
   const int nt = std::min(16, rows - r0);
-  // wave-uniform, so in a scalar register: the tests on it are scalar
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int wave = wave_in_group();
   const int l = lane_id(), i = l & 15, g = l >> 4;
   // 1. lanes 0..nt hold ro[r0 .. r0 + nt]; Q row r0 + i, elements
   //    32 s + 8 g .. + 7 (the B operand of S^T = K_chunk Q^T)

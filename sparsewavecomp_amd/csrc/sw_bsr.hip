@@ -76,7 +76,7 @@ __global__ __launch_bounds__(256) void bsr16_mfma_f32(
     const float *__restrict__ bval, const float *__restrict__ rhs,
     float *__restrict__ out, int64_t k, int nbr) {
   const int br = xcd_block_row(blockIdx.x, nbr);
-  const int wave = threadIdx.x / kWave;
+  const int wave = wave_in_group();
   const int l = lane_id();
   const int i = l & 15, g = l >> 4;
   const int64_t n0 = (int64_t)blockIdx.y * 128 + wave * 32;
@@ -134,7 +134,7 @@ __global__ __launch_bounds__(256) void bsr16_mfma_bf16(
     const uint16_t *__restrict__ bval, const uint16_t *__restrict__ rhs,
     TO *__restrict__ out, int64_t k, int nbr) {
   const int br = xcd_block_row(blockIdx.x, nbr);
-  const int wave = threadIdx.x / kWave;
+  const int wave = wave_in_group();
   const int l = lane_id();
   const int i = l & 15, g = l >> 4;
   const int64_t n0 = (int64_t)blockIdx.y * 128 + wave * 32;
@@ -204,7 +204,7 @@ __global__ __launch_bounds__(64 * SPL) void bsr16_mfma_bf16_x8(
     TO *__restrict__ out, int64_t k, int nbr) {
   __shared__ float red[SPL > 1 ? SPL - 1 : 1][8][4][kWave];
   const int64_t br = xcd_contiguous(blockIdx.x, gridDim.x);
-  const int sp = threadIdx.x / kWave;
+  const int sp = wave_in_group();
   const int l = lane_id();
   const int j = l & 15, g = l >> 4;
   const int64_t cb = (int64_t)blockIdx.y * 128 + 8 * j;
@@ -309,7 +309,7 @@ __global__ __launch_bounds__(64 * kF32Strips * SPL) void bsr16_mfma_f32_x4(
   __shared__ float red[kF32Strips][SPL > 1 ? SPL - 1 : 1][4][4][kWave];
   const int br = xcd_block_row(blockIdx.x, nbr);
   const int strips = blockDim.x / (kWave * SPL);
-  const int wv = threadIdx.x / kWave;
+  const int wv = wave_in_group();
   const int strip = wv % strips, sp = wv / strips;
   const int l = lane_id();
   const int i = l & 15, g = l >> 4;

@@ -25,6 +25,12 @@ typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 __device__ __forceinline__ int lane_id() { return __lane_id(); }
+// The wave's index in its workgroup, in a scalar register: it is the same in
+// every lane, but as threadIdx.x / 64 the compiler keeps it per lane and
+// makes every test and product on it a vector instruction.
+__device__ __forceinline__ int wave_in_group() {
+  return __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+}
 
 // ---- DPP --------------------------------------------------------------
 // DPP control codes (GFX9 encoding).
@@ -342,7 +348,7 @@ __device__ __forceinline__ bool tile_prefix_ok_block(
     const int32_t *__restrict__ ro, const int32_t *__restrict__ col, int r0,
     int nt, int *verdict /* __shared__ int[1] */) {
   const int lane = lane_id();
-  const int wave = threadIdx.x / kWave;
+  const int wave = wave_in_group();
   const int waves = blockDim.x / kWave;
   if (threadIdx.x == 0)
     *verdict = 1;

@@ -248,7 +248,7 @@ __global__ __launch_bounds__(1024) void spmm_wave_position(
   constexpr int PL = kWave / CL;
   const int lane = lane_id();
   const int64_t wave =
-      (int64_t)blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+      (int64_t)blockIdx.x * (blockDim.x / kWave) + wave_in_group();
   if (wave >= chunks * tiles)
     return;
   const int64_t chunk = wave / tiles;
@@ -323,7 +323,7 @@ __global__ __launch_bounds__(1024) void spmm_wave_position(
                                          (uint32_t)rows + 1u,
                                          (int32_t)(wend - 1));
   __shared__ int32_t window[1024 / kWave][kWave];
-  int32_t *win = window[threadIdx.x / kWave];
+  int32_t *win = window[wave_in_group()];
   const int span = last_row - first_row;
   const bool use_win = span < kWave;
   if (use_win) {
@@ -538,7 +538,7 @@ __global__ __launch_bounds__(64 * W) void spmm_tile_mfma(
   __shared__ float part[W][4][4][kWave]; // [wave][n tile][v][lane]
   const int r0 = blockIdx.x * 16;
   const int nt = std::min(16, rows - r0);
-  const int wave = threadIdx.x / kWave;
+  const int wave = wave_in_group();
   const int l = lane_id(), i = l & 15, g = l >> 4;
   // the row bounds are requested before the structure check waits; loads
   // are unconditional from clamped, valid addresses (a guarded load becomes
@@ -659,7 +659,7 @@ __global__ __launch_bounds__(64 * W) void spmm_tile_mfma_bf16(
   __shared__ float part[W][4][4][kWave]; // [wave][n tile][v][lane]
   const int r0 = blockIdx.x * 16;
   const int nt = std::min(16, rows - r0);
-  const int wave = threadIdx.x / kWave;
+  const int wave = wave_in_group();
   const int l = lane_id(), i = l & 15, g = l >> 4;
   const int last = r0 + nt - 1;
   const int32_t bl = ro[last];
@@ -768,7 +768,7 @@ __global__ __launch_bounds__(256) void spmm_row_tile_lds(
     int64_t tiles_per_row) {
   constexpr int PL = kWave / CL, U = kLdsTileSteps;
   __shared__ v4f stage[4][U][kWave];
-  const int wave = threadIdx.x / kWave, l = lane_id();
+  const int wave = wave_in_group(), l = lane_id();
   const int64_t unit = (int64_t)blockIdx.x * 4 + wave;
   if (unit >= rows * tiles_per_row)
     return; // wave-uniform; the kernel has no workgroup barrier
@@ -838,7 +838,7 @@ __global__ __launch_bounds__(256) void spmm_row_owner(
     int64_t chunk, int64_t chunks, int64_t tiles) {
   constexpr int PL = kWave / CL;
   const int64_t wave =
-      (int64_t)blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+      (int64_t)blockIdx.x * (blockDim.x / kWave) + wave_in_group();
   if (wave >= chunks * tiles)
     return;
   const int64_t c = wave / tiles;

@@ -310,7 +310,7 @@ __global__ __launch_bounds__(1024) void spmv_wave_position(
     int64_t wave_count) {
   const int lane = lane_id();
   const int64_t wave =
-      (int64_t)blockIdx.x * (blockDim.x / kWave) + (threadIdx.x / kWave);
+      (int64_t)blockIdx.x * (blockDim.x / kWave) + wave_in_group();
   const uint64_t base = (uint64_t)units / (uint64_t)wave_count;
   const uint64_t rem = (uint64_t)units % (uint64_t)wave_count;
   const uint64_t wv = (uint64_t)wave;
@@ -384,7 +384,7 @@ __global__ __launch_bounds__(1024) void spmv_wave_position(
   // coalesced load per wave) serve the lanes' row lookups whenever the wave
   // spans at most 64 rows; otherwise lanes search the row offsets directly.
   __shared__ int32_t window[1024 / kWave][kWave];
-  int32_t *win = window[threadIdx.x / kWave];
+  int32_t *win = window[wave_in_group()];
   const int span = last_row - first_row; // wave-uniform
   const bool use_win = span < kWave;
   if (use_win) {
