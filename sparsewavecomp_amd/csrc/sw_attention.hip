@@ -631,12 +631,17 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused(
     if (threadIdx.x == 0)
       v_nonfinite = 0;
     int32_t x[2][8], yl[8];
+    // unconditional loads from clamped, valid positions (nnz > 0): a row's
+    // first position as the wave-uniform base (scalar registers) and the
+    // clamped entry index as a 32-bit lane offset (4 nnz fits 32 bits)
+    auto row_entry = [&](int32_t b, int32_t len, int32_t t)
+        __attribute__((always_inline)) {
+      const int32_t *rb = col + (len > 0 ? b : 0);
+      return *at_bytes(rb, 4u * (uint32_t)std::min(t, std::max(len - 1, 0)));
+    };
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int32_t t = l + u * kWave;
-      // unconditional loads from clamped, valid positions (nnz > 0)
-      yl[u] = col[len_last > 0 ? bl + std::min(t, len_last - 1) : 0];
-    }
+    for (int u = 0; u < 8; ++u)
+      yl[u] = row_entry(bl, len_last, l + u * kWave);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int rr = wave + h * W;
@@ -644,10 +649,8 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused(
       const int32_t b = __builtin_amdgcn_readlane(my_ro, rc);
       const int32_t len = __builtin_amdgcn_readlane(my_ro, rc + 1) - b;
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int32_t t = l + u * kWave;
-        x[h][u] = col[len > 0 ? b + std::min(t, len - 1) : 0];
-      }
+      for (int u = 0; u < 8; ++u)
+        x[h][u] = row_entry(b, len, l + u * kWave);
     }
     // without branches: a compare inside a branch would pull its loads
     // into the branch
