@@ -62,7 +62,7 @@ def parse():
     ap.add_argument("--profile", default="",
                     choices=["", "spmv", "floor", "coo", "spmm", "bsr",
                              "bsr-bf16", "bsr-bf16-f32out", "attention",
-                             "attention-bf16", "copy"],
+                             "attention-bf16", "copy", "reference-sweep"],
                     help="run one workload --steps times with no timing or "
                          "JSON (for rocprofv3 kernel-trace / pmc runs)")
     ap.add_argument("--opts", default="",
@@ -70,6 +70,14 @@ def parse():
                          "headline mapping of that workload)")
     ap.add_argument("--k", type=int, default=4,
                     help="rhs columns for --profile spmm")
+    ap.add_argument("--workload", default="uniform/32",
+                    help="for --profile reference-sweep: DISTRIBUTION/"
+                         "NNZ_PER_ROW of the reference harness's synthetic "
+                         "65,536-row matrices (uniform, alternating, skewed)")
+    ap.add_argument("--summarize-reference-sweep", default="",
+                    metavar="DIR",
+                    help="print the reference-sweep table from the rocprofv3 "
+                         "kernel traces under DIR/<distribution>-<nnz>/")
     ap.add_argument("--x-entries", type=int, default=0,
                     help="for --profile spmv / floor: redraw configuration "
                          "2's columns uniformly over an x of this many "
@@ -87,6 +95,38 @@ COPY_BYTES = 256 << 20
 # untimed warm-up of the secondary workloads (SpMM, BSR, attention), on top
 # of --warmup; the headline SpMV keeps exactly --warmup steps
 WARM_MS = 100.0
+
+# The reference harness's SpMV mapping sweep (benchmark/run_spmv_benchmark.py,
+# docs/benchmarks/spmv-mapping-sweep-gfx1101.md:85-102): 65,536 x 65,536
+# synthetic matrices, a vector of ones, each mapping at block sizes 64-512,
+# rocSPARSE's default CSR SpMV as the baseline, 10 warm-up and 50 measured
+# dispatches, medians of kernel timestamps.
+REFERENCE_SWEEP_WORKLOADS = (("uniform", 4), ("uniform", 32),
+                             ("uniform", 256), ("skewed", 4),
+                             ("skewed", 32), ("skewed", 256))
+REFERENCE_SWEEP_CASES = (
+    tuple(f"spmv-mapping={m} spmv-block-size={b}"
+          for m in ("thread-per-row", "wave-per-row", "block-per-row")
+          for b in (64, 128, 256, 512))
+    # this build's Wave64 options beside the reference's: lane groups of
+    # 4-16 per row, the position mapping
+    + tuple(f"spmv-mapping=wave-per-row spmv-lanes-per-row={g} "
+            f"spmv-block-size={b}" for g in (4, 8, 16) for b in (64, 256))
+    + (HEADLINE_SPMV,
+       "spmv-mapping=wave-per-position spmv-positions-per-lane=4 "
+       "spmv-block-size=256",
+       "rocsparse default"))
+REFERENCE_SWEEP_WARMUP, REFERENCE_SWEEP_MEASURED = 10, 50
+# the reference's published gfx1101 rows (RX 7800 XT, Wave32): rocSPARSE
+# median, best SparseWave configuration and its median, in us
+REFERENCE_SWEEP_PUBLISHED = {
+    ("uniform", 4): (38.72, "thread-per-row, block 64", 20.52),
+    ("uniform", 32): (89.96, "wave-per-row, block 512", 74.40),
+    ("uniform", 256): (261.70, "block-per-row, block 64", 256.18),
+    ("skewed", 4): (23.44, "thread-per-row, block 128", 24.18),
+    ("skewed", 32): (132.28, "wave-per-row, block 64", 60.52),
+    ("skewed", 256): (322.94, "block-per-row, block 64", 304.04),
+}
 
 
 def profile(args):
@@ -158,6 +198,38 @@ def profile(args):
         o = sw.Options.parse(args.opts)
         for _ in range(n):
             sw.bsr_spmm(*a4, out, 16, options=o)
+    elif w == "reference-sweep":
+        dist, per_row = args.workload.split("/")
+        csr = W.reference_sweep_matrix(dist, int(per_row))
+        ro, col, val = (T(csr.row_offsets), T(csr.column_indices),
+                        T(csr.values))
+        xv = torch.ones(csr.cols, device=dev)
+        y = torch.empty(csr.rows, device=dev)
+        runs = []
+        for case in REFERENCE_SWEEP_CASES:
+            if case.startswith("rocsparse"):
+                # its buffer and analysis stages run here, before the trace
+                # segments begin
+                from sparsewavecomp_amd.rocsparse_runner import RocSparse
+                runs.append(RocSparse().spmv(ro, col, val, xv, y,
+                                             alg="default"))
+            else:
+                o = sw.Options.parse(case)
+                runs.append((lambda o: lambda: sw.spmv(
+                    ro, col, val, xv, y, options=o))(o))
+        # a gather-floor launch on 8 entries, which no case uses, marks
+        # where each case's dispatches begin and end in the kernel trace
+        sc, sv, sx = (torch.zeros(8, dtype=torch.int32, device=dev),
+                      torch.ones(8, device=dev), torch.ones(1, device=dev))
+        sp = torch.empty(1, device=dev)
+        mark = lambda: sw.spmv_gather_floor(sc, sv, sx, sp)
+        steps = REFERENCE_SWEEP_WARMUP + REFERENCE_SWEEP_MEASURED
+        torch.cuda.synchronize()
+        for run in runs:
+            mark()
+            for _ in range(steps):
+                run()
+        mark()
     elif w in ("attention", "attention-bf16"):
         mask, q, kt, v, alpha = W.config5(seed=0)
         dt = torch.bfloat16 if w == "attention-bf16" else torch.float32
@@ -174,6 +246,66 @@ def profile(args):
             sw.sparse_attention(*att, s, rm, rs, out, alpha, 0.0, options=o)
     torch.cuda.synchronize()
     log(f"profile {w} done")
+
+
+def summarize_reference_sweep(root):
+    """The reference-sweep table from `--profile reference-sweep` kernel
+    traces (one rocprofv3 run per workload under root/<dist>-<nnz>/): each
+    case's dispatches lie between two gather-floor marks; a call's time is the sum
+    of its kernels' durations (init + compute for position mappings, as the
+    reference counts them; every kernel of rocSPARSE's call); medians of the
+    measured calls."""
+    import csv
+    import glob
+    import statistics
+    lines = ["| distribution | NNZ/row | rocSPARSE us | best configuration "
+             "| us | vs rocSPARSE | reference (gfx1101): rocSPARSE us, best, "
+             "us, vs rocSPARSE |",
+             "|---|---:|---:|---|---:|---:|---|"]
+    detail = []
+    for dist, per_row in REFERENCE_SWEEP_WORKLOADS:
+        files = glob.glob(os.path.join(root, f"{dist}-{per_row}", "**",
+                                       "*kernel_trace.csv"), recursive=True)
+        if not files:
+            continue
+        with open(files[0]) as f:
+            rows = sorted(csv.DictReader(f),
+                          key=lambda r: int(r["Start_Timestamp"]))
+        cases, cur = [], None
+        for r in rows:
+            if "spmv_gather_floor" in r["Kernel_Name"]:
+                if cur is not None:
+                    cases.append(cur)
+                cur = []
+            elif cur is not None:
+                cur.append((int(r["End_Timestamp"])
+                            - int(r["Start_Timestamp"])) / 1e3)
+        steps = REFERENCE_SWEEP_WARMUP + REFERENCE_SWEEP_MEASURED
+        if len(cases) != len(REFERENCE_SWEEP_CASES):
+            raise SystemExit(f"{files[0]}: {len(cases)} cases, expected "
+                             f"{len(REFERENCE_SWEEP_CASES)}")
+        med = {}
+        for case, d in zip(REFERENCE_SWEEP_CASES, cases):
+            if len(d) % steps:
+                raise SystemExit(f"{files[0]}: case '{case}' has {len(d)} "
+                                 f"kernels, not a multiple of {steps}")
+            per = len(d) // steps
+            calls = [sum(d[i * per:(i + 1) * per]) for i in range(steps)]
+            med[case] = statistics.median(calls[REFERENCE_SWEEP_WARMUP:])
+        roc = med["rocsparse default"]
+        best = min((c for c in med if not c.startswith("rocsparse")),
+                   key=med.get)
+        pr, pbest, pus = REFERENCE_SWEEP_PUBLISHED[(dist, per_row)]
+        name = best.replace("spmv-mapping=", "").replace(" spmv-", ", ")
+        lines.append(f"| {dist} | {per_row} | {roc:.2f} | {name} | "
+                     f"{med[best]:.2f} | {roc / med[best]:.2f}x | {pr:.2f}, "
+                     f"{pbest}, {pus:.2f}, {pr / pus:.2f}x |")
+        detail.append(f"{dist}/{per_row}: " + "; ".join(
+            f"{c.replace('spmv-mapping=', '')} {v:.2f}"
+            for c, v in med.items()))
+    print("\n".join(lines))
+    print()
+    print("\n".join(detail))
 
 
 def traffic_from_profile(mapping):
@@ -230,6 +362,9 @@ def main():
         print(json.dumps({"error": "this build measures one GPU; every GPU "
                           "box has one MI355X, so --gpus must be 1"}))
         sys.exit(2)
+    if args.summarize_reference_sweep:
+        summarize_reference_sweep(args.summarize_reference_sweep)
+        return
     if args.profile:
         profile(args)
         return

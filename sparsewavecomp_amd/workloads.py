@@ -18,7 +18,10 @@ distributions follow the configuration list of the benchmark contract:
 
 Distinct sorted columns are drawn as ``sort(u_i) + i`` with
 ``u_i ~ U{0, .., m-k}``: a strictly increasing k-subset of ``[0, m)``.  This
-is the synthetic-workload layer only; nothing here is the reference's code.
+is the synthetic-workload layer only.  One generator follows the reference:
+``reference_sweep_matrix`` restates the formulas of the reference harness's
+synthetic SpMV inputs, so that its published mapping sweep can be rerun on
+the same shapes.
 """
 from __future__ import annotations
 
@@ -207,6 +210,30 @@ def config5(seed: int = 0, seq: int = 8192, d: int = 64):
     v = rng.standard_normal(size=(seq, d), dtype=np.float32)
     kt = np.ascontiguousarray(k.T)
     return mask, q, kt, v, 1.0 / math.sqrt(d)
+
+
+def reference_sweep_matrix(distribution: str, nnz_per_row: int,
+                           rows: int = 65536, cols: int = 65536) -> CSR:
+    """The reference harness's synthetic SpMV input, restated
+    (benchmark/run_spmv_benchmark.py:225-259): row lengths ``uniform`` (every
+    row nnz_per_row), ``alternating`` (1 and 2 nnz_per_row - 1) or
+    ``skewed`` (seven of every eight rows 1, the eighth 8 nnz_per_row - 7);
+    the column of position p is p mod cols and every value is 1.0.  The
+    harness multiplies it by a vector of ones (benchmark/spmv.mlir.in)."""
+    r = np.arange(rows, dtype=np.int64)
+    if distribution == "uniform":
+        lengths = np.full(rows, nnz_per_row, dtype=np.int64)
+    elif distribution == "alternating":
+        lengths = np.where(r % 2 == 0, 1, 2 * nnz_per_row - 1)
+    elif distribution == "skewed":
+        lengths = np.where(r % 8 == 7, 8 * nnz_per_row - 7, 1)
+    else:
+        raise ValueError(f"unknown distribution: {distribution}")
+    ro = np.zeros(rows + 1, dtype=np.int32)
+    np.cumsum(lengths, out=ro[1:])
+    nnz = int(ro[-1])
+    col = (np.arange(nnz, dtype=np.int64) % cols).astype(np.int32)
+    return CSR(rows, cols, ro, col, np.ones(nnz, dtype=np.float32))
 
 
 def random_csr(rows: int, cols: int, mean_len: float, seed: int,
