@@ -114,11 +114,28 @@ REFERENCE_SWEEP_CASES = (
             f"spmv-block-size={b}" for g in (4, 8, 16) for b in (64, 256))
     + (HEADLINE_SPMV,
        "spmv-mapping=wave-per-position spmv-positions-per-lane=4 "
-       "spmv-block-size=256",
-       "rocsparse default"))
+       "spmv-block-size=256")
+    # the reference's position schedules (one position per lane, one atomic
+    # per position for thread-per-position; its position-mapping report,
+    # docs/benchmarks/spmv-position-mapping-gfx1101.md:49-80)
+    + tuple(f"spmv-mapping={m} spmv-block-size={b}"
+            for m in ("wave-per-position", "thread-per-position")
+            for b in (64, 128, 256, 512))
+    + ("rocsparse default",))
 REFERENCE_SWEEP_WARMUP, REFERENCE_SWEEP_MEASURED = 10, 50
 # the reference's published gfx1101 rows (RX 7800 XT, Wave32): rocSPARSE
 # median, best SparseWave configuration and its median, in us
+# the reference's position-mapping report (same matrices, its own rocSPARSE
+# run): rocSPARSE median, then (block, median) of wave-per-position and of
+# thread-per-position, in us
+REFERENCE_POSITION_PUBLISHED = {
+    ("uniform", 4): (35.56, (512, 87.81), (512, 105.33)),
+    ("uniform", 32): (35.98, (128, 203.41), (128, 2324.79)),
+    ("uniform", 256): (259.75, (64, 1999.76), (64, 123129.33)),
+    ("skewed", 4): (48.72, (64, 33.08), (512, 209.09)),
+    ("skewed", 32): (132.29, (64, 223.75), (64, 8555.90)),
+    ("skewed", 256): (321.31, (64, 5693.76), (64, 655741.72)),
+}
 REFERENCE_SWEEP_PUBLISHED = {
     ("uniform", 4): (38.72, "thread-per-row, block 64", 20.52),
     ("uniform", 32): (89.96, "wave-per-row, block 512", 74.40),
@@ -263,6 +280,11 @@ def summarize_reference_sweep(root):
              "us, vs rocSPARSE |",
              "|---|---:|---:|---|---:|---:|---|"]
     detail = []
+    pos = ["| distribution | NNZ/row | rocSPARSE us | wave-per-position: "
+           "options, us, vs rocSPARSE | thread-per-position: options, us, vs "
+           "rocSPARSE | reference (gfx1101): rocSPARSE us | its "
+           "wave-per-position | its thread-per-position |",
+           "|---|---:|---:|---|---|---:|---|---|"]
     for dist, per_row in REFERENCE_SWEEP_WORKLOADS:
         files = glob.glob(os.path.join(root, f"{dist}-{per_row}", "**",
                                        "*kernel_trace.csv"), recursive=True)
@@ -303,7 +325,22 @@ def summarize_reference_sweep(root):
         detail.append(f"{dist}/{per_row}: " + "; ".join(
             f"{c.replace('spmv-mapping=', '')} {v:.2f}"
             for c, v in med.items()))
+        # position mappings: the fastest of each kind
+        cells = []
+        for kind in ("wave-per-position", "thread-per-position"):
+            c = min((c for c in med if f"spmv-mapping={kind} " in c),
+                    key=med.get)
+            cells.append(f"{c.split(' ', 1)[1].replace('spmv-', '')}, "
+                         f"{med[c]:.2f}, {roc / med[c]:.2f}x")
+        rr, (wb, wus), (tb, tus) = REFERENCE_POSITION_PUBLISHED[(dist,
+                                                                 per_row)]
+        pos.append(f"| {dist} | {per_row} | {roc:.2f} | {cells[0]} | "
+                   f"{cells[1]} | {rr:.2f} | block {wb}, {wus:.2f}, "
+                   f"{rr / wus:.2f}x | block {tb}, {tus:.2f}, "
+                   f"{rr / tus:.2f}x |")
     print("\n".join(lines))
+    print()
+    print("\n".join(pos))
     print()
     print("\n".join(detail))
 

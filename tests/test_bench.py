@@ -90,11 +90,16 @@ def test_reference_sweep_summary_from_a_kernel_trace(tmp_path, capsys):
     bench.summarize_reference_sweep(str(tmp_path))
     out = capsys.readouterr().out
     line = [l for l in out.splitlines() if l.startswith("| uniform | 32 |")]
-    assert len(line) == 1
+    assert len(line) == 2  # the mapping table and the position table
     cells = [c.strip() for c in line[0].split("|")]
-    # rocSPARSE 32 us per call; the best case is the position mapping at
+    # rocSPARSE 32 us per call; the best case is a wave-per-position case at
     # 1 + 9 us; 3.20x
     assert cells[3] == "32.00" and "wave-per-position" in cells[4]
     assert cells[5] == "10.00" and cells[6] == "3.20x"
+    # thread-per-position at block 64 is case 24 of the list: 44 us
+    pcells = [c.strip() for c in line[1].split("|")]
+    assert pcells[4].endswith("10.00, 3.20x")
+    assert pcells[5] == "block-size=64, 44.00, 0.73x"
+    assert pcells[6] == "35.98"
     assert "thread-per-row spmv-block-size=64 20.00" in out.replace(
         ", spmv-", " spmv-")
