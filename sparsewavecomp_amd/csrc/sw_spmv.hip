@@ -233,20 +233,47 @@ __global__ __launch_bounds__(256) void position_init(
 }
 
 // ---------------------------------------------------------------------------
+// The rows of a wave's positions: the wave's first and last positions'
+// rows found by wave-uniform searches (scalar loads), so that each lane then
+// searches only between them -- the same row as a search over all row
+// offsets, with a few loads per lane instead of one per halving of rows.
+struct WaveRows {
+  uint32_t lo, hi; // lane searches run over ro[lo .. hi)
+};
+__device__ __forceinline__ WaveRows wave_rows(const int32_t *__restrict__ ro,
+                                              int32_t rows, int64_t nnz,
+                                              int64_t chunk) {
+  const int64_t first = ((int64_t)blockIdx.x * blockDim.x +
+                         (int64_t)wave_in_group() * kWave) *
+                        chunk;
+  const int64_t last = std::min(first + (int64_t)kWave * chunk, nnz) - 1;
+  const int fr = row_search_uniform(ro, 1u, (uint32_t)rows + 1u,
+                                    (int32_t)first);
+  const int lr = row_search_gallop(ro, (uint32_t)fr + 1u, (uint32_t)rows + 1u,
+                                   (int32_t)last);
+  return WaveRows{(uint32_t)fr + 1u, (uint32_t)lr + 2u};
+}
+
 // thread-per-position, atomic: worker w handles positions
 // [w*chunk, min((w+1)*chunk, nnz)), recovers each position's row by the row
 // search and adds val*x atomically (SparsePositionScheduling.cpp:135-194).
+// The search runs inside the wave's row range (configuration 2: 2934 ->
+// 2628 us; the atomic add per position is the rest).
 __global__ __launch_bounds__(1024) void spmv_thread_position_atomic(
     const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
     const float *__restrict__ val, const float *__restrict__ x,
     float *__restrict__ y, int32_t rows, int32_t nnz, int32_t chunk) {
-  int64_t w = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  int64_t b = w * chunk;
+  const int64_t w = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t b = w * chunk;
+  if ((((int64_t)blockIdx.x * blockDim.x + (int64_t)wave_in_group() * kWave) *
+       chunk) >= nnz)
+    return; // wave-uniform: the whole wave is past the positions
+  const WaveRows wr = wave_rows(ro, rows, nnz, chunk);
   if (b >= nnz)
     return;
-  int64_t e = b + chunk < nnz ? b + chunk : nnz;
+  const int64_t e = b + chunk < nnz ? b + chunk : nnz;
   for (int64_t p = b; p < e; ++p) {
-    int r = row_search_lane(ro, 1u, (uint32_t)rows + 1u, (int32_t)p);
+    const int r = row_search_lane(ro, wr.lo, wr.hi, (int32_t)p);
     unsafeAtomicAdd(y + r, val[p] * x[col[p]]);
   }
 }
@@ -259,6 +286,8 @@ __global__ __launch_bounds__(1024) void spmv_thread_position_segmented(
     const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
     const float *__restrict__ val, const float *__restrict__ x,
     float *__restrict__ y, int32_t rows, int32_t nnz, int32_t chunk) {
+  // (the chunk's own search over all row offsets: the wave-range form of
+  // the atomic kernel measured 562 -> 596 us here, configuration 2, chunk 8)
   int64_t w = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   int64_t b = w * chunk;
   if (b >= nnz)

@@ -27,6 +27,11 @@ MAPPINGS = [
     "spmv-mapping=thread-per-position spmv-position-chunk-size=4",
     "spmv-mapping=thread-per-position spmv-position-chunk-size=7 "
     "spmv-position-reduction=segmented",
+    # partial waves: a wave's row search covers a wider range than its lanes
+    "spmv-mapping=thread-per-position spmv-block-size=100 "
+    "spmv-position-chunk-size=3",
+    "spmv-mapping=thread-per-position spmv-block-size=96 "
+    "spmv-position-chunk-size=5 spmv-position-reduction=segmented",
     "spmv-mapping=wave-per-position",
     "spmv-mapping=wave-per-position spmv-block-size=64",
     "spmv-mapping=wave-per-position spmv-positions-per-lane=2",
