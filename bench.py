@@ -266,12 +266,12 @@ def profile(args):
 
 
 def summarize_reference_sweep(root):
-    """The reference-sweep table from `--profile reference-sweep` kernel
+    """The reference-sweep tables from `--profile reference-sweep` kernel
     traces (one rocprofv3 run per workload under root/<dist>-<nnz>/): each
-    case's dispatches lie between two gather-floor marks; a call's time is the sum
-    of its kernels' durations (init + compute for position mappings, as the
-    reference counts them; every kernel of rocSPARSE's call); medians of the
-    measured calls."""
+    case's dispatches lie between two gather-floor marks; a call's time is
+    the sum of its kernels' durations (init + compute for position mappings,
+    as the reference counts them; every kernel of rocSPARSE's call); medians
+    of the measured calls."""
     import csv
     import glob
     import statistics
