@@ -387,31 +387,4 @@ __device__ __forceinline__ bool tile_prefix_ok_block(
 }
 
 
-// Wave-cooperative 64-ary search for a wave-uniform position: every round
-// each lane probes one offset and a ballot narrows the range 64-fold, so a
-// 1M-row matrix needs four dependent loads instead of twenty.
-__device__ __forceinline__ int row_search_wave(const int32_t *__restrict__ ro,
-                                               uint32_t lo, uint32_t hi,
-                                               int32_t pos) {
-  const uint32_t lane = (uint32_t)lane_id();
-  while (hi - lo > (uint32_t)kWave) {
-    uint32_t step = (hi - lo + kWave - 1) / kWave;
-    uint32_t idx = lo + lane * step;
-    bool pred = idx < hi && ro[idx] <= pos;
-    uint32_t cnt = (uint32_t)__builtin_popcountll(ballot(pred));
-    uint32_t base = lo;
-    if (cnt > 0)
-      lo = base + (cnt - 1) * step + 1;
-    uint32_t cap = base + cnt * step;
-    if (cap < hi)
-      hi = cap;
-    lo = __builtin_amdgcn_readfirstlane(lo);
-    hi = __builtin_amdgcn_readfirstlane(hi);
-  }
-  uint32_t idx = lo + lane;
-  bool pred = idx < hi && ro[idx] <= pos;
-  uint32_t cnt = (uint32_t)__builtin_popcountll(ballot(pred));
-  return (int)(lo + cnt) - 1;
-}
-
 } // namespace swd
