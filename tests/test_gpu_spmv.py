@@ -315,3 +315,27 @@ def test_repeat_is_stable(dev, orc):
             "spmv-mapping=wave-per-position spmv-positions-per-lane=8"))
     torch.cuda.synchronize()
     _check(orc, csr, x, y.cpu().numpy())
+
+
+@pytest.mark.parametrize("workload", ["uniform/4", "uniform/32", "uniform/256",
+                                      "alternating/32", "skewed/4",
+                                      "skewed/32", "skewed/256"])
+def test_reference_sweep_matrices(dev, workload):
+    """The reference harness's synthetic sweep matrices (65,536 rows; the
+    column of position p is p mod 65,536, so a row's columns wrap past the
+    last column; values 1) times its vector of ones: every output is exactly
+    the row's length in fp32, for every mapping."""
+    dist, per_row = workload.split("/")
+    csr = W.reference_sweep_matrix(dist, int(per_row))
+    want = np.diff(csr.row_offsets).astype(np.float32)
+    ro, col, val = (G.t(csr.row_offsets), G.t(csr.column_indices),
+                    G.t(csr.values))
+    xv = torch.ones(csr.cols, device=G.DEV)
+    y = torch.empty(csr.rows, device=G.DEV)
+    for opts in MAPPINGS + ["spmv-mapping=wave-per-row spmv-lanes-per-row=4 "
+                            "spmv-block-size=256"]:
+        G.say(f"reference sweep {workload} opts='{opts}'")
+        y.fill_(float("nan"))
+        sw.spmv(ro, col, val, xv, y, options=opts)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(y.cpu().numpy(), want, err_msg=opts)
