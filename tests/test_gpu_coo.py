@@ -145,3 +145,18 @@ def test_errors(dev):
     with pytest.raises(sw.SparseWaveError, match="positions-per-lane"):
         sw.coo_spmv(z, z, v, v, v, options="spmv-mapping=wave-per-position "
                                            "spmv-positions-per-lane=3")
+
+
+@pytest.mark.parametrize("workload", ["uniform/32", "skewed/4", "skewed/256"])
+def test_reference_sweep_matrices(dev, workload):
+    """The reference harness's sweep matrices as COO (its --formats=coo runs
+    the same entries) times a vector of ones: every output is exactly the
+    row's length in fp32, for every mapping."""
+    dist, per_row = workload.split("/")
+    csr = W.reference_sweep_matrix(dist, int(per_row))
+    ri, ci, val = _coo(csr)
+    want = np.diff(csr.row_offsets).astype(np.float32)
+    x = np.ones(csr.cols, np.float32)
+    for opts in MAPPINGS:
+        np.testing.assert_array_equal(_run(csr.rows, ri, ci, val, x, opts),
+                                      want, err_msg=opts)
