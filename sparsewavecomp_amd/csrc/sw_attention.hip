@@ -562,15 +562,20 @@ constexpr int kFusedChunks = kFusedCols / (16 * kFusedWaves);
 // output column 4j + n of the block -- so that one 128-bit load of a V row
 // gives a lane its values for all four tiles, and one 128-bit store writes
 // four outputs of a row.
+// SO (SDDMM only): the kernel serves the sddmm op on its own -- mask is the
+// op's sample values, q its lhs, kt its rhs, scores its output, and `kind`
+// its region; the tile stores its scores and ends (value, rmax, rsum, out
+// and dv are unused).  The attention chain takes the affine region.
 // (at most 128 VGPRs: the two workgroups of a CU need four waves per SIMD)
-template <int KB, int W, bool IL>
+template <int KB, int W, bool IL, bool SO>
 __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused(
     const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
     const float *__restrict__ mask, const float *__restrict__ q,
     const float *__restrict__ kt, const float *__restrict__ value,
     float *scores, float *__restrict__ rmax, float *__restrict__ rsum,
     float *__restrict__ out, int32_t rows, int64_t cols, int32_t kdim,
-    int64_t dv, float alpha, float beta, uint32_t amax) {
+    int64_t dv, float alpha, float beta, uint32_t amax, int kind) {
+  const int region = SO ? kind : SW_SDDMM_AFFINE;
   static_assert(W == 8 && kFusedCols == 8 * kWave && kFusedChunks == 4,
                 "check layout");
   __shared__ float part[W][4][4][kWave]; // [wave][n tile][v][lane]
@@ -684,12 +689,14 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused(
   }
   if (!ok) { // workgroup-uniform
     for (int r = r0 + wave; r < r0 + nt; r += W) {
-      sddmm_row_wave(ro, col, mask, q, kt, scores, r, cols, kdim,
-                     SW_SDDMM_AFFINE, alpha, beta);
-      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
-      attention_row_softmax(ro, scores, rmax, rsum, r);
-      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
-      attention_row_output(ro, col, scores, value, out, r, dv);
+      sddmm_row_wave(ro, col, mask, q, kt, scores, r, cols, kdim, region,
+                     alpha, beta);
+      if constexpr (!SO) {
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+        attention_row_softmax(ro, scores, rmax, rsum, r);
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+        attention_row_output(ro, col, scores, value, out, r, dv);
+      }
     }
     return;
   }
@@ -764,8 +771,8 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused(
                    d == 0 ? w.y : d == 1 ? w.z : w.w, d == 0 ? w.z : w.w, w.w};
 #pragma unroll
     for (int v = 0; v < 4; ++v)
-      sv[k][v] = combine_sddmm(SW_SDDMM_AFFINE, valid(k, v) ? x[v] : 0.0f,
-                               acc[v], alpha, beta);
+      sv[k][v] = combine_sddmm(region, valid(k, v) ? x[v] : 0.0f, acc[v],
+                               alpha, beta);
   };
   float bv[kFusedChunks][4][4];
   // two chunks' K^T gathers and mask windows per batch; a chunk past the
@@ -800,6 +807,27 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused(
       for (int v = 0; v < 4; ++v)
         sv[k0 + 1][v] = 0.0f;
     }
+  }
+  if constexpr (SO) {
+    // the scores of entries t0(k) + 4g .. + 3 of row i: one (unaligned)
+    // vector store when all four are the row's, else the row's ones one by
+    // one
+#pragma unroll
+    for (int k = 0; k < kFusedChunks; ++k) {
+      if (chunk_t0(k) >= len_last) // wave-uniform
+        continue;
+      float *dst = scores + rbase + chunk_t0(k) + 4 * g;
+      if (valid(k, 3)) {
+        const v4f x = v4f{sv[k][0], sv[k][1], sv[k][2], sv[k][3]};
+        __builtin_memcpy(dst, &x, sizeof x);
+      } else {
+#pragma unroll
+        for (int v = 0; v < 3; ++v)
+          if (valid(k, v))
+            dst[v] = sv[k][v];
+      }
+    }
+    return;
   }
   // in flight over the softmax (the V rows of chunks 2-3 are loaded after
   // it: holding all four chunks' rows over it would take more registers
@@ -1479,6 +1507,25 @@ int launch_sddmm(const int32_t *ro, const int32_t *col, const T *val,
       int rc = grid_for(rows, 16, "SDDMM", &grid);
       if (rc)
         return rc;
+      // d of 64 or 128 with sample values, 32-bit offsets and an output
+      // apart from the samples: the fused attention kernel's product phase
+      // (its 4-entry sample windows may reach a neighbouring lane's entries)
+      if ((kdim == 64 || kdim == 128) && val != nullptr && nnz >= 4 &&
+          narrow_offsets(nnz, 1) && narrow_offsets(cols, kdim) &&
+          (out + nnz <= val || val + nnz <= out)) {
+#define SW_SDDMM_FUSED(KB)                                                    \
+  hipLaunchKernelGGL((attention_tile_fused<KB, kFusedWaves, false, true>),    \
+                     dim3((unsigned)grid), dim3(64 * kFusedWaves), 0, st, ro, \
+                     col, val, lhs, rhs, nullptr, out, nullptr, nullptr,      \
+                     nullptr, (int32_t)rows, cols, (int32_t)kdim, (int64_t)0, \
+                     alpha, beta, (uint32_t)(nnz - 4), kind)
+        if (kb == 1)
+          SW_SDDMM_FUSED(1);
+        else
+          SW_SDDMM_FUSED(2);
+#undef SW_SDDMM_FUSED
+        return launch_check("SDDMM tile MFMA kernel");
+      }
 #define SW_SDDMM_TILE(KB)                                                     \
   hipLaunchKernelGGL((sddmm_tile_mfma<KB, kSddmmTileWaves>),                  \
                      dim3((unsigned)grid), dim3(64 * kSddmmTileWaves), 0, st, \
@@ -1691,11 +1738,11 @@ bool launch_fused_attention(const int32_t *ro, const int32_t *col,
   // interleaved output tiles (configuration 5: 25.2 -> 24.0 us)
   const bool il = dv % 64 == 0 && aligned16(v) && aligned16(out);
 #define SW_FUSED(KB, IL)                                                      \
-  hipLaunchKernelGGL((attention_tile_fused<KB, kFusedWaves, IL>),             \
+  hipLaunchKernelGGL((attention_tile_fused<KB, kFusedWaves, IL, false>),      \
                      dim3((unsigned)grid), dim3(64 * kFusedWaves), 0, st, ro, \
                      col, mask, q, kt, v, scores, rmax, rsum, out,            \
                      (int32_t)rows, cols, (int32_t)d, dv, alpha, beta,        \
-                     (uint32_t)(nnz - 4))
+                     (uint32_t)(nnz - 4), (int)SW_SDDMM_AFFINE)
   if (d == 64 && il)
     SW_FUSED(1, true);
   else if (d == 64)

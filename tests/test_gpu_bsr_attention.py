@@ -247,15 +247,17 @@ def _tile_structure_csr():
     return W.CSR(len(rows_cols), cols, ro, col, val)
 
 
-@pytest.mark.parametrize("kind", ["mul", "affine"])
-def test_sddmm_tile_structure_paths(dev, orc, kind):
+@pytest.mark.parametrize("kdim", [64, 128])
+@pytest.mark.parametrize("kind", ["mul", "affine", "dot"])
+def test_sddmm_tile_structure_paths(dev, orc, kind, kdim):
     csr = _tile_structure_csr()
     rng = np.random.default_rng(5)
-    lhs = rng.standard_normal((csr.rows, 64)).astype(np.float32)
-    rhs = rng.standard_normal((64, csr.cols)).astype(np.float32)
-    k = sw.SDDMM_MUL if kind == "mul" else sw.SDDMM_AFFINE
+    lhs = rng.standard_normal((csr.rows, kdim)).astype(np.float32)
+    rhs = rng.standard_normal((kdim, csr.cols)).astype(np.float32)
+    k = {"mul": sw.SDDMM_MUL, "affine": sw.SDDMM_AFFINE,
+         "dot": sw.SDDMM_DOT}[kind]
     out = torch.full((csr.nnz,), float("nan"), device=G.DEV)
-    G.say(f"sddmm tile structure paths kind={kind}")
+    G.say(f"sddmm tile structure paths kind={kind} kdim={kdim}")
     sw.sddmm(G.t(csr.row_offsets), G.t(csr.column_indices), G.t(csr.values),
              G.t(lhs), G.t(rhs), out, k, 0.3, 0.7,
              options="sddmm-mapping=row-tile-mfma")
@@ -266,7 +268,7 @@ def test_sddmm_tile_structure_paths(dev, orc, kind):
     b = (np.abs(lhs.astype(np.float64)) @ np.abs(rhs.astype(np.float64)))[
         rows, csr.column_indices]
     v = np.abs(csr.values.astype(np.float64))
-    bound = v * b if kind == "mul" else 0.7 * v + 0.3 * b
+    bound = {"mul": v * b, "affine": 0.7 * v + 0.3 * b, "dot": b}[kind]
     assert_within_bound(out.cpu().numpy(), ref, bound + 1e-30)
 
 
@@ -668,18 +670,22 @@ def _check_attention(orc, csr, scores, rmax, rsum, out, refs, v):
     np.testing.assert_allclose(rsum.cpu().numpy(), sum_ref, rtol=1e-4)
 
 
+@pytest.mark.parametrize("in_place", [False, True])
 @pytest.mark.parametrize("kdim", [64, 128, 32])
-def test_sddmm_tile_mfma_block_mask(dev, orc, kdim):
-    """Block-structured masks take the 16-row MFMA tiles."""
+def test_sddmm_tile_mfma_block_mask(dev, orc, kdim, in_place):
+    """Block-structured masks take the 16-row MFMA tiles; with the output in
+    place of the sample values the tiles read each entry's sample before
+    writing it."""
     mask = W.attention_mask(seq=2048, block=64, window=4, random_blocks=2,
                             seed=3)
     rng = np.random.default_rng(kdim)
     lhs = rng.standard_normal((mask.rows, kdim)).astype(np.float32)
     rhs = rng.standard_normal((kdim, mask.cols)).astype(np.float32)
     vals = rng.uniform(-1, 1, mask.nnz).astype(np.float32)
-    out = torch.empty(mask.nnz, device=G.DEV)
-    G.say(f"sddmm tile mfma kdim={kdim}")
-    sw.sddmm(G.t(mask.row_offsets), G.t(mask.column_indices), G.t(vals),
+    vt = G.t(vals)
+    out = vt if in_place else torch.empty(mask.nnz, device=G.DEV)
+    G.say(f"sddmm tile mfma kdim={kdim} in_place={in_place}")
+    sw.sddmm(G.t(mask.row_offsets), G.t(mask.column_indices), vt,
              G.t(lhs), G.t(rhs), out, sw.SDDMM_AFFINE, 0.125, 0.5,
              options="sddmm-mapping=row-tile-mfma")
     torch.cuda.synchronize()
