@@ -1134,17 +1134,20 @@ __global__ __launch_bounds__(64 * W) void sddmm_tile_mfma_bf16(
 // K^T (2 * d * cols) and V (2 * cols * dv) fit 32 bits, that nnz >= 4
 // (amax = nnz - 4) and that Q is 16-byte and V 8-byte aligned.
 // (at most 128 VGPRs: the two workgroups of a CU need four waves per SIMD)
-template <int KB, int W>
+template <int KB, int W, bool SO>
 __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused_bf16(
     const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
     const uint16_t *__restrict__ mask, const uint16_t *__restrict__ q,
     const uint16_t *__restrict__ kt, const uint16_t *__restrict__ value,
     uint16_t *scores, uint16_t *__restrict__ rmax, uint16_t *__restrict__ rsum,
     uint16_t *__restrict__ out, int32_t rows, int64_t cols, int32_t kdim,
-    int64_t dv, float alpha, float beta, uint32_t amax) {
+    int64_t dv, float alpha, float beta, uint32_t amax, int kind) {
   static_assert(W == 8 && kFusedCols == 8 * kWave && kFusedChunks == 4,
                 "check layout");
   constexpr int S = 2 * KB;
+  // SO: the SDDMM alone (combine kind `kind`), its scores stored from
+  // registers; no softmax and no P V
+  const int region = SO ? kind : SW_SDDMM_AFFINE;
   __shared__ float part[W][4][4][kWave]; // [wave][n tile][v][lane]
   __shared__ float wred[2][W][16];       // [max, sum][wave][row]
   __shared__ int wshared[W]; // each wave's rows share the last row's columns
@@ -1241,7 +1244,7 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused_bf16(
       const float x = valid(k, v) ? bf16_to_f32((uint16_t)(w >> (16 * v)))
                                   : 0.0f;
       sv[k][v] = as_stored<uint16_t>(
-          combine_sddmm(SW_SDDMM_AFFINE, x, acc[v], alpha, beta));
+          combine_sddmm(region, x, acc[v], alpha, beta));
     }
   };
   // two chunks' K^T gathers per batch; a chunk past the last row's entries
@@ -1319,31 +1322,34 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused_bf16(
     for (int k = 0; k < kFusedChunks; ++k)
       yk[k] = wave >= 4 ? yl[2 * k + 1] : yl[2 * k];
     batch(0);
-    if constexpr (KB == 1) { // in flight over the second batch and softmax
+    if constexpr (KB == 1 && !SO) { // in flight over the second batch and softmax
       load_v(0, 0, bv[0]);
       load_v(1, 0, bv[1]);
     }
     batch(2);
-    if constexpr (KB == 1) { // in flight over the softmax
+    if constexpr (SO) {
+    } else if constexpr (KB == 1) { // in flight over the softmax
       load_v(2, 0, bv[2]);
       load_v(3, 0, bv[3]);
     } else {
       load_v(0, 0, bv[0]);
       load_v(1, 0, bv[1]);
     }
-    // B. row softmax on the stored (bf16) scores, each op's result rounded:
-    // this wave's row maxima
-    float m = -INFINITY;
+    if constexpr (!SO) {
+      // B. row softmax on the stored (bf16) scores, each op's result
+      // rounded: this wave's row maxima
+      float m = -INFINITY;
 #pragma unroll
-    for (int k = 0; k < kFusedChunks; ++k)
+      for (int k = 0; k < kFusedChunks; ++k)
 #pragma unroll
-      for (int v = 0; v < 4; ++v)
-        if (valid(k, v))
-          m = maximumf(m, sv[k][v]);
-    m = maximumf(m, swizzle_xor16(m));
-    m = maximumf(m, shfl_xor32(m));
-    if (g == 0)
-      wred[0][wave][i] = m;
+        for (int v = 0; v < 4; ++v)
+          if (valid(k, v))
+            m = maximumf(m, sv[k][v]);
+      m = maximumf(m, swizzle_xor16(m));
+      m = maximumf(m, shfl_xor32(m));
+      if (g == 0)
+        wred[0][wave][i] = m;
+    }
   }
   __syncthreads();
   if (ok) {
@@ -1353,12 +1359,34 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused_bf16(
   }
   if (!ok) { // workgroup-uniform; nothing has been stored yet
     for (int r = r0 + wave; r < r0 + nt; r += W) {
-      sddmm_row_wave(ro, col, mask, q, kt, scores, r, cols, kdim,
-                     SW_SDDMM_AFFINE, alpha, beta);
-      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
-      attention_row_softmax(ro, scores, rmax, rsum, r);
-      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
-      attention_row_output(ro, col, scores, value, out, r, dv);
+      sddmm_row_wave(ro, col, mask, q, kt, scores, r, cols, kdim, region,
+                     alpha, beta);
+      if constexpr (!SO) {
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+        attention_row_softmax(ro, scores, rmax, rsum, r);
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+        attention_row_output(ro, col, scores, value, out, r, dv);
+      }
+    }
+    return;
+  }
+  if constexpr (SO) {
+    // the scores, already rounded to bf16, as pairs
+#pragma unroll
+    for (int k = 0; k < kFusedChunks; ++k) {
+      if (chunk_t0(k) < len_last) { // wave-uniform
+        const v2u pr = v2u{pack_bf16x2(sv[k][0], sv[k][1]),
+                           pack_bf16x2(sv[k][2], sv[k][3])};
+        uint16_t *dst = scores + rbase + chunk_t0(k) + 4 * g;
+        if (valid(k, 3)) {
+          __builtin_memcpy(dst, &pr, sizeof pr);
+        } else {
+#pragma unroll
+          for (int v = 0; v < 3; ++v)
+            if (valid(k, v))
+              dst[v] = (uint16_t)(pr[v >> 1] >> (16 * (v & 1)));
+        }
+      }
     }
     return;
   }
@@ -1546,6 +1574,23 @@ int launch_sddmm(const int32_t *ro, const int32_t *col, const T *val,
       int rc = grid_for(rows, 16, "SDDMM", &grid);
       if (rc)
         return rc;
+      // d of 64 or 128 with sample values and an output apart from them:
+      // the fused attention kernel's product phase, as for fp32
+      if ((kdim == 64 || kdim == 128) && val != nullptr && nnz >= 4 &&
+          (out + nnz <= val || val + nnz <= out)) {
+#define SW_SDDMM_FUSED(KB)                                                    \
+  hipLaunchKernelGGL((attention_tile_fused_bf16<KB, kFusedWaves, true>),      \
+                     dim3((unsigned)grid), dim3(64 * kFusedWaves), 0, st, ro, \
+                     col, val, lhs, rhs, nullptr, out, nullptr, nullptr,      \
+                     nullptr, (int32_t)rows, cols, (int32_t)kdim, (int64_t)0, \
+                     alpha, beta, (uint32_t)(nnz - 4), kind)
+        if (kb == 1)
+          SW_SDDMM_FUSED(1);
+        else
+          SW_SDDMM_FUSED(2);
+#undef SW_SDDMM_FUSED
+        return launch_check("SDDMM tile MFMA kernel");
+      }
 #define SW_SDDMM_TILE(KB)                                                     \
   hipLaunchKernelGGL((sddmm_tile_mfma_bf16<KB, kSddmmTileWaves>),             \
                      dim3((unsigned)grid), dim3(64 * kSddmmTileWaves), 0, st, \
@@ -1775,11 +1820,11 @@ bool launch_fused_attention(const int32_t *ro, const int32_t *col,
   if (*rc)
     return true;
 #define SW_FUSED(KB)                                                          \
-  hipLaunchKernelGGL((attention_tile_fused_bf16<KB, kFusedWaves>),            \
+  hipLaunchKernelGGL((attention_tile_fused_bf16<KB, kFusedWaves, false>),     \
                      dim3((unsigned)grid), dim3(64 * kFusedWaves), 0, st, ro, \
                      col, mask, q, kt, v, scores, rmax, rsum, out,            \
-                     (int32_t)rows, cols, (int32_t)d, dv, alpha, beta,     \
-                     (uint32_t)(nnz - 4))
+                     (int32_t)rows, cols, (int32_t)d, dv, alpha, beta,        \
+                     (uint32_t)(nnz - 4), (int)SW_SDDMM_AFFINE)
   if (d == 64)
     SW_FUSED(1);
   else

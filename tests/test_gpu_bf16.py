@@ -116,7 +116,7 @@ def test_bf16_sddmm(dev, orc, golden, opts):
 @pytest.mark.parametrize("shape", ["block", "structure"])
 def test_bf16_sddmm_tiles(dev, orc, kdim, shape):
     """The bf16 matrix-core SDDMM tiles on a block mask, and on tiles that
-    take its row-by-row fallback."""
+    take its row-by-row fallback, for each combine kind."""
     from tests.test_gpu_bsr_attention import _tile_structure_csr
     csr = (W.attention_mask(seq=2048, block=64, window=4, random_blocks=2,
                             seed=3) if shape == "block"
@@ -125,9 +125,32 @@ def test_bf16_sddmm_tiles(dev, orc, kdim, shape):
     lhs = rng.standard_normal((csr.rows, kdim)).astype(np.float32)
     rhs = rng.standard_normal((kdim, csr.cols)).astype(np.float32)
     vals = rng.uniform(-1, 1, csr.nnz).astype(np.float32)
-    got = _sddmm(csr, vals, lhs, rhs, sw.SDDMM_AFFINE, 0.125, 0.5,
-                 "sddmm-mapping=row-tile-mfma")
-    _sddmm_check(orc, csr, vals, lhs, rhs, sw.SDDMM_AFFINE, 0.125, 0.5, got)
+    for kind, alpha, beta in ((sw.SDDMM_AFFINE, 0.125, 0.5),
+                              (sw.SDDMM_MUL, 1.0, 0.0),
+                              (sw.SDDMM_DOT, 0.3, 0.7)):
+        got = _sddmm(csr, vals, lhs, rhs, kind, alpha, beta,
+                     "sddmm-mapping=row-tile-mfma")
+        _sddmm_check(orc, csr, vals, lhs, rhs, kind, alpha, beta, got)
+
+
+@pytest.mark.parametrize("kdim", [64, 128])
+def test_bf16_sddmm_tiles_in_place(dev, orc, kdim):
+    """Output in place of the sample values: each entry's sample is read
+    before it is written."""
+    csr = W.attention_mask(seq=2048, block=64, window=4, random_blocks=2,
+                           seed=3)
+    rng = np.random.default_rng(kdim)
+    lhs = rng.standard_normal((csr.rows, kdim)).astype(np.float32)
+    rhs = rng.standard_normal((kdim, csr.cols)).astype(np.float32)
+    vals = rng.uniform(-1, 1, csr.nnz).astype(np.float32)
+    vt = b16(vals)
+    G.say(f"bf16 sddmm in place kdim={kdim}")
+    sw.sddmm(G.t(csr.row_offsets), G.t(csr.column_indices), vt, b16(lhs),
+             b16(rhs), vt, sw.SDDMM_AFFINE, 0.125, 0.5,
+             options="sddmm-mapping=row-tile-mfma")
+    torch.cuda.synchronize()
+    _sddmm_check(orc, csr, vals, lhs, rhs, sw.SDDMM_AFFINE, 0.125, 0.5,
+                 host(vt))
 
 
 # ---- row reduce / row-wise map ---------------------------------------------
