@@ -566,8 +566,10 @@ constexpr int kFusedChunks = kFusedCols / (16 * kFusedWaves);
 // op's sample values, q its lhs, kt its rhs, scores its output, and `kind`
 // its region; the tile stores its scores and ends (value, rmax, rsum, out
 // and dv are unused).  The attention chain takes the affine region.
+// NS (with SO; no sample values, mask is null): every sample reads as zero
+// and no sample window is loaded.
 // (at most 128 VGPRs: the two workgroups of a CU need four waves per SIMD)
-template <int KB, int W, bool IL, bool SO>
+template <int KB, int W, bool IL, bool SO, bool NS = false>
 __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused(
     const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
     const float *__restrict__ mask, const float *__restrict__ q,
@@ -578,6 +580,7 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused(
   const int region = SO ? kind : SW_SDDMM_AFFINE;
   static_assert(W == 8 && kFusedCols == 8 * kWave && kFusedChunks == 4,
                 "check layout");
+  static_assert(SO || !NS, "the attention chain reads its mask");
   __shared__ float part[W][4][4][kWave]; // [wave][n tile][v][lane]
   __shared__ float wred[2][W][16];       // [max, sum][wave][row]
   __shared__ int32_t lcol[kFusedCols];   // the last row's columns
@@ -747,6 +750,12 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused(
       }
     }
   };
+  auto load_window = [&](int k, v4f &w) __attribute__((always_inline)) {
+    if constexpr (NS)
+      w = v4f{0.f, 0.f, 0.f, 0.f};
+    else
+      __builtin_memcpy(&w, mask + window_at(k), sizeof(v4f));
+  };
   // A. S^T per chunk: sv[k][v] = score (i, t0(k) + 4g + v)
   float sv[kFusedChunks][4];
   auto sddmm_chunk = [&](int k, const float (&a)[16 * KB], const v4f &w)
@@ -785,8 +794,8 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused(
       v4f w[2];
       gather_k(k0, a[0]);
       gather_k(k0 + 1, a[1]);
-      __builtin_memcpy(&w[0], mask + window_at(k0), sizeof(v4f));
-      __builtin_memcpy(&w[1], mask + window_at(k0 + 1), sizeof(v4f));
+      load_window(k0, w[0]);
+      load_window(k0 + 1, w[1]);
       __builtin_amdgcn_sched_barrier(0);
       sddmm_chunk(k0, a[0], w[0]);
       sddmm_chunk(k0 + 1, a[1], w[1]);
@@ -795,7 +804,7 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused(
         float a[16 * KB];
         v4f w;
         gather_k(k0, a);
-        __builtin_memcpy(&w, mask + window_at(k0), sizeof(v4f));
+        load_window(k0, w);
         __builtin_amdgcn_sched_barrier(0);
         sddmm_chunk(k0, a, w);
       } else {
@@ -1134,7 +1143,7 @@ __global__ __launch_bounds__(64 * W) void sddmm_tile_mfma_bf16(
 // K^T (2 * d * cols) and V (2 * cols * dv) fit 32 bits, that nnz >= 4
 // (amax = nnz - 4) and that Q is 16-byte and V 8-byte aligned.
 // (at most 128 VGPRs: the two workgroups of a CU need four waves per SIMD)
-template <int KB, int W, bool SO>
+template <int KB, int W, bool SO, bool NS = false>
 __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused_bf16(
     const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
     const uint16_t *__restrict__ mask, const uint16_t *__restrict__ q,
@@ -1146,8 +1155,10 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused_bf16(
                 "check layout");
   constexpr int S = 2 * KB;
   // SO: the SDDMM alone (combine kind `kind`), its scores stored from
-  // registers; no softmax and no P V
+  // registers; no softmax and no P V.  NS (with SO): no sample values (mask
+  // is null), every sample reads as zero
   const int region = SO ? kind : SW_SDDMM_AFFINE;
+  static_assert(SO || !NS, "the attention chain reads its mask");
   __shared__ float part[W][4][4][kWave]; // [wave][n tile][v][lane]
   __shared__ float wred[2][W][16];       // [max, sum][wave][row]
   __shared__ int wshared[W]; // each wave's rows share the last row's columns
@@ -1297,8 +1308,12 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused_bf16(
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int k = 0; k < kFusedChunks; ++k)
-      __builtin_memcpy(&mw[k], mask + window_at(k), sizeof(uint64_t));
+    for (int k = 0; k < kFusedChunks; ++k) {
+      if constexpr (NS)
+        mw[k] = 0;
+      else
+        __builtin_memcpy(&mw[k], mask + window_at(k), sizeof(uint64_t));
+    }
     __builtin_amdgcn_sched_barrier(0);
     // without branches: a compare inside a branch would pull its loads
     // into the branch, behind the mask windows
@@ -1535,22 +1550,26 @@ int launch_sddmm(const int32_t *ro, const int32_t *col, const T *val,
       int rc = grid_for(rows, 16, "SDDMM", &grid);
       if (rc)
         return rc;
-      // d of 64 or 128 with sample values, 32-bit offsets and an output
-      // apart from the samples: the fused attention kernel's product phase
-      // (its 4-entry sample windows may reach a neighbouring lane's entries)
-      if ((kdim == 64 || kdim == 128) && val != nullptr && nnz >= 4 &&
+      // d of 64 or 128 with 32-bit offsets, and no sample values or an
+      // output apart from them: the fused attention kernel's product phase
+      // (its 4-entry sample windows may reach a neighbouring tile's entries)
+      if ((kdim == 64 || kdim == 128) && nnz >= 4 &&
           narrow_offsets(nnz, 1) && narrow_offsets(cols, kdim) &&
-          (out + nnz <= val || val + nnz <= out)) {
-#define SW_SDDMM_FUSED(KB)                                                    \
-  hipLaunchKernelGGL((attention_tile_fused<KB, kFusedWaves, false, true>),    \
+          (val == nullptr || out + nnz <= val || val + nnz <= out)) {
+#define SW_SDDMM_FUSED(KB, NS)                                                \
+  hipLaunchKernelGGL((attention_tile_fused<KB, kFusedWaves, false, true, NS>),\
                      dim3((unsigned)grid), dim3(64 * kFusedWaves), 0, st, ro, \
                      col, val, lhs, rhs, nullptr, out, nullptr, nullptr,      \
                      nullptr, (int32_t)rows, cols, (int32_t)kdim, (int64_t)0, \
                      alpha, beta, (uint32_t)(nnz - 4), kind)
-        if (kb == 1)
-          SW_SDDMM_FUSED(1);
+        if (kb == 1 && val != nullptr)
+          SW_SDDMM_FUSED(1, false);
+        else if (kb == 1)
+          SW_SDDMM_FUSED(1, true);
+        else if (val != nullptr)
+          SW_SDDMM_FUSED(2, false);
         else
-          SW_SDDMM_FUSED(2);
+          SW_SDDMM_FUSED(2, true);
 #undef SW_SDDMM_FUSED
         return launch_check("SDDMM tile MFMA kernel");
       }
@@ -1574,20 +1593,24 @@ int launch_sddmm(const int32_t *ro, const int32_t *col, const T *val,
       int rc = grid_for(rows, 16, "SDDMM", &grid);
       if (rc)
         return rc;
-      // d of 64 or 128 with sample values and an output apart from them:
+      // d of 64 or 128, and no sample values or an output apart from them:
       // the fused attention kernel's product phase, as for fp32
-      if ((kdim == 64 || kdim == 128) && val != nullptr && nnz >= 4 &&
-          (out + nnz <= val || val + nnz <= out)) {
-#define SW_SDDMM_FUSED(KB)                                                    \
-  hipLaunchKernelGGL((attention_tile_fused_bf16<KB, kFusedWaves, true>),      \
+      if ((kdim == 64 || kdim == 128) && nnz >= 4 &&
+          (val == nullptr || out + nnz <= val || val + nnz <= out)) {
+#define SW_SDDMM_FUSED(KB, NS)                                                \
+  hipLaunchKernelGGL((attention_tile_fused_bf16<KB, kFusedWaves, true, NS>),  \
                      dim3((unsigned)grid), dim3(64 * kFusedWaves), 0, st, ro, \
                      col, val, lhs, rhs, nullptr, out, nullptr, nullptr,      \
                      nullptr, (int32_t)rows, cols, (int32_t)kdim, (int64_t)0, \
                      alpha, beta, (uint32_t)(nnz - 4), kind)
-        if (kb == 1)
-          SW_SDDMM_FUSED(1);
+        if (kb == 1 && val != nullptr)
+          SW_SDDMM_FUSED(1, false);
+        else if (kb == 1)
+          SW_SDDMM_FUSED(1, true);
+        else if (val != nullptr)
+          SW_SDDMM_FUSED(2, false);
         else
-          SW_SDDMM_FUSED(2);
+          SW_SDDMM_FUSED(2, true);
 #undef SW_SDDMM_FUSED
         return launch_check("SDDMM tile MFMA kernel");
       }
