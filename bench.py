@@ -5,9 +5,9 @@ Headline: CSR SpMV fp32/i32 on the 1,048,576-row lognormal matrix
 (configuration 2), reported as achieved HBM GB/s of algorithmic bytes
 (4(n+1) + 8 nnz + 4 m + 4 n per SpMV) and GFLOP/s (2 nnz), for the tuned
 headline mapping; the run's fastest mapping is named beside it.  Every
-mapping, CSR SpMM (K = 4, 64), BSR SpMM (fp32, bf16) and the
-sparse-attention chain are measured on the same run and reported under
-"workloads".  A step is one call of the C ABI over one resident batch.
+mapping, CSR SpMM (K = 4, 64), BSR SpMM (fp32, bf16), the
+sparse-attention chain and its SDDMM on its own are measured on the same
+run and reported under "workloads".  A step is one call of the C ABI over one resident batch.
 
 Timing: W untimed warmup steps, then K timed steps between HIP events on
 the stream the kernels run on, with a device synchronize on both sides.
@@ -62,7 +62,8 @@ def parse():
     ap.add_argument("--profile", default="",
                     choices=["", "spmv", "floor", "coo", "spmm", "bsr",
                              "bsr-bf16", "bsr-bf16-f32out", "attention",
-                             "attention-bf16", "copy", "reference-sweep"],
+                             "attention-bf16", "sddmm", "sddmm-bf16", "copy",
+                             "reference-sweep"],
                     help="run one workload --steps times with no timing or "
                          "JSON (for rocprofv3 kernel-trace / pmc runs)")
     ap.add_argument("--opts", default="",
@@ -261,6 +262,15 @@ def profile(args):
             "spmm-mapping=row-tile-mfma"))
         for _ in range(n):
             sw.sparse_attention(*att, s, rm, rs, out, alpha, 0.0, options=o)
+    elif w in ("sddmm", "sddmm-bf16"):
+        mask, q, kt, v, alpha = W.config5(seed=0)
+        dt = torch.bfloat16 if w == "sddmm-bf16" else torch.float32
+        sd = (T(mask.row_offsets), T(mask.column_indices),
+              T(mask.values, dt), T(q, dt), T(kt, dt))
+        s = torch.empty(mask.nnz, device=dev, dtype=dt)
+        o = sw.Options.parse(args.opts or "sddmm-mapping=row-tile-mfma")
+        for _ in range(n):
+            sw.sddmm(*sd, s, sw.SDDMM_AFFINE, alpha, 0.0, options=o)
     torch.cuda.synchronize()
     log(f"profile {w} done")
 
@@ -662,6 +672,20 @@ def main():
                     key = "bf16: " + key
                 workloads.setdefault("attention_config5", {})[key] = {
                     "ms": ms, "GFLOP/s": 4 * mask.nnz * 64 / ms / 1e6}
+                log(f"  {ms * 1e3:.1f} us")
+            # the chain's first op on its own: scores = alpha Q K^T on the
+            # mask's positions
+            for opts in ["", "sddmm-mapping=row-tile-mfma"]:
+                o = sw.Options.parse(opts)
+                log(f"SDDMM {dname} '{opts}'")
+                ms = time_steps(lambda: sw.sddmm(
+                    att[0], att[1], att[2], att[3], att[4], scores,
+                    sw.SDDMM_AFFINE, alpha, 0.0, options=o), K, Wm, WARM_MS)
+                key = opts or "reference defaults"
+                if dname == "bf16":
+                    key = "bf16: " + key
+                workloads.setdefault("sddmm_config5", {})[key] = {
+                    "ms": ms, "GFLOP/s": 2 * mask.nnz * 64 / ms / 1e6}
                 log(f"  {ms * 1e3:.1f} us")
             del att, scores, rmax, rsum, outa
 
