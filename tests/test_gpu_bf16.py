@@ -113,14 +113,17 @@ def test_bf16_sddmm(dev, orc, golden, opts):
 
 
 @pytest.mark.parametrize("kdim", [64, 128, 256])
-@pytest.mark.parametrize("shape", ["block", "structure"])
+@pytest.mark.parametrize("shape", ["block", "structure", "long"])
 def test_bf16_sddmm_tiles(dev, orc, kdim, shape):
-    """The bf16 matrix-core SDDMM tiles on a block mask, and on tiles that
-    take its row-by-row fallback, for each combine kind."""
-    from tests.test_gpu_bsr_attention import _tile_structure_csr
+    """The bf16 matrix-core SDDMM tiles on a block mask, on tiles that take
+    its row-by-row fallback, and on tiles whose last rows hold 512, 513 and
+    700 entries, for each combine kind."""
+    from tests.test_gpu_bsr_attention import (_long_prefix_csr,
+                                              _tile_structure_csr)
     csr = (W.attention_mask(seq=2048, block=64, window=4, random_blocks=2,
                             seed=3) if shape == "block"
-           else _tile_structure_csr())
+           else _tile_structure_csr() if shape == "structure"
+           else _long_prefix_csr())
     rng = np.random.default_rng(kdim)
     lhs = rng.standard_normal((csr.rows, kdim)).astype(np.float32)
     rhs = rng.standard_normal((kdim, csr.cols)).astype(np.float32)

@@ -247,17 +247,20 @@ def _tile_structure_csr():
     return W.CSR(len(rows_cols), cols, ro, col, val)
 
 
+@pytest.mark.parametrize("shape", ["structure", "long"])
 @pytest.mark.parametrize("kdim", [64, 128])
 @pytest.mark.parametrize("kind", ["mul", "affine", "dot"])
-def test_sddmm_tile_structure_paths(dev, orc, kind, kdim):
-    csr = _tile_structure_csr()
+def test_sddmm_tile_structure_paths(dev, orc, kind, kdim, shape):
+    """Each path of the SDDMM tiles (see the two matrices' docstrings), for
+    each combine kind."""
+    csr = _tile_structure_csr() if shape == "structure" else _long_prefix_csr()
     rng = np.random.default_rng(5)
     lhs = rng.standard_normal((csr.rows, kdim)).astype(np.float32)
     rhs = rng.standard_normal((kdim, csr.cols)).astype(np.float32)
     k = {"mul": sw.SDDMM_MUL, "affine": sw.SDDMM_AFFINE,
          "dot": sw.SDDMM_DOT}[kind]
     out = torch.full((csr.nnz,), float("nan"), device=G.DEV)
-    G.say(f"sddmm tile structure paths kind={kind} kdim={kdim}")
+    G.say(f"sddmm tile {shape} paths kind={kind} kdim={kdim}")
     sw.sddmm(G.t(csr.row_offsets), G.t(csr.column_indices), G.t(csr.values),
              G.t(lhs), G.t(rhs), out, k, 0.3, 0.7,
              options="sddmm-mapping=row-tile-mfma")
