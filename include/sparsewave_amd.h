@@ -237,6 +237,10 @@ int sw_bsr_spmm_bf16_f32out(const int32_t *block_row_offsets,
  * sparsewave.sddmm: output_values[p] = region(values[p], lhs[r,:] . rhs[:,c])
  * for every stored (r, c) at position p.  lhs[rows][kdim], rhs[kdim][cols]
  * row-major.  ThreadPerRowSDDMMPattern (SparseWaveToGPU.cpp:667-750).
+ * sddmm-mapping=row-tile-mfma runs 16-row v_mfma_f32_16x16x4_f32 tiles for
+ * kdim in {64,128,256}; with kdim 64 or 128, at least 4 entries, and
+ * output_values not overlapping values (or SW_SDDMM_DOT), the tiles are the
+ * fused attention kernel's product phase.  Other kdim take one wave per row.
  */
 int sw_sddmm_csr_f32(const int32_t *row_offsets, const int32_t *column_indices,
                      const float *values, const float *lhs, const float *rhs,
@@ -248,7 +252,8 @@ int sw_sddmm_csr_f32(const int32_t *row_offsets, const int32_t *column_indices,
  * SparseWaveOps.cpp:374-425: values, lhs, rhs and output values share one
  * element type).  The region is evaluated in fp32 on the fp32 dot product
  * and rounded once.  sddmm-mapping=row-tile-mfma with kdim in {64,128,256}
- * runs v_mfma_f32_16x16x32_bf16 tiles (lhs 16-byte aligned). */
+ * runs v_mfma_f32_16x16x32_bf16 tiles (lhs 16-byte aligned); with kdim 64
+ * or 128 as for fp32, through the bf16 fused attention kernel. */
 int sw_sddmm_csr_bf16(const int32_t *row_offsets,
                       const int32_t *column_indices, const uint16_t *values,
                       const uint16_t *lhs, const uint16_t *rhs,
