@@ -166,6 +166,7 @@ def test_bsr_config4_sample(dev, orc):
 # ---- SDDMM / row reduce / row-wise map / attention -------------------------
 
 ROW_OPTS = ["", "sddmm-lanes-per-row=64", "sddmm-block-size=64",
+            "sddmm-block-size=512", "sddmm-block-size=1024",
             "sddmm-mapping=row-tile-mfma", "sddmm-mapping=wave-per-row"]
 
 
