@@ -317,16 +317,15 @@ __global__ __launch_bounds__(1024) void row_reduce_thread(
   float acc = MAX ? -INFINITY : 0.0f;
   const int32_t e = ro[r + 1];
   int32_t p = ro[r];
-  // sixteen loads in flight while that many remain, then four, combined in
-  // position order (a thread's row is a chain of memory trips)
+  // sixteen loads in flight while that many remain (as unaligned vector
+  // loads), then four, combined in position order (a thread's row is a
+  // chain of memory trips)
   for (; p + 15 < e; p += 16) {
-    float v[16];
+    T v[16];
+    __builtin_memcpy(v, val + p, sizeof v);
 #pragma unroll
     for (int u = 0; u < 16; ++u)
-      v[u] = ldv(val + p + u);
-#pragma unroll
-    for (int u = 0; u < 16; ++u)
-      acc = MAX ? maximumf(acc, v[u]) : acc + v[u];
+      acc = MAX ? maximumf(acc, tof(v[u])) : acc + tof(v[u]);
   }
   for (; p + 3 < e; p += 4) {
     float v[4];
@@ -381,15 +380,16 @@ __global__ __launch_bounds__(1024) void rowwise_map_thread(
   const int32_t e = ro[r + 1];
   int32_t p = ro[r];
   // sixteen entries loaded before they are written back: out may be val
-  // itself (in place), and each entry is read before its own write
+  // itself (in place), and each entry is read before its own write; both
+  // as (unaligned) vector accesses, so that a lane's 16 entries take 4 (2
+  // for bf16) memory instructions instead of 16
   for (; p + 15 < e; p += 16) {
-    float v[16];
+    T v[16];
+    __builtin_memcpy(v, val + p, sizeof v);
 #pragma unroll
     for (int u = 0; u < 16; ++u)
-      v[u] = ldv(val + p + u);
-#pragma unroll
-    for (int u = 0; u < 16; ++u)
-      stv(out + p + u, map_value(kind, v[u], rv));
+      stv(&v[u], map_value(kind, tof(v[u]), rv));
+    __builtin_memcpy(out + p, v, sizeof v);
   }
   for (; p < e; ++p)
     stv(out + p, map_value(kind, ldv(val + p), rv));
