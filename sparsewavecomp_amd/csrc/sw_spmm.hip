@@ -38,7 +38,10 @@ __device__ __forceinline__ float rhs_at(const T *__restrict__ rhs, int32_t c,
     return ldv(rhs + (int64_t)c * k + j);
 }
 
-template <bool NARROW, typename T>
+// ROW (k and the block size multiples of 64): a wave's 64 outputs lie in
+// one row, so the row index is put in a scalar register and the row's
+// column and value loads become scalar loads shared by the wave.
+template <bool NARROW, bool ROW, typename T>
 __global__ __launch_bounds__(1024) void spmm_thread_per_output(
     const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
     const T *__restrict__ val, const T *__restrict__ rhs,
@@ -47,6 +50,8 @@ __global__ __launch_bounds__(1024) void spmm_thread_per_output(
   if (e >= rows * k)
     return;
   int64_t r = e / k, c = e - r * k;
+  if constexpr (ROW) // rows * k < 2^31 * 64: the row fits 32 bits
+    r = __builtin_amdgcn_readfirstlane((int32_t)r);
   int32_t s = ro[r], t = ro[r + 1];
   float acc = 0.0f;
   int32_t p = s;
@@ -978,12 +983,19 @@ bool launch_spmm_rows(const int32_t *ro, const int32_t *col, const T *val,
     if (*rc)
       return true;
     dim3 g((unsigned)grid), b((unsigned)B);
-    if (narrow_offsets(rhs_rows, k))
-      hipLaunchKernelGGL((spmm_thread_per_output<true, T>), g, b, 0, st, ro,
-                         col, val, rhs, out, rows, k);
+    const bool row = k % kWave == 0 && B % kWave == 0 && rows <= INT32_MAX;
+    if (narrow_offsets(rhs_rows, k) && row)
+      hipLaunchKernelGGL((spmm_thread_per_output<true, true, T>), g, b, 0, st,
+                         ro, col, val, rhs, out, rows, k);
+    else if (narrow_offsets(rhs_rows, k))
+      hipLaunchKernelGGL((spmm_thread_per_output<true, false, T>), g, b, 0,
+                         st, ro, col, val, rhs, out, rows, k);
+    else if (row)
+      hipLaunchKernelGGL((spmm_thread_per_output<false, true, T>), g, b, 0,
+                         st, ro, col, val, rhs, out, rows, k);
     else
-      hipLaunchKernelGGL((spmm_thread_per_output<false, T>), g, b, 0, st, ro,
-                         col, val, rhs, out, rows, k);
+      hipLaunchKernelGGL((spmm_thread_per_output<false, false, T>), g, b, 0,
+                         st, ro, col, val, rhs, out, rows, k);
     *rc = launch_check("thread-per-output SpMM kernel");
     return true;
   }
