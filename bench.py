@@ -652,6 +652,15 @@ def main():
                 "roofline_ceiling_TFLOP/s": ceiling,
                 "roofline_frac": tf / ceiling}
             log(f"  {ms * 1e3:.1f} us  {tf:.1f} TFLOP/s")
+            if name != "bf16_f32out":
+                # the reference's mapping (thread-per-output) on the same call
+                o0 = sw.Options(bsr_use_mfma=0)
+                ms0 = time_steps(lambda: sw.bsr_spmm(*args4, out4, 16,
+                                                     options=o0),
+                                 max(K // 10, 1), Wm, WARM_MS)
+                workloads[f"bsr_config4_{name}"][
+                    "thread_per_output_ms"] = ms0
+                log(f"  thread-per-output {ms0 * 1e3:.1f} us")
             del args4, out4
         del bsr, rhs4
 

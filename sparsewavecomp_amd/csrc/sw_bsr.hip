@@ -26,23 +26,43 @@ using namespace swd;
 
 namespace {
 
-// thread-per-output for any block size: one thread per output element.
-template <typename T, typename TO>
+// thread-per-output for any block size: one thread per output element,
+// the products added in block and column order.  BS = 16: the block size
+// known, a block's 16 values and rhs rows requested together.  ROW (k and
+// the workgroup size multiples of 64): a wave's outputs lie in one row, whose
+// index is put in a scalar register, so that the block values and column
+// indices are scalar loads shared by the wave.
+template <typename T, typename TO, int BS, bool ROW>
 __global__ __launch_bounds__(1024) void bsr_thread_per_output(
     const int32_t *__restrict__ bro, const int32_t *__restrict__ bcol,
     const T *__restrict__ bval, const T *__restrict__ rhs,
-    TO *__restrict__ out, int64_t rows, int64_t k, int32_t b) {
+    TO *__restrict__ out, int64_t rows, int64_t k, int32_t b_any) {
+  const int32_t b = BS > 0 ? BS : b_any;
   int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= rows * k)
     return;
   int64_t r = e / k, c = e - r * k;
+  if constexpr (ROW) // rows < 2^31
+    r = __builtin_amdgcn_readfirstlane((int32_t)r);
   int64_t br = r / b, lr = r - br * b;
   float acc = 0.0f;
   for (int32_t bp = bro[br]; bp < bro[br + 1]; ++bp) {
     const T *blk = bval + (int64_t)bp * b * b + lr * b;
     int64_t rb = (int64_t)bcol[bp] * b;
-    for (int32_t lc = 0; lc < b; ++lc)
-      acc = __builtin_fmaf(tof(blk[lc]), tof(rhs[(rb + lc) * k + c]), acc);
+    if constexpr (BS > 0) {
+      float a[BS], x[BS];
+#pragma unroll
+      for (int lc = 0; lc < BS; ++lc) {
+        a[lc] = tof(blk[lc]);
+        x[lc] = tof(rhs[(rb + lc) * k + c]);
+      }
+#pragma unroll
+      for (int lc = 0; lc < BS; ++lc)
+        acc = __builtin_fmaf(a[lc], x[lc], acc);
+    } else {
+      for (int32_t lc = 0; lc < b; ++lc)
+        acc = __builtin_fmaf(tof(blk[lc]), tof(rhs[(rb + lc) * k + c]), acc);
+    }
   }
   stv(out + e, acc);
 }
@@ -483,9 +503,20 @@ int launch_bsr(const int32_t *bro, const int32_t *bcol, const T *bval,
   int rc = sw::check_grid(grid, "BSR SpMM");
   if (rc)
     return rc;
-  hipLaunchKernelGGL((bsr_thread_per_output<T, TO>), dim3((unsigned)grid),
-                     dim3((unsigned)B), 0, st, bro, bcol, bval, rhs, out, rows,
-                     k, (int32_t)b);
+  const bool row = k % 64 == 0 && B % 64 == 0 && rows <= INT32_MAX;
+#define SW_BSR_TPO(BS, ROW)                                                   \
+  hipLaunchKernelGGL((bsr_thread_per_output<T, TO, BS, ROW>),                 \
+                     dim3((unsigned)grid), dim3((unsigned)B), 0, st, bro,     \
+                     bcol, bval, rhs, out, rows, k, (int32_t)b)
+  if (b == 16 && row)
+    SW_BSR_TPO(16, true);
+  else if (b == 16)
+    SW_BSR_TPO(16, false);
+  else if (row)
+    SW_BSR_TPO(0, true);
+  else
+    SW_BSR_TPO(0, false);
+#undef SW_BSR_TPO
   return sw::launch_check("thread-per-output BSR SpMM kernel");
 }
 

@@ -45,7 +45,7 @@ def test_bsr_golden(dev, golden, opts):
 # k % 4 == 0 takes the column-interleaved MFMA kernels (partial strips at 40
 # and 200), other k the scalar-load MFMA kernels
 @pytest.mark.parametrize("b,k", [(16, 128), (16, 40), (16, 200), (16, 30),
-                                 (16, 7), (4, 9)])
+                                 (16, 7), (4, 9), (4, 64), (8, 128)])
 def test_bsr_fp32(dev, orc, opts, b, k):
     bsr = W.bsr_banded(seed=b + k, rows=b * 96, block_size=b,
                        blocks_per_row=6, band=3, band_blocks=3,
