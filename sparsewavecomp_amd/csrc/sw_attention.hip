@@ -369,10 +369,13 @@ __global__ __launch_bounds__(256) void row_reduce_wave(
 }
 
 // ---- row-wise map ----------------------------------------------------------
-template <typename T>
+// (KIND a template argument: the map is straight-line code, with no switch
+// per entry)
+template <typename T, int KIND>
 __global__ __launch_bounds__(1024) void rowwise_map_thread(
     const int32_t *__restrict__ ro, const T *val,
-    const T *__restrict__ rowv, T *out, int32_t rows, int kind) {
+    const T *__restrict__ rowv, T *out, int32_t rows) {
+  constexpr int kind = KIND;
   int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (r >= rows)
     return;
@@ -382,14 +385,29 @@ __global__ __launch_bounds__(1024) void rowwise_map_thread(
   // sixteen entries loaded before they are written back: out may be val
   // itself (in place), and each entry is read before its own write; both
   // as (unaligned) vector accesses, so that a lane's 16 entries take 4 (2
-  // for bf16) memory instructions instead of 16
-  for (; p + 15 < e; p += 16) {
+  // for bf16) memory instructions instead of 16.  The next 16 entries are
+  // requested before this step's stores (the ranges are disjoint), so that
+  // waiting for them does not wait for the stores as well (one counter
+  // tracks both).
+  if (p + 15 < e) {
     T v[16];
     __builtin_memcpy(v, val + p, sizeof v);
+    for (; p + 31 < e; p += 16) {
+      T next[16];
+      __builtin_memcpy(next, val + p + 16, sizeof next);
+#pragma unroll
+      for (int u = 0; u < 16; ++u)
+        stv(&v[u], map_value(kind, tof(v[u]), rv));
+      __builtin_memcpy(out + p, v, sizeof v);
+#pragma unroll
+      for (int u = 0; u < 16; ++u)
+        v[u] = next[u];
+    }
 #pragma unroll
     for (int u = 0; u < 16; ++u)
       stv(&v[u], map_value(kind, tof(v[u]), rv));
     __builtin_memcpy(out + p, v, sizeof v);
+    p += 16;
   }
   for (; p < e; ++p)
     stv(out + p, map_value(kind, ldv(val + p), rv));
@@ -1704,9 +1722,25 @@ int launch_rowwise_map(const int32_t *ro, const T *val, const T *rowv, T *out,
     int rc = grid_for(rows, B, "CSR row-wise map", &grid);
     if (rc)
       return rc;
-    hipLaunchKernelGGL(rowwise_map_thread<T>, dim3((unsigned)grid),
-                       dim3((unsigned)B), 0, st, ro, val, rowv, out,
-                       (int32_t)rows, kind);
+#define SW_MAP_THREAD(KIND)                                                   \
+  hipLaunchKernelGGL((rowwise_map_thread<T, KIND>), dim3((unsigned)grid),     \
+                     dim3((unsigned)B), 0, st, ro, val, rowv, out,            \
+                     (int32_t)rows)
+    switch (kind) {
+    case SW_MAP_EXP_SUB:
+      SW_MAP_THREAD(SW_MAP_EXP_SUB);
+      break;
+    case SW_MAP_DIV:
+      SW_MAP_THREAD(SW_MAP_DIV);
+      break;
+    case SW_MAP_SUB:
+      SW_MAP_THREAD(SW_MAP_SUB);
+      break;
+    default:
+      SW_MAP_THREAD(SW_MAP_MUL);
+      break;
+    }
+#undef SW_MAP_THREAD
   }
   return launch_check("CSR row-wise map kernel");
 }
