@@ -573,6 +573,24 @@ def main():
                 raise RuntimeError(f"sw_spmv_csr_f32 returned {rc}")
             ms = time_steps(lambda: lib.sw_spmv_csr_f32(*cargs), K, Wm)
             res1[opts] = {"us": ms * 1e3}
+        if not args.no_cpu:
+            # the reference's CPU path on the same matrix, beside the GPU
+            # mappings ("correctness + CPU
+            # comparison"): the oracle's scalar restatement of
+            # benchmark/SparseBenchmarkUtils.cpp:211-229, one thread,
+            # median of at least 5 passes
+            import oracle
+            oracle.build()
+            passes, t0 = [], time.time()
+            while len(passes) < 5 or (time.time() - t0 < 1.0 and
+                                      len(passes) < 2000):
+                t1 = time.perf_counter()
+                oracle.spmv(c1.row_offsets, c1.column_indices, c1.values, x1)
+                passes.append(time.perf_counter() - t1)
+            res1["cpu_oracle_1_thread"] = {
+                "us": float(np.median(passes)) * 1e6,
+                "passes": len(passes),
+                "min_us": min(passes) * 1e6, "max_us": max(passes) * 1e6}
         workloads["spmv_config1"] = res1
 
         # ---- configuration 3: CSR SpMM K = 4 and 64 -------------------------
@@ -718,6 +736,8 @@ def main():
             passes.append(time.perf_counter() - t1)
         dt = float(np.median(passes))
         cpu = {"value": spmv_bytes / dt / 1e9, "unit": "GB/s", "cores": 1,
+               "host_cores": os.cpu_count(),
+               "host_cores_usable": len(os.sched_getaffinity(0)),
                "kind": "port",
                "sample": f"median of {len(passes)} timed full "
                          f"configuration-2 SpMV passes ({dt * 1e3:.1f} ms; "

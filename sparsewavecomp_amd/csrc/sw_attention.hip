@@ -16,6 +16,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <type_traits>
 
 using namespace swd;
 
@@ -1794,6 +1795,8 @@ int sddmm_entry(const int32_t *row_offsets, const int32_t *column_indices,
                  combine == SW_SDDMM_DOT ? (const void *)output_values
                                          : (const void *)values,
                  rows, nnz, true);
+  if (!rc)
+    rc = check_value_alignment(sizeof(T), {values, lhs, rhs, output_values});
   if (rc)
     return rc;
   if (cols < 0 || kdim < 0 || kdim > INT32_MAX)
@@ -1822,6 +1825,8 @@ int row_reduce_entry(const int32_t *row_offsets, const int32_t *column_indices,
                 "expected CSR row reduction kind 'sum' or 'max', but got '%s'",
                 kind ? kind : "(null)");
   rc = check_csr(row_offsets, column_indices, values, rows, nnz, false);
+  if (!rc)
+    rc = check_value_alignment(sizeof(T), {values, output});
   if (rc)
     return rc;
   if (rows == 0)
@@ -1846,6 +1851,8 @@ int rowwise_map_entry(const int32_t *row_offsets,
   if (map < SW_MAP_EXP_SUB || map > SW_MAP_MUL)
     return fail(SW_ERR_INVALID_ARGUMENT, "unknown row-wise map kind %d", map);
   rc = check_csr(row_offsets, column_indices, values, rows, nnz, false);
+  if (!rc)
+    rc = check_value_alignment(sizeof(T), {values, row_values, output_values});
   if (rc)
     return rc;
   if (rows == 0 || nnz == 0)
@@ -1942,10 +1949,19 @@ int attention_entry(const int32_t *row_offsets, const int32_t *column_indices,
   if (rc)
     return rc;
   rc = check_csr(row_offsets, column_indices, mask_values, rows, nnz, true);
+  if (!rc)
+    rc = check_value_alignment(sizeof(T), {mask_values, query, transposed_key,
+                                           value, scores, row_maximum,
+                                           row_sum, output});
   if (rc)
     return rc;
   if (cols < 0 || d < 0 || dv < 0 || d > INT32_MAX)
     return fail(SW_ERR_INVALID_SHAPE, "invalid attention shapes");
+  if constexpr (std::is_same_v<T, uint16_t>) {
+    rc = check_bf16_spmm_mapping(o); // before any launch
+    if (rc)
+      return rc;
+  }
   if (rows == 0)
     return SW_OK;
   if (!row_maximum || !row_sum || (dv > 0 && !output) ||

@@ -535,14 +535,16 @@ int bsr_entry(const int32_t *block_row_offsets,
                  output, rows, cols, nnzb, k, block_size);
   if (rc)
     return rc;
+  rc = sw::check_value_alignment(sizeof(T), {block_values, rhs});
+  if (!rc)
+    rc = sw::check_value_alignment(sizeof(TO), {output});
+  if (rc)
+    return rc;
   // the MFMA kernels read A rows of a block as 16-byte (fp32) or 8-byte
   // (bf16) vectors
   const bool mfma = o.bsr_use_mfma && block_size == 16 &&
                     (reinterpret_cast<uintptr_t>(block_values) &
                      (4 * sizeof(T) - 1)) == 0;
-  if constexpr (sizeof(TO) == 2)
-    if (mfma && (reinterpret_cast<uintptr_t>(output) & 1u) != 0)
-      return sw::fail(SW_ERR_INVALID_ARGUMENT, "bf16 output is misaligned");
   return launch_bsr<T, TO>(block_row_offsets, block_column_indices,
                            block_values, rhs, output, rows, nnzb, k,
                            block_size, o, sw::as_stream(stream), mfma);

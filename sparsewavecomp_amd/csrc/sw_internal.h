@@ -7,6 +7,7 @@
 
 #include <cstdint>
 #include <cstring>
+#include <initializer_list>
 
 namespace sw {
 
@@ -61,6 +62,35 @@ inline int resolve_options(const sw_options *opts, sw_options *out) {
 }
 
 inline bool streq(const char *a, const char *b) { return std::strcmp(a, b) == 0; }
+
+// Every value buffer must be aligned to its element (2 bytes for bf16, 4 for
+// fp32) on every path, whatever the options: a kernel may take any buffer as
+// a whole element, so an odd bf16 address is rejected before any launch.
+inline int check_value_alignment(size_t elem,
+                                 std::initializer_list<const void *> ptrs) {
+  for (const void *p : ptrs)
+    if (p && (reinterpret_cast<uintptr_t>(p) & (elem - 1)) != 0)
+      return fail(SW_ERR_INVALID_ARGUMENT,
+                  "a value buffer is not aligned to its %zu-byte element",
+                  elem);
+  return SW_OK;
+}
+
+// The SpMM position mappings add partial sums into the output across
+// workgroups, which a bf16 output cannot hold.  Checked before the first
+// launch of every entry point that ends in a bf16 SpMM (the SpMM itself and
+// the attention chain), so a rejected call leaves every buffer untouched.
+inline int check_bf16_spmm_mapping(const sw_options &o) {
+  if (streq(o.spmm_mapping, "thread-per-position") ||
+      streq(o.spmm_mapping, "wave-per-position"))
+    return fail(SW_ERR_INVALID_OPTION,
+                "spmm-mapping=%s adds partial sums into the output across "
+                "workgroups, which a bf16 output cannot hold; bf16 takes "
+                "thread-per-output, wave-per-row-tile, wave-per-row-balanced "
+                "or row-tile-mfma",
+                o.spmm_mapping);
+  return SW_OK;
+}
 
 // Largest nnz a CSR operand may have.  Row loops step a position index past
 // the row's end by less than one step (at most 16 positions for each of up

@@ -1199,15 +1199,9 @@ int launch_spmm(const int32_t *ro, const int32_t *col, const uint16_t *val,
                 const uint16_t *rhs, uint16_t *out, int64_t rows,
                 int64_t rhs_rows, int64_t nnz, int64_t k, const sw_options &o,
                 const char *what, hipStream_t st) {
-  int rc = SW_OK;
-  if (streq(o.spmm_mapping, "thread-per-position") ||
-      streq(o.spmm_mapping, "wave-per-position"))
-    return fail(SW_ERR_INVALID_OPTION,
-                "spmm-mapping=%s adds partial sums into the output across "
-                "workgroups, which a bf16 output cannot hold; bf16 takes "
-                "thread-per-output, wave-per-row-tile, wave-per-row-balanced "
-                "or row-tile-mfma",
-                o.spmm_mapping);
+  int rc = check_bf16_spmm_mapping(o);
+  if (rc)
+    return rc;
   launch_spmm_rows<uint16_t>(ro, col, val, rhs, out, rows, rhs_rows, nnz, k,
                              o, what, st, &rc);
   return rc;
@@ -1228,6 +1222,8 @@ int spmm_entry(const int32_t *row_offsets, const int32_t *column_indices,
   if (rc)
     return rc;
   rc = sw::check_csr(row_offsets, column_indices, values, rows, nnz, true);
+  if (!rc)
+    rc = sw::check_value_alignment(sizeof(T), {values, rhs, output});
   if (rc)
     return rc;
   if (cols < 0 || k < 0)

@@ -872,6 +872,8 @@ extern "C" int sw_spmv_csr_f32(const int32_t *row_offsets,
   if (rc)
     return rc;
   rc = sw::check_csr(row_offsets, column_indices, values, rows, nnz, true);
+  if (!rc)
+    rc = sw::check_value_alignment(sizeof(float), {values, vector, output});
   if (rc)
     return rc;
   if (cols < 0)
@@ -925,6 +927,9 @@ extern "C" int sw_spmv_coo_f32(const int32_t *row_indices,
     return sw::fail(SW_ERR_INVALID_SHAPE,
                     "i32 COO row indices cannot address %lld rows",
                     (long long)rows);
+  rc = sw::check_value_alignment(sizeof(float), {values, vector, output});
+  if (rc)
+    return rc;
   if (rows == 0)
     return SW_OK;
   if (!output)

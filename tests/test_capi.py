@@ -180,6 +180,73 @@ def test_bf16_entry_points_reject_before_launch():
                                         1.0, 0.0, None, None) == 0
 
 
+def test_bf16_attention_rejects_position_spmm_before_any_launch():
+    """The bf16 chain ends in a bf16 SpMM, which refuses the position
+    mappings: the attention entry point rejects them before its first
+    kernel (the SDDMM), so the scores, row maxima and row sums keep what
+    they held.  Host buffers stand in for device memory: the call must
+    return before it reads or writes any of them."""
+    import numpy as np
+    lib = sw.load_library()
+    rows, nnz, d, dv = 4, 8, 64, 64
+    ro = np.array([0, 2, 4, 6, 8], np.int32)
+    col = np.array([0, 1] * 4, np.int32)
+    ins = [np.zeros(n, np.uint16) for n in (nnz, rows * d, d * 2, 2 * dv)]
+    scores = np.full(nnz, 0x7fc1, np.uint16)
+    rmax = np.full(rows, 0x7fc2, np.uint16)
+    rsum = np.full(rows, 0x7fc3, np.uint16)
+    out = np.full(rows * dv, 0x7fc4, np.uint16)
+    before = [a.copy() for a in (scores, rmax, rsum, out)]
+    P = ctypes.c_void_p
+    for mapping in ("wave-per-position", "thread-per-position"):
+        o = sw.Options(spmm_mapping=mapping)
+        rc = lib.sw_sparse_attention_bf16(
+            P(ro.ctypes.data), P(col.ctypes.data),
+            *(P(a.ctypes.data) for a in ins),
+            *(P(a.ctypes.data) for a in (scores, rmax, rsum, out)),
+            rows, 2, nnz, d, dv, 0.125, 0.0, o.ref, None)
+        assert rc == -1
+        assert b"bf16 output cannot hold" in lib.sw_last_error()
+        for a, b in zip((scores, rmax, rsum, out), before):
+            assert np.array_equal(a, b)
+
+
+def test_value_buffers_must_be_element_aligned():
+    """An odd address for a bf16 buffer (or a float buffer off its 4-byte
+    element) is rejected on every path, whatever the options choose:
+    BSR with and without the matrix cores, SpMM, SDDMM, the row ops, the
+    attention chain and SpMV."""
+    lib = sw.load_library()
+    P = ctypes.c_void_p
+    ok, odd = P(64), P(65)
+    for use_mfma in (1, 0):
+        o = sw.Options(bsr_use_mfma=use_mfma)
+        for fn in (lib.sw_bsr_spmm_bf16, lib.sw_bsr_spmm_bf16_f32out):
+            for args in ((odd, ok, ok), (ok, odd, ok)):
+                rc = fn(ok, ok, *args[:2], args[2], 32, 32, 2, 8, 16, o.ref,
+                        None)
+                assert rc == -3 and b"aligned" in lib.sw_last_error()
+        rc = lib.sw_bsr_spmm_bf16(ok, ok, ok, ok, odd, 32, 32, 2, 8, 16,
+                                  o.ref, None)
+        assert rc == -3 and b"2-byte element" in lib.sw_last_error()
+        rc = lib.sw_bsr_spmm_f32(ok, ok, ok, ok, P(66), 32, 32, 2, 8, 16,
+                                 o.ref, None)
+        assert rc == -3 and b"4-byte element" in lib.sw_last_error()
+    assert lib.sw_spmm_csr_bf16(ok, ok, ok, ok, odd, 4, 4, 4, 8, None,
+                                None) == -3
+    assert lib.sw_sddmm_csr_bf16(ok, ok, ok, odd, ok, ok, 4, 4, 4, 4, 0, 1.0,
+                                 0.0, None, None) == -3
+    assert lib.sw_csr_row_reduce_bf16(ok, None, ok, odd, 4, 4, b"sum", None,
+                                      None) == -3
+    assert lib.sw_csr_rowwise_map_bf16(ok, None, ok, odd, ok, 4, 4, 0, None,
+                                       None) == -3
+    assert lib.sw_sparse_attention_bf16(ok, ok, ok, ok, ok, ok, odd, ok, ok,
+                                        ok, 4, 4, 4, 4, 4, 1.0, 0.0, None,
+                                        None) == -3
+    assert lib.sw_spmv_csr_f32(ok, ok, ok, P(66), ok, 4, 4, 4, None,
+                               None) == -3
+
+
 def _cpu(*shape, dtype=None):
     import torch
     return torch.zeros(shape, dtype=dtype or torch.float32)

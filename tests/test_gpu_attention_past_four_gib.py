@@ -119,7 +119,8 @@ def test_attention_kt_v_past_four_gib(dev, orc, wide, opts):
     torch.cuda.synchronize()
     refs = orc.sparse_attention(compact.row_offsets, compact.column_indices,
                                 compact.values, q, kp, vp, 0.125, 0.5)
-    _check_attention(orc, compact, scores, rmax, rsum, out, refs, vp)
+    _check_attention(orc, compact, scores, rmax, rsum, out, refs, vp,
+                     (compact.values, q, kp, 0.125, 0.5))
     del kt, v
     torch.cuda.empty_cache()
 

@@ -219,6 +219,19 @@ def config3():
     (64, "spmm-mapping=wave-per-row-balanced spmm-positions-per-lane=4 "
          "spmm-block-size=64"),
     (4, "spmm-mapping=wave-per-row-balanced spmm-positions-per-lane=4"),
+    # the exact mappings bench.py times on configuration 3
+    (4, ""),   # the reference's default, thread-per-output
+    (64, ""),
+    (4, "spmm-mapping=wave-per-position spmm-positions-per-lane=8 "
+        "spmm-block-size=256"),
+    (4, "spmm-mapping=wave-per-row-tile spmm-tile-size=4 "
+        "spmm-block-size=64"),
+    (4, "spmm-mapping=wave-per-row-tile-lds spmm-tile-size=4"),
+    (64, "spmm-mapping=wave-per-position spmm-positions-per-lane=16 "
+         "spmm-block-size=64"),
+    (64, "spmm-mapping=wave-per-row-tile spmm-tile-size=32 "
+         "spmm-lanes-per-row=64 spmm-block-size=64"),
+    (64, "spmm-mapping=wave-per-row-tile-lds spmm-tile-size=32"),
 ])
 def test_config3_full_size(dev, orc, config3, k, opts):
     csr = config3
@@ -230,6 +243,7 @@ def test_config3_full_size(dev, orc, config3, k, opts):
     rows = np.concatenate([rows, np.argsort(np.diff(csr.row_offsets))[-50:]])
     sub = _row_subset(csr, rows)
     _check(orc, sub, rhs, out[rows])
+    assert np.all(np.isfinite(out))  # every row written (output NaN-filled)
 
 
 def _row_subset(csr, rows):

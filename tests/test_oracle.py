@@ -370,13 +370,79 @@ def test_attention_matches_dense_softmax(orc):
     _, _, _, out = orc.sparse_attention(mask.row_offsets, mask.column_indices,
                                         mask.values, q, kt, v, alpha)
     want, bound = _dense_attention(mask, q, kt, v, alpha)
-    assert_within_bound(out, want, bound, rel=2e-5)
+    tol = _fp32_chain_vs_exact_tolerance(orc, mask, q, kt, v, alpha)
+    assert np.all(np.abs(out - want) <= tol)
+    # the bound is not vacuous: at most 1e-4 of sum |P V| on every output
+    assert np.all(tol <= 1e-4 * bound)
     # a non-transposed key (operand mistake) must fail
     _, _, _, bad = orc.sparse_attention(mask.row_offsets, mask.column_indices,
                                         mask.values, q, np.ascontiguousarray(
                                             kt.reshape(256, 8).T), v, alpha)
-    with pytest.raises(AssertionError):
-        assert_within_bound(bad, want, bound, rel=2e-5)
+    assert not np.all(np.abs(bad - want) <= tol)
+
+
+def _fp32_chain_vs_exact_tolerance(orc, mask, q, kt, v, alpha):
+    """|out_fp32 - out_exact| for the oracle's fp32 chain: each score is a
+    d-term fp32 dot product and one scaling, so |s - s_exact| <= (d + 2) u
+    B_p (u = 2^-24, B_p = |alpha| sum_k |q_rk kt_kc|); the probabilities
+    then obey the softmax bound of tests/_attention_check.py with that E_r,
+    and the output SpMM adds its sequential-sum rounding (n_r + 2) u
+    sum_p |P_p V_pc| to sum_p tolP_p |V_pc|."""
+    from tests._attention_check import (U, row_error, score_bounds,
+                                        tolerances)
+    d = q.shape[1]
+    s_ref, m_ref, _, _ = orc.sparse_attention(
+        mask.row_offsets, mask.column_indices, mask.values, q, kt, v, alpha)
+    raw = orc.sddmm(mask.row_offsets, mask.column_indices, mask.values, q, kt,
+                    orc.SDDMM_AFFINE, alpha, 0.0).astype(np.float64)
+    rows = np.repeat(np.arange(mask.rows), np.diff(mask.row_offsets))
+    e_row = row_error(mask, (d + 2) * U * score_bounds(orc, 
+        mask, mask.values, q, kt, alpha, 0.0), raw)
+    tol_p, _ = tolerances(mask, s_ref, raw - m_ref[rows], e_row)
+    n = np.diff(mask.row_offsets).astype(np.float64)
+    pv = orc.spmm_abs_bound(mask.row_offsets, mask.column_indices, s_ref, v)
+    carried = orc.spmm_abs_bound(mask.row_offsets, mask.column_indices,
+                                 tol_p.astype(np.float32), v)
+    return carried + (n[:, None] + 2) * U * pv
+
+
+def test_attention_checker_accepts_oracle_and_rejects_mistakes(orc):
+    """tests/_attention_check.check_attention_f32 (the GPU tests' checker)
+    passes the oracle's own chain and fails planted mistakes: one
+    probability moved by 1e-3 of itself, a row maximum off by 1e-3, a
+    wrong alpha, and an output element moved by 1e-4 of sum |P V|."""
+    from tests._attention_check import check_attention_f32
+    mask = W.attention_mask(seq=256, block=16, window=3, random_blocks=2,
+                            seed=7)
+    rng = np.random.default_rng(7)
+    q = rng.standard_normal((256, 16)).astype(np.float32)
+    kt = rng.standard_normal((16, 256)).astype(np.float32)
+    v = rng.standard_normal((256, 16)).astype(np.float32)
+    mv = rng.uniform(-1, 1, mask.nnz).astype(np.float32)
+    mv[rng.random(mask.nnz) < 0.1] = -np.inf
+    alpha, beta = 0.25, 0.5
+    refs = orc.sparse_attention(mask.row_offsets, mask.column_indices, mv, q,
+                                kt, v, alpha, beta)
+    s, m, r, o = refs
+    check_attention_f32(orc, mask, mv, q, kt, v, alpha, beta, s, m, r, o)
+    p = int(np.argmax(s))
+    for what in ("p", "m", "alpha", "o"):
+        s2, m2, r2, o2 = (a.copy() for a in refs)
+        if what == "p":
+            s2[p] *= 1 + 1e-3
+        elif what == "m":
+            m2[3] += 1e-3 * max(1.0, abs(m2[3]))
+        elif what == "alpha":
+            s2, m2, r2, o2 = orc.sparse_attention(
+                mask.row_offsets, mask.column_indices, mv, q, kt, v,
+                alpha * 1.01, beta)
+        else:
+            pv = orc.spmm_abs_bound(mask.row_offsets, mask.column_indices,
+                                    s, v)
+            o2[5, 2] += 1e-4 * pv[5, 2]
+        with pytest.raises(AssertionError):
+            check_attention_f32(orc, mask, mv, q, kt, v, alpha, beta, s2, m2,
+                                r2, o2)
 
 
 # ---- index work: bit-exact ------------------------------------------------
