@@ -50,7 +50,11 @@ extern "C" {
  */
 typedef struct sw_options {
   char spmv_mapping[32];            /* thread-per-row | wave-per-row | block-per-row |
-                                       thread-per-position | wave-per-position */
+                                       thread-per-position | wave-per-position |
+                                       wave-per-row-balanced (Wave64 extension:
+                                       each row summed whole by the wave whose
+                                       nonzero chunk holds its first position;
+                                       no atomics, bit-identical repeats) */
   int64_t spmv_block_size;          /* 1..1024, default 256 */
   int64_t spmv_position_chunk_size; /* thread-per-position chunk, default 1 */
   char spmv_position_reduction[16]; /* atomic | segmented (thread-per-position) */

@@ -214,11 +214,15 @@ int sw_validate_options(const sw_options *o) {
   bool spmv_row = spmv == "thread-per-row" || spmv == "wave-per-row" ||
                   spmv == "block-per-row";
   bool spmv_pos = spmv == "thread-per-position" || spmv == "wave-per-position";
-  if (!spmv_row && !spmv_pos)
+  // Wave64 extension: rows owned by the wave whose nonzero chunk holds
+  // their first position
+  bool spmv_owner = spmv == "wave-per-row-balanced";
+  if (!spmv_row && !spmv_pos && !spmv_owner)
     return sw::fail(SW_ERR_INVALID_OPTION,
                     "unsupported SpMV mapping strategy '%s'; expected "
                     "'thread-per-row', 'wave-per-row', 'block-per-row', "
-                    "'thread-per-position', or 'wave-per-position'",
+                    "'thread-per-position', 'wave-per-position', or "
+                    "'wave-per-row-balanced'",
                     o->spmv_mapping);
   if (spmm != "thread-per-output" && spmm != "wave-per-row-tile" &&
       spmm != "thread-per-position" && spmm != "wave-per-position" &&
@@ -263,7 +267,7 @@ int sw_validate_options(const sw_options *o) {
                    spmm == "wave-per-row-balanced" ||
                    spmm == "wave-per-row-tile-lds";
   bool wave_spmv = spmv == "wave-per-row" || spmv == "block-per-row" ||
-                   spmv == "wave-per-position";
+                   spmv == "wave-per-position" || spmv_owner;
   if ((wave_spmm || wave_spmv) && w != 64)
     return sw::fail(SW_ERR_INVALID_OPTION,
                     "%s currently requires Wave64 on gfx950, but got wave "

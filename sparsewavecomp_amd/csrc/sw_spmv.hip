@@ -471,9 +471,11 @@ __global__ __launch_bounds__(1024) void spmv_wave_position(
   const float prev_scanned = shfl_up1_f(scanned, 0.0f);
   const int next_lrow = shfl_down1_i(active ? lrow : -2, -2);
   // Segment emissions are fire-and-forget atomic adds into the zeroed
-  // output.  (Plain 4-byte stores of the rows owned by one wave measured
-  // twice as slow: neighbouring rows of a cache line are written from waves
-  // on different XCDs.)
+  // output.  Measured on configuration 2 (P = 4, 64-thread blocks, 206.7 us
+  // as written): plain stores for the rows a wave holds whole with atomic
+  // adds only for the two rows it may share, 402 us with the waves in
+  // XCD-contiguous order (stores and atomics then meet in nearly every
+  // 128-byte line of the output); all-atomic in that order 229 us.
   if (active) {
     if (closed > 0) {
       float h = head + (prev_key == lrow ? prev_scanned : 0.0f);
@@ -482,6 +484,219 @@ __global__ __launch_bounds__(1024) void spmv_wave_position(
     if (next_lrow != row)
       unsafeAtomicAdd(y + row, scanned);
   }
+}
+
+// The values and gathered x of one lane's P positions q0 .. q0 + P - 1 that
+// lie in [lb_all, le_all) (zeros elsewhere); 128-bit column / value loads
+// when the whole group lies inside the arrays.
+template <int P, bool VEC>
+__device__ __forceinline__ void owner_step_loads(
+    const int32_t *__restrict__ col, const float *__restrict__ val,
+    const float *__restrict__ x, int32_t q0, int32_t lb_all, int32_t le_all,
+    int32_t nnz, float (&vv)[P], float (&xg)[P]) {
+  const int32_t lb = std::max(q0, lb_all);
+  const int32_t le = std::min(q0 + P, le_all);
+#pragma unroll
+  for (int q = 0; q < P; ++q) {
+    vv[q] = 0.0f;
+    xg[q] = 0.0f;
+  }
+  if (lb >= le)
+    return;
+  if constexpr (VEC && P >= 4) {
+    if (q0 + P <= nnz) {
+#pragma unroll
+      for (int q = 0; q < P; q += 4) {
+        const uint32_t bo = 4u * (uint32_t)(q0 + q);
+        const v4i c =
+            ld_stream(at_bytes(reinterpret_cast<const v4i *>(col), bo));
+        const v4f v =
+            ld_nontemporal(at_bytes(reinterpret_cast<const v4f *>(val), bo));
+        const int32_t p = q0 + q;
+        vv[q + 0] = v.x;
+        vv[q + 1] = v.y;
+        vv[q + 2] = v.z;
+        vv[q + 3] = v.w;
+        if (p + 0 >= lb && p + 0 < le) xg[q + 0] = gather<true>(x, c.x);
+        if (p + 1 >= lb && p + 1 < le) xg[q + 1] = gather<true>(x, c.y);
+        if (p + 2 >= lb && p + 2 < le) xg[q + 2] = gather<true>(x, c.z);
+        if (p + 3 >= lb && p + 3 < le) xg[q + 3] = gather<true>(x, c.w);
+      }
+      return;
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < P; ++q) {
+    const int32_t p = q0 + q;
+    if (p >= lb && p < le) {
+      vv[q] = ld_stream(val + p);
+      xg[q] = x[ld_stream(col + p)];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// wave-per-row-balanced: row-owner SpMV (Wave64 extension).
+//
+// The nonzeros are cut into chunks of C = 64 * P * S positions, and wave w
+// owns the rows whose first position lies in chunk w (ro[r] in
+// [wC, (w+1)C); rows beginning at or past the last chunk's start belong to
+// the last wave).  So every output row has exactly one writer, which stores
+// it with a plain store: no zero fill and no atomics, and the work stays
+// balanced by nonzeros (a wave's rows hold C positions give or take the row
+// that straddles each chunk end).  Waves run in XCD-contiguous order, so the
+// short row ranges that neighbouring waves store share one XCD's L2.
+//
+// A wave finds its first row (a wave-uniform binary search) and the first
+// row of the next chunk (a gallop from there), then walks its positions
+// [ro[r_lo], ro[r_hi]) in steps of 64 * P: lane l takes P consecutive
+// positions, finds the row of its first position in an LDS window of 64 row
+// ends, and walks them as the position kernel does -- rows that begin and end
+// inside the lane are stored directly, a lane's first and last rows are
+// joined across lanes by the DPP segmented scan.  A row still open at the
+// end of a step is carried, wave-uniform, into the next step's lane 0.
+// Rows with no entries, which no position reaches, are stored as zero by a
+// pass over the wave's rows.
+//
+// Every sum is formed in a fixed order (a lane's positions in sequence, the
+// scan's fixed DPP steps, the carry), so repeated calls give bit-identical
+// outputs, which the atomic position mappings do not.  It costs time: on
+// configuration 2 (P = 4, S = 4) 235 us against the position kernel's
+// 207 us; S = 1 248 us, S = 2 240 us; loading each step's values one step
+// ahead measured no faster (237 us).  A wave's rows run to the end of the
+// row that straddles its chunk end, so the few waves holding the start of a
+// row of thousands of entries finish last.
+template <int P, bool VEC>
+__global__ __launch_bounds__(256) void spmv_row_owner(
+    const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
+    const float *__restrict__ val, const float *__restrict__ x,
+    float *__restrict__ y, int32_t rows, int32_t nnz, int64_t chunk,
+    int64_t waves) {
+  const int lane = lane_id();
+  const int64_t wave =
+      xcd_contiguous(blockIdx.x, gridDim.x) * (blockDim.x / kWave) +
+      wave_in_group();
+  if (wave >= waves)
+    return; // wave-uniform
+  const int r_lo =
+      wave == 0 ? 0
+                : row_search_uniform(ro, 0u, (uint32_t)rows + 1u,
+                                     (int32_t)(wave * chunk - 1)) + 1;
+  const int r_hi =
+      wave == waves - 1
+          ? rows
+          : row_search_gallop(ro, (uint32_t)r_lo, (uint32_t)rows + 1u,
+                              (int32_t)((wave + 1) * chunk - 1)) + 1;
+  if (r_lo >= r_hi)
+    return; // no row begins in this chunk
+  // positions of the owned rows, kept inside [0, nnz]
+  const int32_t p_beg = std::min(std::max(ro[r_lo], 0), nnz);
+  const int32_t p_end = std::min(std::max(ro[r_hi], p_beg), nnz);
+
+  __shared__ int32_t window[256 / kWave][kWave];
+  int32_t *win = window[wave_in_group()];
+  constexpr int32_t kStep = kWave * P;
+  const int32_t a0 = VEC ? (p_beg & ~3) : p_beg;
+  int r_cur = r_lo;          // row of the step's first position
+  float carry = 0.0f;        // partial of r_cur from earlier steps
+  for (int32_t s0 = a0; s0 < p_end; s0 += kStep) {
+    const int32_t q0 = s0 + lane * P; // lane's first position
+    const int32_t lb = std::max(q0, p_beg);
+    const int32_t le = std::min(q0 + P, p_end);
+    const bool active = lb < le;
+    float va[P], xa[P];
+    owner_step_loads<P, VEC>(col, val, x, q0, p_beg, p_end, nnz, va, xa);
+    // row ends of rows r_cur .. r_cur + 63 (INT32_MAX past the wave's rows)
+    const int jw = r_cur + 1 + lane;
+    const int32_t wv = jw <= r_hi ? ro[jw] : INT32_MAX;
+    win[lane] = wv;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    int lrow = 0, row = 0, closed = 0;
+    float head = 0.0f, acc = 0.0f;
+    int32_t next = 0;
+    if (active) {
+      // number of window row ends <= lb; 64 means lb lies past the window
+      int lo = 0, hi = kWave;
+      while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (win[mid] <= lb)
+          lo = mid + 1;
+        else
+          hi = mid;
+      }
+      // (the minimum keeps rows inside the wave's range whatever the row
+      // offsets hold; for a valid CSR operand it never binds)
+      if (lo < kWave) {
+        lrow = std::min(r_cur + lo, r_hi - 1);
+        next = win[lrow - r_cur];
+      } else {
+        lrow = std::min(row_search_lane(ro, (uint32_t)r_cur + kWave + 1u,
+                                        (uint32_t)r_hi + 1u, lb),
+                        r_hi - 1);
+        next = ro[lrow + 1];
+      }
+      row = lrow;
+      // lane 0 of a later step continues the row carried from the last
+      if (lane == 0)
+        acc = carry;
+#pragma unroll
+      for (int q = 0; q < P; ++q) {
+        const int32_t p = q0 + q;
+        if (p >= lb && p < le) {
+          while (p >= next && row < r_hi - 1) {
+            if (closed == 0)
+              head = acc;
+            else
+              y[row] = acc; // began and ended inside this lane
+            ++closed;
+            acc = 0.0f;
+            ++row;
+            next = row - r_cur < kWave ? win[row - r_cur] : ro[row + 1];
+          }
+          acc = __builtin_fmaf(va[q], xa[q], acc);
+        }
+      }
+    }
+    // every lane's window reads done before the next step rewrites it
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int key = active ? row : -1;
+    const float scanned = wave_segmented_scan(key, active ? acc : 0.0f);
+    const int prev_key = shfl_up1_i(key, INT32_MIN);
+    const float prev_scanned = shfl_up1_f(scanned, 0.0f);
+    const int next_lrow = shfl_down1_i(active ? lrow : -2, -2);
+    const int32_t step_end = std::min(s0 + kStep, p_end);
+    if (active) {
+      if (closed > 0)
+        y[lrow] = head + (prev_key == lrow ? prev_scanned : 0.0f);
+      // the tail row ends in this step unless it reaches past step_end
+      if (next_lrow != row && next <= step_end)
+        y[row] = scanned;
+    }
+    // a row open past the step end is held by lane 63 (the step is full)
+    const int last_row = __builtin_amdgcn_readlane(row, kWave - 1);
+    const int32_t last_next = __builtin_amdgcn_readlane(next, kWave - 1);
+    const bool open = s0 + kStep < p_end && last_next > s0 + kStep;
+    carry = open ? __int_as_float(__builtin_amdgcn_readlane(
+                       __float_as_int(scanned), kWave - 1))
+                 : 0.0f;
+    // the next step's first row: lane 63's last row when that row is open,
+    // else the row holding the next position (after it, usually right after)
+    if (s0 + kStep < p_end)
+      r_cur = open ? last_row
+                   : std::min(row_search_gallop(ro, (uint32_t)last_row + 1u,
+                                                (uint32_t)r_hi + 1u,
+                                                s0 + kStep),
+                              r_hi - 1);
+  }
+  // rows with no entries, which no position reaches, are zero (r_hi <= rows,
+  // so ro[r + 1] exists)
+  for (int r = r_lo + lane; r < r_hi; r += kWave)
+    if (ro[r] == ro[r + 1])
+      y[r] = 0.0f;
 }
 
 // ---------------------------------------------------------------------------
@@ -664,6 +879,19 @@ void launch_group(dim3 grid, dim3 block, hipStream_t st, const int32_t *ro,
 }
 
 template <int P, bool VEC>
+void launch_row_owner(dim3 grid, dim3 block, hipStream_t st,
+                      const int32_t *ro, const int32_t *col, const float *val,
+                      const float *x, float *y, int32_t rows, int32_t nnz,
+                      int64_t chunk, int64_t waves) {
+  hipLaunchKernelGGL((spmv_row_owner<P, VEC>), grid, block, 0, st, ro, col,
+                     val, x, y, rows, nnz, chunk, waves);
+}
+
+// Steps of 64 * P positions in one wave's chunk of the row-owner SpMV
+// (configuration 2, P = 4: 1 step 248 us, 2 steps 240 us, 4 steps 235 us).
+constexpr int64_t kRowOwnerSteps = 4;
+
+template <int P, bool VEC>
 void launch_wave_position(dim3 grid, dim3 block, hipStream_t st,
                           const int32_t *ro, const int32_t *col,
                           const float *val, const float *x, float *y,
@@ -779,6 +1007,40 @@ int launch_spmv(const int32_t *ro, const int32_t *col, const float *val,
                          dim3((unsigned)B), 0, st, ro, col, val, x, y, n,
                          (int32_t)nnz, (int32_t)std::min<int64_t>(chunk, nnz));
     return launch_check("thread-per-position SpMV kernel");
+  }
+  if (streq(o.spmv_mapping, "wave-per-row-balanced")) {
+    if (nnz == 0) // every row is empty
+      return launch_fill_zero(y, rows, B, st);
+    const int64_t P = o.spmv_positions_per_lane;
+    const int64_t chunk = kWave * P * kRowOwnerSteps;
+    const int64_t waves = ceil_div(nnz, chunk);
+    // the kernel is compiled for at most 256 threads per workgroup
+    const int64_t OB = std::min<int64_t>(B, 256);
+    const int64_t grid = ceil_div(waves, OB / kWave);
+    rc = check_grid(grid, "wave-per-row-balanced SpMV");
+    if (rc)
+      return rc;
+    const bool vec = aligned16(col) && aligned16(val) && narrow &&
+                     narrow_offsets(nnz, 1);
+    dim3 g((unsigned)grid), b((unsigned)OB);
+    const int32_t z = (int32_t)nnz;
+    switch (P) {
+    case 1: launch_row_owner<1, false>(g, b, st, ro, col, val, x, y, n, z, chunk, waves); break;
+    case 2: launch_row_owner<2, false>(g, b, st, ro, col, val, x, y, n, z, chunk, waves); break;
+    case 4:
+      if (vec) launch_row_owner<4, true>(g, b, st, ro, col, val, x, y, n, z, chunk, waves);
+      else launch_row_owner<4, false>(g, b, st, ro, col, val, x, y, n, z, chunk, waves);
+      break;
+    case 8:
+      if (vec) launch_row_owner<8, true>(g, b, st, ro, col, val, x, y, n, z, chunk, waves);
+      else launch_row_owner<8, false>(g, b, st, ro, col, val, x, y, n, z, chunk, waves);
+      break;
+    default:
+      if (vec) launch_row_owner<16, true>(g, b, st, ro, col, val, x, y, n, z, chunk, waves);
+      else launch_row_owner<16, false>(g, b, st, ro, col, val, x, y, n, z, chunk, waves);
+      break;
+    }
+    return launch_check("wave-per-row-balanced SpMV kernel");
   }
   // wave-per-position
   const int64_t P = o.spmv_positions_per_lane;

@@ -39,6 +39,15 @@ MAPPINGS = [
     "spmv-mapping=wave-per-position spmv-positions-per-lane=8",
     "spmv-mapping=wave-per-position spmv-positions-per-lane=16 "
     "spmv-block-size=512",
+    # row owner (Wave64 extension): every row stored once, no fill
+    "spmv-mapping=wave-per-row-balanced",
+    "spmv-mapping=wave-per-row-balanced spmv-positions-per-lane=4 "
+    "spmv-block-size=64",
+    "spmv-mapping=wave-per-row-balanced spmv-positions-per-lane=2 "
+    "spmv-block-size=128",
+    "spmv-mapping=wave-per-row-balanced spmv-positions-per-lane=8",
+    "spmv-mapping=wave-per-row-balanced spmv-positions-per-lane=16 "
+    "spmv-block-size=1024",
 ]
 
 
@@ -161,13 +170,14 @@ def test_unaligned_operands(dev, orc):
     valp[1:] = G.t(csr.values)
     col, val = colp[1:], valp[1:]
     assert col.data_ptr() % 16 != 0
-    for p in (4, 8, 16):
-        G.say(f"unaligned wave-per-position P={p}")
-        y = torch.full((csr.rows,), float("nan"), device=G.DEV)
-        sw.spmv(ro, col, val, G.t(x), y, options=(
-            f"spmv-mapping=wave-per-position spmv-positions-per-lane={p}"))
-        torch.cuda.synchronize()
-        _check(orc, csr, x, y.cpu().numpy())
+    for mapping in ("wave-per-position", "wave-per-row-balanced"):
+        for p in (4, 8, 16):
+            G.say(f"unaligned {mapping} P={p}")
+            y = torch.full((csr.rows,), float("nan"), device=G.DEV)
+            sw.spmv(ro, col, val, G.t(x), y, options=(
+                f"spmv-mapping={mapping} spmv-positions-per-lane={p}"))
+            torch.cuda.synchronize()
+            _check(orc, csr, x, y.cpu().numpy())
 
 
 def test_vector_past_four_gib(dev):
@@ -203,7 +213,11 @@ def test_vector_past_four_gib(dev):
         assert_within_bound(yc.cpu().numpy(), ref, bound)
     for opts in ("spmv-mapping=thread-per-row", "spmv-mapping=wave-per-row",
                  "spmv-mapping=wave-per-row spmv-lanes-per-row=4",
-                 "spmv-mapping=block-per-row spmv-block-size=128"):
+                 "spmv-mapping=block-per-row spmv-block-size=128",
+                 "spmv-mapping=wave-per-row-balanced "
+                 "spmv-positions-per-lane=4",
+                 "spmv-mapping=wave-per-row-balanced "
+                 "spmv-positions-per-lane=1"):
         G.say(f"x of {cols} floats, {opts}")
         y = torch.full((rows,), float("nan"), device=G.DEV)
         sw.spmv(G.t(ro), G.t(col), G.t(val), x, y, options=opts)
@@ -231,8 +245,10 @@ def test_positions_past_four_gib(dev):
     x = torch.ones(cols, dtype=torch.float32, device=G.DEV)
     ro32 = ro.to(torch.int32)
     del ro
-    for p in (4, 8):
-        opts = f"spmv-mapping=wave-per-position spmv-positions-per-lane={p}"
+    for opts in ("spmv-mapping=wave-per-position spmv-positions-per-lane=4",
+                 "spmv-mapping=wave-per-position spmv-positions-per-lane=8",
+                 "spmv-mapping=wave-per-row-balanced "
+                 "spmv-positions-per-lane=4"):
         G.say(f"nnz={nnz}, {opts}")
         y = torch.full((rows,), float("nan"), device=G.DEV)
         sw.spmv(ro32, col, val, x, y, options=opts)
@@ -260,6 +276,11 @@ def config2():
     "spmv-mapping=wave-per-position spmv-positions-per-lane=8 "
     "spmv-block-size=64",
     "spmv-mapping=wave-per-position spmv-positions-per-lane=16",
+    "spmv-mapping=wave-per-row-balanced spmv-positions-per-lane=4 "
+    "spmv-block-size=64",
+    "spmv-mapping=wave-per-row-balanced spmv-positions-per-lane=8 "
+    "spmv-block-size=256",
+    "spmv-mapping=wave-per-row-balanced spmv-positions-per-lane=1",
 ])
 def test_config2_full_size(dev, orc, config2, opts):
     csr, x = config2
