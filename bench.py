@@ -636,6 +636,33 @@ def main():
                 except Exception as e:
                     rocsparse[key] = {"error": str(e)}
             del rhs, out
+        # the lrrt bundle of this configuration (K = 4, wave-per-row-tile,
+        # tile 4; built in-tree by __graft_entry__.build()), launched as
+        # lrrt does: Bundle::launch(n = rows, args) on the same buffers
+        try:
+            from sparsewavecomp_amd import bundle as BU
+            from sparsewavecomp_amd.bundle.runtime import Bundle
+            bun = Bundle(BU.CONFIG3_BUNDLE)
+            rhs = T(W.config3_rhs(m, 4, seed=0))
+            out = torch.empty((n, 4), device=dev)
+            ptrs = {"rowOffsets": ro.data_ptr(), "columnIndices": col.data_ptr(),
+                    "values": val.data_ptr(), "rhs": rhs.data_ptr(),
+                    "output": out.data_ptr()}
+            st = torch.cuda.current_stream().cuda_stream
+            log("SpMM K=4 lrrt bundle (launch(n, args))")
+            ms = time_steps(lambda: bun.launch("spmm", n, ptrs, stream=st),
+                            max(K // 2, 1), Wm, WARM_MS)
+            b = W.algorithmic_bytes_spmm(n, m, nnz, 4)
+            workloads["spmm_config3_k4"][
+                "lrrt bundle: wave-per-row-tile tile 4 (launch(n, args))"] = {
+                "ms": ms, "GB/s": b / ms / 1e6,
+                "GFLOP/s": 2 * nnz * 4 / ms / 1e6,
+                "hbm_frac": b / ms / 1e6 / HBM_PEAK_GBS}
+            log(f"  {ms * 1e3:.1f} us  {b / ms / 1e6:.0f} GB/s")
+            bun.close()
+            del rhs, out
+        except Exception as e:  # the bundle is reported when it was built
+            workloads["spmm_config3_k4"]["lrrt bundle error"] = str(e)
         del ro, col, val, xv, y
         torch.cuda.empty_cache()
 

@@ -329,6 +329,25 @@ def build_spmm_bundle(output, rows: int, rhs_columns: int,
     return manifest
 
 
+# The SpMM bundle of benchmark configuration 3 at K = 4 (the bundle's
+# wave-per-row-tile, tile 4 case over 1,048,576 rows), built in-tree by
+# __graft_entry__.build() so that bench.py and the GPU tests load it without
+# a compiler.
+CONFIG3_ROWS = 1 << 20
+CONFIG3_BUNDLE = Path(__file__).resolve().parent / "prebuilt" / \
+    "spmm_config3_k4"
+
+
+def build_config3_bundle() -> Path:
+    """(Re)build the configuration-3 bundle in place."""
+    if CONFIG3_BUNDLE.exists():
+        shutil.rmtree(CONFIG3_BUNDLE)
+    build_spmm_bundle(CONFIG3_BUNDLE, rows=CONFIG3_ROWS, rhs_columns=4,
+                      tile_size=4)
+    verify_bundle(CONFIG3_BUNDLE)
+    return CONFIG3_BUNDLE
+
+
 def attention_buffers(rows, key_rows, head_dim, value_cols) -> dict:
     """The ten-buffer ABI with dtype/shape/kind (sparsewave_bundle_ir.py:82-93,
     specialised shapes as parse_sparse_attention_ir_text records them)."""

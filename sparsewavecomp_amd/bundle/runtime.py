@@ -1,5 +1,7 @@
-"""A stand-in for the lrrt runtime's Bundle::launch(n, args), used to run
-bundles produced by sparsewavecomp_amd.bundle on the GPU in tests.
+"""A Python consumer of the bundles sparsewavecomp_amd.bundle produces: the
+launch side of the lrrt runtime's Bundle::launch(n, args)
+(README.md:111-140 in the reference), used by the GPU tests and by
+bench.py to run a bundle the way lrrt would.
 
 It follows the manifest exactly as a consumer would: evaluate the grid
 expression (total work-items) for n, divide by the block, pack each

@@ -11,7 +11,7 @@ from sparsewavecomp_amd import workloads as W
 from tests import gpu_util as G
 from tests._attention_check import check_attention_f32
 from tests._check import assert_within_bound
-from tests.lrrt_stub import Bundle
+from sparsewavecomp_amd.bundle.runtime import Bundle
 
 pytestmark = pytest.mark.gpu
 
@@ -74,3 +74,41 @@ def test_attention_bundle_matches_oracle(dev, orc, tmp_path):
                         *(bufs[k].cpu().numpy() for k in (
                             "scores", "rowMaximum", "rowSum", "output")))
     assert math.isfinite(float(bufs["rowSum"].sum()))
+
+
+def test_config3_bundle_at_full_size(dev, orc):
+    """The in-tree bundle of configuration 3 at K = 4 (1,048,576 rows, the
+    configuration-2 matrix times 4 RHS columns), launched as lrrt does with
+    n = rows: 20,000 random rows and the 50 longest checked against the
+    oracle within the fp32 bound, every row written."""
+    from tests.test_gpu_spmm import _row_subset
+    if not (B.CONFIG3_BUNDLE / "manifest.json").exists():
+        pytest.fail("the configuration-3 bundle is not built "
+                    "(__graft_entry__.build() writes it)")
+    B.verify_bundle(B.CONFIG3_BUNDLE)
+    csr, _ = W.config2(seed=0)
+    assert csr.rows == B.CONFIG3_ROWS
+    rhs = W.config3_rhs(csr.cols, 4, seed=0)
+    bun = Bundle(B.CONFIG3_BUNDLE)
+    ro, col, val, b = (G.t(csr.row_offsets), G.t(csr.column_indices),
+                       G.t(csr.values), G.t(rhs))
+    out = torch.full((csr.rows, 4), float("nan"), device=G.DEV)
+    G.say("configuration-3 bundle, 1,048,576 rows, K = 4")
+    bun.launch("spmm", csr.rows, {"rowOffsets": ro.data_ptr(),
+                                  "columnIndices": col.data_ptr(),
+                                  "values": val.data_ptr(),
+                                  "rhs": b.data_ptr(),
+                                  "output": out.data_ptr()})
+    torch.cuda.synchronize()
+    bun.close()
+    got = out.cpu().numpy()
+    assert np.all(np.isfinite(got))
+    rows = np.sort(np.random.default_rng(3).choice(csr.rows, 20000,
+                                                   replace=False))
+    rows = np.concatenate([rows, np.argsort(np.diff(csr.row_offsets))[-50:]])
+    sub = _row_subset(csr, rows)
+    ref = orc.spmm(sub.row_offsets, sub.column_indices, sub.values, rhs)
+    bound = orc.spmm_abs_bound(sub.row_offsets, sub.column_indices,
+                               sub.values, rhs)
+    assert_within_bound(got[rows], ref, bound)
+
