@@ -62,8 +62,11 @@ def parse():
                          "harness's SuiteSparse workloads)")
     ap.add_argument("--profile", default="",
                     choices=["", "spmv", "floor", "coo", "spmm", "bsr",
-                             "bsr-bf16", "bsr-bf16-f32out", "attention",
-                             "attention-bf16", "sddmm", "sddmm-bf16", "copy",
+                             "bsr-bf16", "bsr-bf16-f32out", "bsr-floor",
+                             "bsr-bf16-floor", "bsr-bf16-f32out-floor",
+                             "attention", "attention-bf16",
+                             "attention-floor", "attention-bf16-floor",
+                             "sddmm", "sddmm-bf16", "copy",
                              "reference-sweep"],
                     help="run one workload --steps times with no timing or "
                          "JSON (for rocprofv3 kernel-trace / pmc runs)")
@@ -206,17 +209,23 @@ def profile(args):
             out = torch.empty((csr.rows, args.k), device=dev)
             for _ in range(n):
                 sw.spmm(ro, col, val, rhs, out, options=o)
-    elif w in ("bsr", "bsr-bf16", "bsr-bf16-f32out"):
+    elif w.startswith("bsr"):
+        # bsr, bsr-bf16, bsr-bf16-f32out; "-floor" runs the slab floor
+        floor = w.endswith("-floor")
+        kind = w[:-len("-floor")] if floor else w
         bsr, rhs = W.config4(seed=0)
-        dt = torch.bfloat16 if w != "bsr" else None
+        dt = torch.bfloat16 if kind != "bsr" else None
         a4 = (T(bsr.block_row_offsets), T(bsr.block_column_indices),
               T(bsr.block_values, dt), T(rhs, dt))
         out = torch.empty((bsr.rows, 128), device=dev,
-                          dtype=torch.bfloat16 if w == "bsr-bf16"
+                          dtype=torch.bfloat16 if kind == "bsr-bf16"
                           else torch.float32)
         o = sw.Options.parse(args.opts)
         for _ in range(n):
-            sw.bsr_spmm(*a4, out, 16, options=o)
+            if floor:
+                sw.bsr_slab_floor(*a4, out)
+            else:
+                sw.bsr_spmm(*a4, out, 16, options=o)
     elif w == "reference-sweep":
         dist, per_row = args.workload.split("/")
         csr = W.reference_sweep_matrix(dist, int(per_row))
@@ -249,9 +258,12 @@ def profile(args):
             for _ in range(steps):
                 run()
         mark()
-    elif w in ("attention", "attention-bf16"):
+    elif w.startswith("attention"):
+        # attention, attention-bf16; "-floor" runs the tile floor
+        floor = w.endswith("-floor")
+        kind = w[:-len("-floor")] if floor else w
         mask, q, kt, v, alpha = W.config5(seed=0)
-        dt = torch.bfloat16 if w == "attention-bf16" else torch.float32
+        dt = torch.bfloat16 if kind == "attention-bf16" else torch.float32
         att = (T(mask.row_offsets), T(mask.column_indices),
                T(mask.values, dt), T(q, dt), T(kt, dt), T(v, dt))
         s = torch.empty(mask.nnz, device=dev, dtype=dt)
@@ -262,7 +274,11 @@ def profile(args):
             "sddmm-mapping=row-tile-mfma sddmm-lanes-per-row=64 "
             "spmm-mapping=row-tile-mfma"))
         for _ in range(n):
-            sw.sparse_attention(*att, s, rm, rs, out, alpha, 0.0, options=o)
+            if floor:
+                sw.attention_tile_floor(*att, s, rm, rs, out)
+            else:
+                sw.sparse_attention(*att, s, rm, rs, out, alpha, 0.0,
+                                    options=o)
     elif w in ("sddmm", "sddmm-bf16"):
         mask, q, kt, v, alpha = W.config5(seed=0)
         dt = torch.bfloat16 if w == "sddmm-bf16" else torch.float32
@@ -697,6 +713,13 @@ def main():
                 "roofline_ceiling_TFLOP/s": ceiling,
                 "roofline_frac": tf / ceiling}
             log(f"  {ms * 1e3:.1f} us  {tf:.1f} TFLOP/s")
+            # the slab floor: the same launch with the block products
+            # replaced by an XOR of the loaded words (memory trips only)
+            msf = time_steps(lambda: sw.bsr_slab_floor(*args4, out4), K, Wm,
+                             WARM_MS)
+            workloads[f"bsr_config4_{name}"]["slab_floor"] = {
+                "ms": msf, "kernel_over_floor": ms / msf}
+            log(f"  slab floor {msf * 1e3:.1f} us")
             if name != "bf16_f32out":
                 # the reference's mapping (thread-per-output) on the same call
                 o0 = sw.Options(bsr_use_mfma=0)
@@ -732,6 +755,14 @@ def main():
                 workloads.setdefault("attention_config5", {})[key] = {
                     "ms": ms, "GFLOP/s": 4 * mask.nnz * 64 / ms / 1e6}
                 log(f"  {ms * 1e3:.1f} us")
+                if opts:
+                    # the tile floor: the fused kernel's loads, structure
+                    # check and stores with XORs in place of the math
+                    msf = time_steps(lambda: sw.attention_tile_floor(
+                        *att, scores, rmax, rsum, outa), K, Wm, WARM_MS)
+                    workloads["attention_config5"][key]["tile_floor"] = {
+                        "ms": msf, "kernel_over_floor": ms / msf}
+                    log(f"  tile floor {msf * 1e3:.1f} us")
             # the chain's first op on its own: scores = alpha Q K^T on the
             # mask's positions
             for opts in ["", "sddmm-mapping=row-tile-mfma"]:

@@ -230,6 +230,25 @@ int sw_bsr_spmm_bf16_f32out(const int32_t *block_row_offsets,
                             int64_t nnzb, int64_t k, int64_t block_size,
                             const sw_options *opts, void *stream);
 
+/*
+ * BSR slab floor, a diagnostic with no counterpart in the reference: the
+ * launch that sw_bsr_spmm_f32 / _bf16 / _bf16_f32out make on the matrix
+ * cores for these operands (16 x 16 blocks; value_bytes 4 with k % 4 == 0,
+ * or 2 with k % 8 == 0; 16-byte aligned rhs and output; output_bytes 4, or 2
+ * for the bf16 output) with its grid, block order, block and RHS-slab
+ * loads, LDS reduction and stores unchanged and the block products replaced
+ * by an XOR of the 32-bit words each lane loads.  Every output element of a
+ * lane's region holds that XOR (its low 16 bits for a bf16 output); the
+ * regions and the words follow the MFMA kernels' lane layout.  Its time is
+ * the floor of the kernels' memory trips; bench.py reports the BSR SpMM
+ * against it.
+ */
+int sw_bsr_slab_floor(const int32_t *block_row_offsets,
+                      const int32_t *block_column_indices,
+                      const void *block_values, const void *rhs, void *output,
+                      int64_t rows, int64_t cols, int64_t nnzb, int64_t k,
+                      int value_bytes, int output_bytes, void *stream);
+
 /* Scalar regions the reference attaches to sddmm
  * (SparseWaveOps.td:171-223).  SW_SDDMM_AFFINE is the attention form
  * sample*beta + dot*alpha (SparseAttentionToSparseWave.cpp:270-283). */
@@ -352,6 +371,29 @@ int sw_sparse_attention_bf16(const int32_t *row_offsets,
                              int64_t nnz, int64_t d, int64_t dv, float alpha,
                              float beta, const sw_options *opts,
                              void *stream);
+
+/*
+ * Attention tile floor, a diagnostic with no counterpart in the reference:
+ * the fused one-kernel launch of sw_sparse_attention_f32 (value_bytes 4) or
+ * _bf16 (value_bytes 2) for these buffers -- d of 64 or 128, dv a multiple
+ * of 16 (fp32) or 64 (bf16, with 16-byte aligned query and 8-byte aligned
+ * value and output), nnz >= 4 -- with its loads, structure check and
+ * barrier, score / row / output stores and output reduction unchanged, and
+ * every product, exponential and division replaced by an XOR of the words
+ * each lane loads (so the two softmax barriers go too).  The outputs hold
+ * those XORs as bit patterns; tiles whose rows do not share the last row's
+ * columns take the fused kernel's row path and compute the chain.  Its
+ * time is the floor of the tile's chain of memory trips; bench.py reports
+ * the fused attention against it.
+ */
+int sw_attention_tile_floor(const int32_t *row_offsets,
+                            const int32_t *column_indices,
+                            const void *mask_values, const void *query,
+                            const void *transposed_key, const void *value,
+                            void *scores, void *row_maximum, void *row_sum,
+                            void *output, int64_t rows, int64_t cols,
+                            int64_t nnz, int64_t d, int64_t dv,
+                            int value_bytes, void *stream);
 
 /*
  * sparsewave.csr_row_at_position for a batch of positions:

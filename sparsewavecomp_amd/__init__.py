@@ -18,7 +18,7 @@ import os
 __all__ = [
     "Options", "SparseWaveError", "ShapeError", "library_path",
     "load_library", "spmv",
-    "coo_spmv", "spmv_gather_floor",
+    "coo_spmv", "spmv_gather_floor", "bsr_slab_floor", "attention_tile_floor",
     "spmm", "bsr_spmm", "sddmm", "csr_row_reduce", "csr_rowwise_map",
     "sparse_attention", "csr_row_at_position", "SDDMM_MUL", "SDDMM_AFFINE",
     "SDDMM_DOT", "MAP_EXP_SUB", "MAP_DIV", "MAP_SUB", "MAP_MUL",
@@ -36,11 +36,12 @@ EXPORTED_SYMBOLS = (
     "sw_validate_options", "sw_last_error", "sw_version", "sw_spmv_csr_f32",
     "sw_spmv_coo_f32", "sw_spmv_gather_floor_f32",
     "sw_spmm_csr_f32", "sw_spmm_csr_bf16", "sw_bsr_spmm_f32",
-    "sw_bsr_spmm_bf16", "sw_bsr_spmm_bf16_f32out", "sw_sddmm_csr_f32",
+    "sw_bsr_spmm_bf16", "sw_bsr_spmm_bf16_f32out", "sw_bsr_slab_floor",
+    "sw_sddmm_csr_f32",
     "sw_sddmm_csr_bf16", "sw_csr_row_reduce_f32", "sw_csr_row_reduce_bf16",
     "sw_csr_rowwise_map_f32", "sw_csr_rowwise_map_bf16",
     "sw_sparse_attention_f32", "sw_sparse_attention_bf16",
-    "sw_csr_row_at_position",
+    "sw_csr_row_at_position", "sw_attention_tile_floor",
     "sw_host_matrix_free", "sw_host_bsr_free", "sw_matrix_market_read",
     "sw_csr_binary_write", "sw_coo_binary_write", "sw_csr_binary_read",
     "sw_coo_binary_read", "sw_convert_to_bsr", "sw_bsr_binary_write",
@@ -116,6 +117,11 @@ def load_library():
         "sw_spmv_coo_f32": (ctypes.c_int, [P, P, P, P, P, I64, I64, I64, OP,
                                            P]),
         "sw_spmv_gather_floor_f32": (ctypes.c_int, [P, P, P, P, I64, P]),
+        "sw_bsr_slab_floor": (ctypes.c_int, [P, P, P, P, P, I64, I64, I64,
+                                             I64, ctypes.c_int, ctypes.c_int,
+                                             P]),
+        "sw_attention_tile_floor": (ctypes.c_int, [P] * 10 + [I64] * 5 + [
+            ctypes.c_int, P]),
         "sw_spmm_csr_f32": (ctypes.c_int, [P, P, P, P, P, I64, I64, I64, I64,
                                            OP, P]),
         "sw_spmm_csr_bf16": (ctypes.c_int, [P, P, P, P, P, I64, I64, I64, I64,
@@ -379,6 +385,71 @@ def bsr_spmm(block_row_offsets, block_column_indices, block_values, rhs,
               _dev(block_values, dt, "block_values"), _dev(rhs, dt, "rhs"),
               _dev(output, odt, "output"), rows, rhs.shape[0], nnzb,
               rhs.shape[1], block_size, _opts(options), _stream(stream)))
+    return output
+
+
+def bsr_slab_floor(block_row_offsets, block_column_indices, block_values,
+                   rhs, output, stream=None):
+    """Diagnostic (no reference counterpart): the matrix-core BSR SpMM
+    launch for these operands (16 x 16 blocks) with its loads, reduction and
+    stores as they are and the block products replaced by an XOR of the
+    words each lane loads (sw_bsr_slab_floor); the output holds those XORs
+    as bit patterns.  float32 operands, or bfloat16 block values and rhs with
+    a bfloat16 or float32 output."""
+    import torch
+    rows = _rows_of(block_row_offsets, "block_row_offsets") * 16
+    nnzb = block_column_indices.numel()
+    dt = _value_dtype(block_values, "block_values")
+    _need(block_values.numel() == nnzb * 256,
+          "block values must hold nnzb * 16 * 16 entries")
+    _need(rhs.dim() == 2 and output.dim() == 2 and
+          tuple(output.shape) == (rows, rhs.shape[1]),
+          "expected rhs [cols, k] and output [rows, k]")
+    _need(output.dtype in (torch.float32, torch.bfloat16) and
+          (dt == torch.bfloat16 or output.dtype == torch.float32),
+          "fp32 operands take a float32 output; bf16 a bf16 or float32 one")
+    vb = 4 if dt == torch.float32 else 2
+    ob = 4 if output.dtype == torch.float32 else 2
+    _check(load_library().sw_bsr_slab_floor(
+        _dev(block_row_offsets, torch.int32, "block_row_offsets"),
+        _dev(block_column_indices, torch.int32, "block_column_indices"),
+        _dev(block_values, dt, "block_values"), _dev(rhs, dt, "rhs"),
+        _dev(output, output.dtype, "output"), rows, rhs.shape[0], nnzb,
+        rhs.shape[1], vb, ob, _stream(stream)))
+    return output
+
+
+def attention_tile_floor(row_offsets, column_indices, mask_values, query,
+                         transposed_key, value, scores, row_maximum, row_sum,
+                         output, stream=None):
+    """Diagnostic (no reference counterpart): the fused attention tile
+    kernel for these buffers with its loads, structure check, stores and
+    output reduction as they are and every product, exponential and
+    division replaced by an XOR of the loaded words
+    (sw_attention_tile_floor).  float32 or bfloat16 buffers."""
+    import torch
+    rows = _rows_of(row_offsets)
+    nnz = column_indices.numel()
+    dt = _value_dtype(query, "query")
+    _need(query.dim() == 2 and transposed_key.dim() == 2 and
+          value.dim() == 2 and output.dim() == 2 and
+          query.shape[1] == transposed_key.shape[0] and
+          transposed_key.shape[1] == value.shape[0] and
+          tuple(output.shape) == (rows, value.shape[1]),
+          "expected query [rows, d], transposed_key [d, cols], "
+          "value [cols, dv] and output [rows, dv]")
+    _need(mask_values.numel() == nnz and scores.numel() == nnz and
+          row_maximum.numel() == rows and row_sum.numel() == rows,
+          "mask values and scores hold nnz entries, row buffers rows")
+    _check(load_library().sw_attention_tile_floor(
+        _dev(row_offsets, torch.int32, "row_offsets"),
+        _dev(column_indices, torch.int32, "column_indices"),
+        _dev(mask_values, dt, "mask_values"), _dev(query, dt, "query"),
+        _dev(transposed_key, dt, "transposed_key"), _dev(value, dt, "value"),
+        _dev(scores, dt, "scores"), _dev(row_maximum, dt, "row_maximum"),
+        _dev(row_sum, dt, "row_sum"), _dev(output, dt, "output"), rows,
+        transposed_key.shape[1], nnz, query.shape[1], value.shape[1],
+        4 if dt == torch.float32 else 2, _stream(stream)))
     return output
 
 

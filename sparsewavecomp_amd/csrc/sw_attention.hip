@@ -614,8 +614,13 @@ constexpr int kFusedChunks = kFusedCols / (16 * kFusedWaves);
 // and dv are unused).  The attention chain takes the affine region.
 // NS (with SO; no sample values, mask is null): every sample reads as zero
 // and no sample window is loaded.
+// FLOOR (the chain only; the tile-floor diagnostic sw_attention_tile_floor):
+// the same loads, structure check, barrier, stores and output reduction,
+// with every product, exponential and division replaced by an XOR of the
+// words the lane loaded and without the softmax's two barriers.  Its time is
+// the floor of the tile's chain of memory trips.
 // (at most 128 VGPRs: the two workgroups of a CU need four waves per SIMD)
-template <int KB, int W, bool IL, bool SO, bool NS = false>
+template <int KB, int W, bool IL, bool SO, bool NS = false, bool FLOOR = false>
 __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused(
     const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
     const float *__restrict__ mask, const float *__restrict__ q,
@@ -627,6 +632,7 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused(
   static_assert(W == 8 && kFusedCols == 8 * kWave && kFusedChunks == 4,
                 "check layout");
   static_assert(SO || !NS, "the attention chain reads its mask");
+  static_assert(!(SO && FLOOR), "the floor runs the chain");
   __shared__ float part[W][4][4][kWave]; // [wave][n tile][v][lane]
   __shared__ float wred[2][W][16];       // [max, sum][wave][row]
   __shared__ int32_t lcol[kFusedCols];   // the last row's columns
@@ -806,6 +812,16 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused(
   float sv[kFusedChunks][4];
   auto sddmm_chunk = [&](int k, const float (&a)[16 * KB], const v4f &w)
       __attribute__((always_inline)) {
+    if constexpr (FLOOR) {
+      uint32_t x = 0;
+#pragma unroll
+      for (int st = 0; st < 16 * KB; ++st)
+        x ^= __float_as_uint(a[st]);
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        sv[k][v] = __uint_as_float(x ^ __float_as_uint(w[v]));
+      return;
+    }
     v4f acc = {0.f, 0.f, 0.f, 0.f};
     if (chunk_t0(k) < len_last) { // wave-uniform
       // two independent chains of products (even and odd K steps): one
@@ -889,6 +905,34 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused(
   // than four waves per SIMD leave)
   load_v(0, 0, bv[0]);
   load_v(1, 0, bv[1]);
+  if constexpr (FLOOR) {
+    // the scores' stores and the row outputs' stores, no softmax
+    uint32_t x = 0;
+#pragma unroll
+    for (int k = 0; k < kFusedChunks; ++k) {
+      if (chunk_t0(k) >= len_last) // wave-uniform
+        continue;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        sv[k][v] = valid(k, v) ? sv[k][v] : 0.0f;
+        x ^= __float_as_uint(sv[k][v]);
+      }
+      float *dst = scores + rbase + chunk_t0(k) + 4 * g;
+      if (valid(k, 3)) {
+        const v4f y = v4f{sv[k][0], sv[k][1], sv[k][2], sv[k][3]};
+        __builtin_memcpy(dst, &y, sizeof y);
+      } else {
+#pragma unroll
+        for (int v = 0; v < 3; ++v)
+          if (valid(k, v))
+            dst[v] = sv[k][v];
+      }
+    }
+    if (wave == 0 && g == 0 && i < nt) {
+      rmax[r0 + i] = __uint_as_float(x);
+      rsum[r0 + i] = __uint_as_float(x);
+    }
+  } else {
   // B. row softmax: lanes (i, 0..3) of every wave hold row i's entries
   {
     float m = -INFINITY;
@@ -965,10 +1009,22 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused(
       rsum[r0 + i] = sum;
     }
   }
+  } // FLOOR
   // C. output = P V with P from sv (lane (i, g) holds P[i][t0(k)+4g+st],
   // the A operand of step st); the waves' partial tiles are summed in LDS
   auto mfma_chunk = [&](int k, const float (&b)[4][4], v4f (&acc)[4])
       __attribute__((always_inline)) {
+    if constexpr (FLOOR) {
+      if (chunk_t0(k) < len_last) // wave-uniform
+#pragma unroll
+        for (int n = 0; n < 4; ++n)
+#pragma unroll
+          for (int st = 0; st < 4; ++st)
+            acc[n][st] = __uint_as_float(__float_as_uint(acc[n][st]) ^
+                                         __float_as_uint(sv[k][st]) ^
+                                         __float_as_uint(b[n][st]));
+      return;
+    }
     if (chunk_t0(k) < len_last) // wave-uniform
 #pragma unroll
       for (int n = 0; n < 4; ++n)
@@ -976,6 +1032,13 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused(
         for (int st = 0; st < 4; ++st)
           acc[n] = __builtin_amdgcn_mfma_f32_16x16x4f32(sv[k][st], b[n][st],
                                                         acc[n], 0, 0, 0);
+  };
+  // the waves' partial tiles combine by sum (by XOR in the floor)
+  auto combine = [&](float a, float b) __attribute__((always_inline)) {
+    if constexpr (FLOOR)
+      return __uint_as_float(__float_as_uint(a) ^ __float_as_uint(b));
+    else
+      return a + b;
   };
   bool nonfinite = false;
   for (int64_t nb = 0; nb < dv; nb += 64) {
@@ -1012,9 +1075,9 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused(
           float sum = 0.0f;
 #pragma unroll
           for (int w = 0; w < W; ++w)
-            sum += part[w][n][wave][l];
+            sum = combine(sum, part[w][n][wave][l]);
           o[n] = sum;
-          nf |= !__builtin_isfinite(sum);
+          nf |= !FLOOR && !__builtin_isfinite(sum);
         }
         const int rr = 4 * g + wave;
         if (rr < nt) {
@@ -1031,11 +1094,11 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused(
         float sum = 0.0f;
 #pragma unroll
         for (int w = 0; w < W; ++w)
-          sum += part[w][wave][v][l];
+          sum = combine(sum, part[w][wave][v][l]);
         const int rr = 4 * g + v;
         if (rr < nt) {
           out[(int64_t)(r0 + rr) * dv + nb + 16 * wave + i] = sum;
-          nonfinite |= !__builtin_isfinite(sum);
+          nonfinite |= !FLOOR && !__builtin_isfinite(sum);
         }
       }
       if (__builtin_amdgcn_ballot_w64(nonfinite) != 0 && l == 0)
@@ -1189,7 +1252,8 @@ __global__ __launch_bounds__(64 * W) void sddmm_tile_mfma_bf16(
 // K^T (2 * d * cols) and V (2 * cols * dv) fit 32 bits, that nnz >= 4
 // (amax = nnz - 4) and that Q is 16-byte and V 8-byte aligned.
 // (at most 128 VGPRs: the two workgroups of a CU need four waves per SIMD)
-template <int KB, int W, bool SO, bool NS = false>
+// FLOOR: the tile-floor diagnostic, as for the fp32 kernel above.
+template <int KB, int W, bool SO, bool NS = false, bool FLOOR = false>
 __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused_bf16(
     const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
     const uint16_t *__restrict__ mask, const uint16_t *__restrict__ q,
@@ -1205,6 +1269,7 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused_bf16(
   // is null), every sample reads as zero
   const int region = SO ? kind : SW_SDDMM_AFFINE;
   static_assert(SO || !NS, "the attention chain reads its mask");
+  static_assert(!(SO && FLOOR), "the floor runs the chain");
   __shared__ float part[W][4][4][kWave]; // [wave][n tile][v][lane]
   __shared__ float wred[2][W][16];       // [max, sum][wave][row]
   __shared__ int wshared[W]; // each wave's rows share the last row's columns
@@ -1288,6 +1353,16 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused_bf16(
   float sv[kFusedChunks][4];
   auto sddmm_chunk = [&](int k, const v4u (&a)[S])
       __attribute__((always_inline)) {
+    if constexpr (FLOOR) {
+      uint32_t x = (uint32_t)mw[k] ^ (uint32_t)(mw[k] >> 32);
+#pragma unroll
+      for (int s2 = 0; s2 < S; ++s2)
+        x ^= a[s2].x ^ a[s2].y ^ a[s2].z ^ a[s2].w;
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        sv[k][v] = __uint_as_float(x ^ (uint32_t)v);
+      return;
+    }
     v4f acc = {0.f, 0.f, 0.f, 0.f};
     if (chunk_t0(k) < len_last) { // wave-uniform
 #pragma unroll
@@ -1396,7 +1471,7 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused_bf16(
       load_v(0, 0, bv[0]);
       load_v(1, 0, bv[1]);
     }
-    if constexpr (!SO) {
+    if constexpr (!SO && !FLOOR) {
       // B. row softmax on the stored (bf16) scores, each op's result
       // rounded: this wave's row maxima
       float m = -INFINITY;
@@ -1451,7 +1526,29 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused_bf16(
     }
     return;
   }
-  {
+  if constexpr (FLOOR) {
+    // the scores' stores and the row outputs' stores, no softmax
+    uint32_t x = 0;
+#pragma unroll
+    for (int k = 0; k < kFusedChunks; ++k) {
+      pk[k] = v2u{valid(k, 0) ? __float_as_uint(sv[k][0]) : 0u,
+                  valid(k, 2) ? __float_as_uint(sv[k][2]) : 0u};
+      x ^= pk[k].x ^ pk[k].y;
+      uint16_t *dst = scores + rbase + chunk_t0(k) + 4 * g;
+      if (valid(k, 3)) {
+        __builtin_memcpy(dst, &pk[k], sizeof pk[k]);
+      } else {
+#pragma unroll
+        for (int v = 0; v < 3; ++v)
+          if (valid(k, v))
+            dst[v] = (uint16_t)(pk[k][v >> 1] >> (16 * (v & 1)));
+      }
+    }
+    if (wave == 0 && g == 0 && i < nt) {
+      rmax[r0 + i] = (uint16_t)x;
+      rsum[r0 + i] = (uint16_t)(x >> 16);
+    }
+  } else {
     float m = wred[0][0][i];
 #pragma unroll
     for (int w = 1; w < W; ++w)
@@ -1511,6 +1608,16 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused_bf16(
   // C. output = P V: P from pk (lane (i, g) holds P[i][t0(k) + 4g + st])
   auto mfma_chunk = [&](int k, const v2u (&b)[4], v4f (&acc)[4])
       __attribute__((always_inline)) {
+    if constexpr (FLOOR) {
+      if (chunk_t0(k) < len_last) // wave-uniform
+#pragma unroll
+        for (int n = 0; n < 4; ++n)
+#pragma unroll
+          for (int st = 0; st < 4; ++st)
+            acc[n][st] = __uint_as_float(__float_as_uint(acc[n][st]) ^
+                                         pk[k][st >> 1] ^ b[n][st & 1]);
+      return;
+    }
     if (chunk_t0(k) < len_last) { // wave-uniform
 #pragma unroll
       for (int n = 0; n < 4; ++n) {
@@ -1551,15 +1658,22 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused_bf16(
       for (int n = 0; n < 4; ++n) {
         float sum = 0.0f;
 #pragma unroll
-        for (int w = 0; w < W; ++w)
-          sum += part[w][n][wave][l];
+        for (int w = 0; w < W; ++w) {
+          if constexpr (FLOOR) // the waves' partial words combine by XOR
+            sum = __uint_as_float(__float_as_uint(sum) ^
+                                  __float_as_uint(part[w][n][wave][l]));
+          else
+            sum += part[w][n][wave][l];
+        }
         o[n] = sum;
-        nf |= !__builtin_isfinite(sum);
+        nf |= !FLOOR && !__builtin_isfinite(sum);
       }
       const int rr = 4 * g + wave;
       if (rr < nt) {
         *reinterpret_cast<v2u *>(out + (int64_t)(r0 + rr) * dv + nb + 4 * i) =
-            v2u{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+            FLOOR ? v2u{__float_as_uint(o[0]) ^ __float_as_uint(o[1]),
+                        __float_as_uint(o[2]) ^ __float_as_uint(o[3])}
+                  : v2u{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
         nonfinite |= nf;
       }
       if (__builtin_amdgcn_ballot_w64(nonfinite) != 0 && l == 0)
@@ -1935,6 +2049,110 @@ bool launch_fused_attention(const int32_t *ro, const int32_t *col,
   return true;
 }
 
+// The tile floor: the fused kernel launch_fused_attention would run for
+// these operands, in its FLOOR form; false when the shapes do not take the
+// fused kernel.
+bool launch_attention_floor(const int32_t *ro, const int32_t *col,
+                            const float *mask, const float *q,
+                            const float *kt, const float *v, float *scores,
+                            float *rmax, float *rsum, float *out,
+                            int64_t rows, int64_t cols, int64_t nnz,
+                            int64_t d, int64_t dv, hipStream_t st, int *rc) {
+  if (!((d == 64 || d == 128) && dv > 0 && dv % 16 == 0 && nnz >= 4 &&
+        narrow_offsets(nnz, 1) && narrow_offsets(cols, d) &&
+        narrow_offsets(cols, dv)))
+    return false;
+  int64_t grid;
+  *rc = grid_for(rows, 16, "attention tile floor", &grid);
+  if (*rc)
+    return true;
+  const bool il = dv % 64 == 0 && aligned16(v) && aligned16(out);
+#define SW_FLOOR(KB, IL)                                                      \
+  hipLaunchKernelGGL(                                                         \
+      (attention_tile_fused<KB, kFusedWaves, IL, false, false, true>),        \
+      dim3((unsigned)grid), dim3(64 * kFusedWaves), 0, st, ro, col, mask, q,  \
+      kt, v, scores, rmax, rsum, out, (int32_t)rows, cols, (int32_t)d, dv,    \
+      1.0f, 0.0f, (uint32_t)(nnz - 4), (int)SW_SDDMM_AFFINE)
+  if (d == 64 && il)
+    SW_FLOOR(1, true);
+  else if (d == 64)
+    SW_FLOOR(1, false);
+  else if (il)
+    SW_FLOOR(2, true);
+  else
+    SW_FLOOR(2, false);
+#undef SW_FLOOR
+  *rc = launch_check("attention tile floor kernel");
+  return true;
+}
+
+bool launch_attention_floor(const int32_t *ro, const int32_t *col,
+                            const uint16_t *mask, const uint16_t *q,
+                            const uint16_t *kt, const uint16_t *v,
+                            uint16_t *scores, uint16_t *rmax, uint16_t *rsum,
+                            uint16_t *out, int64_t rows, int64_t cols,
+                            int64_t nnz, int64_t d, int64_t dv,
+                            hipStream_t st, int *rc) {
+  if (!((d == 64 || d == 128) && dv > 0 && dv % 64 == 0 && nnz >= 4 &&
+        aligned16(q) &&
+        (reinterpret_cast<uintptr_t>(v) & 7u) == 0 &&
+        (reinterpret_cast<uintptr_t>(out) & 7u) == 0 &&
+        narrow_offsets(nnz, 1) && narrow_offsets(cols, d) &&
+        narrow_offsets(cols, dv)))
+    return false;
+  int64_t grid;
+  *rc = grid_for(rows, 16, "attention tile floor", &grid);
+  if (*rc)
+    return true;
+#define SW_FLOOR(KB)                                                          \
+  hipLaunchKernelGGL(                                                         \
+      (attention_tile_fused_bf16<KB, kFusedWaves, false, false, true>),       \
+      dim3((unsigned)grid), dim3(64 * kFusedWaves), 0, st, ro, col, mask, q,  \
+      kt, v, scores, rmax, rsum, out, (int32_t)rows, cols, (int32_t)d, dv,    \
+      1.0f, 0.0f, (uint32_t)(nnz - 4), (int)SW_SDDMM_AFFINE)
+  if (d == 64)
+    SW_FLOOR(1);
+  else
+    SW_FLOOR(2);
+#undef SW_FLOOR
+  *rc = launch_check("attention tile floor kernel");
+  return true;
+}
+
+template <typename T>
+int attention_floor_entry(const int32_t *row_offsets,
+                          const int32_t *column_indices, const T *mask_values,
+                          const T *query, const T *transposed_key,
+                          const T *value, T *scores, T *row_maximum,
+                          T *row_sum, T *output, int64_t rows, int64_t cols,
+                          int64_t nnz, int64_t d, int64_t dv, void *stream) {
+  int rc = check_csr(row_offsets, column_indices, mask_values, rows, nnz,
+                     true);
+  if (!rc)
+    rc = check_value_alignment(sizeof(T), {mask_values, query, transposed_key,
+                                           value, scores, row_maximum,
+                                           row_sum, output});
+  if (rc)
+    return rc;
+  if (cols < 0 || d < 0 || dv < 0 || d > INT32_MAX)
+    return fail(SW_ERR_INVALID_SHAPE, "invalid attention shapes");
+  if (rows == 0)
+    return SW_OK;
+  if (!row_maximum || !row_sum || !output || !scores || !query ||
+      !transposed_key || !value)
+    return fail(SW_ERR_INVALID_ARGUMENT, "attention buffer pointer is null");
+  if (!launch_attention_floor(row_offsets, column_indices, mask_values, query,
+                              transposed_key, value, scores, row_maximum,
+                              row_sum, output, rows, cols, nnz, d, dv,
+                              as_stream(stream), &rc))
+    return fail(SW_ERR_INVALID_ARGUMENT,
+                "the tile floor needs the fused kernel's shapes: d of 64 or "
+                "128, dv a multiple of %d, at least 4 entries%s",
+                sizeof(T) == 4 ? 16 : 64,
+                sizeof(T) == 4 ? "" : ", aligned query, value and output");
+  return rc;
+}
+
 template <typename T>
 int attention_entry(const int32_t *row_offsets, const int32_t *column_indices,
                     const T *mask_values, const T *query,
@@ -2108,6 +2326,36 @@ extern "C" int sw_sparse_attention_f32(
       row_offsets, column_indices, mask_values, query, transposed_key, value,
       scores, row_maximum, row_sum, output, rows, cols, nnz, d, dv, alpha,
       beta, opts, stream);
+}
+
+extern "C" int sw_attention_tile_floor(
+    const int32_t *row_offsets, const int32_t *column_indices,
+    const void *mask_values, const void *query, const void *transposed_key,
+    const void *value, void *scores, void *row_maximum, void *row_sum,
+    void *output, int64_t rows, int64_t cols, int64_t nnz, int64_t d,
+    int64_t dv, int value_bytes, void *stream) {
+  sw::clear_error();
+  if (value_bytes == 4)
+    return sw::attention_floor_entry<float>(
+        row_offsets, column_indices, static_cast<const float *>(mask_values),
+        static_cast<const float *>(query),
+        static_cast<const float *>(transposed_key),
+        static_cast<const float *>(value), static_cast<float *>(scores),
+        static_cast<float *>(row_maximum), static_cast<float *>(row_sum),
+        static_cast<float *>(output), rows, cols, nnz, d, dv, stream);
+  if (value_bytes == 2)
+    return sw::attention_floor_entry<uint16_t>(
+        row_offsets, column_indices,
+        static_cast<const uint16_t *>(mask_values),
+        static_cast<const uint16_t *>(query),
+        static_cast<const uint16_t *>(transposed_key),
+        static_cast<const uint16_t *>(value), static_cast<uint16_t *>(scores),
+        static_cast<uint16_t *>(row_maximum),
+        static_cast<uint16_t *>(row_sum), static_cast<uint16_t *>(output),
+        rows, cols, nnz, d, dv, stream);
+  return sw::fail(SW_ERR_INVALID_ARGUMENT,
+                  "tile floor value bytes must be 4 or 2, but got %d",
+                  value_bytes);
 }
 
 extern "C" int sw_sparse_attention_bf16(

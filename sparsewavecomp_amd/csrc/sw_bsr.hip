@@ -217,7 +217,13 @@ __global__ __launch_bounds__(256) void bsr16_mfma_bf16(
 // tiles are summed in LDS by wave 0.  Each lane ends with eight consecutive
 // columns of four output rows: one 128-bit (bf16) or two 128-bit (fp32)
 // stores per row.  Workgroups run in XCD-contiguous block-row order.
-template <int NB, int SPL, typename TO>
+//
+// FLOOR (the slab-floor diagnostic, sw_bsr_slab_floor): the same grid, block
+// order, loads, LDS reduction and stores, with the matrix-core products
+// replaced by an XOR of every 32-bit word the lane loads; every output
+// element of the lane's region then holds that XOR (truncated to 16 bits for
+// a bf16 output).  Its time is the floor of the kernel's memory trips.
+template <int NB, int SPL, typename TO, bool FLOOR = false>
 __global__ __launch_bounds__(64 * SPL) void bsr16_mfma_bf16_x8(
     const int32_t *__restrict__ bro, const int32_t *__restrict__ bcol,
     const uint16_t *__restrict__ bval, const uint16_t *__restrict__ rhs,
@@ -256,6 +262,14 @@ __global__ __launch_bounds__(64 * SPL) void bsr16_mfma_bf16_x8(
 #pragma unroll
     for (int u = 0; u < NB; ++u) {
       if (u < nb) {
+        if constexpr (FLOOR) {
+          uint32_t x = a[u].x ^ a[u].y;
+#pragma unroll
+          for (int st = 0; st < 4; ++st)
+            x ^= q[u][st].x ^ q[u][st].y ^ q[u][st].z ^ q[u][st].w;
+          acc[0].x = __uint_as_float(__float_as_uint(acc[0].x) ^ x);
+          continue;
+        }
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
           // element t of the four rows (dword t / 2, half t % 2), paired by
@@ -269,6 +283,38 @@ __global__ __launch_bounds__(64 * SPL) void bsr16_mfma_bf16_x8(
         }
       }
     }
+  }
+  if constexpr (FLOOR) {
+    // the XOR of the waves' words, in every element the lane stores
+    if constexpr (SPL > 1) {
+      if (sp > 0)
+        red[sp - 1][0][0][l] = acc[0].x;
+      __syncthreads();
+      if (sp > 0)
+        return; // after the only barrier
+      uint32_t x = __float_as_uint(acc[0].x);
+#pragma unroll
+      for (int w = 0; w < SPL - 1; ++w)
+        x ^= __float_as_uint(red[w][0][0][l]);
+      acc[0].x = __uint_as_float(x);
+    }
+    const uint32_t x = __float_as_uint(acc[0].x);
+    if (ok) {
+      TO *o = out + (br * 16 + g * 4) * k + cb;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        if constexpr (sizeof(TO) == 2) {
+          const uint32_t h = (x & 0xFFFFu) | (x << 16);
+          __builtin_nontemporal_store(v4u{h, h, h, h},
+                                      reinterpret_cast<v4u *>(o + v * k));
+        } else {
+          const float f = __uint_as_float(x);
+          st4_nt(o + v * k, v4f{f, f, f, f});
+          st4_nt(o + v * k + 4, v4f{f, f, f, f});
+        }
+      }
+    }
+    return;
   }
   if constexpr (SPL > 1) {
     if (sp > 0)
@@ -321,7 +367,8 @@ __global__ __launch_bounds__(64 * SPL) void bsr16_mfma_bf16_x8(
 // are summed through LDS by wave 0 of each strip.
 constexpr int kF32Strips = 2;
 
-template <int NB, int SPL>
+// FLOOR: the slab-floor diagnostic, as for the bf16 kernel above.
+template <int NB, int SPL, bool FLOOR = false>
 __global__ __launch_bounds__(64 * kF32Strips * SPL) void bsr16_mfma_f32_x4(
     const int32_t *__restrict__ bro, const int32_t *__restrict__ bcol,
     const float *__restrict__ bval, const float *__restrict__ rhs,
@@ -360,6 +407,16 @@ __global__ __launch_bounds__(64 * kF32Strips * SPL) void bsr16_mfma_f32_x4(
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
       if (j < nb) {
+        if constexpr (FLOOR) {
+          uint32_t x = 0;
+#pragma unroll
+          for (int st = 0; st < 4; ++st)
+            x ^= __float_as_uint(a[j][st]) ^ __float_as_uint(bv[j][st].x) ^
+                 __float_as_uint(bv[j][st].y) ^ __float_as_uint(bv[j][st].z) ^
+                 __float_as_uint(bv[j][st].w);
+          acc[0].x = __uint_as_float(__float_as_uint(acc[0].x) ^ x);
+          continue;
+        }
 #pragma unroll
         for (int st = 0; st < 4; ++st) {
           acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j][st], bv[j][st].x,
@@ -373,6 +430,29 @@ __global__ __launch_bounds__(64 * kF32Strips * SPL) void bsr16_mfma_f32_x4(
         }
       }
     }
+  }
+  if constexpr (FLOOR) {
+    if constexpr (SPL > 1) {
+      if (sp > 0)
+        red[strip][sp - 1][0][0][l] = acc[0].x;
+      __syncthreads();
+      if (sp > 0)
+        return;
+      uint32_t x = __float_as_uint(acc[0].x);
+#pragma unroll
+      for (int w = 0; w < SPL - 1; ++w)
+        x ^= __float_as_uint(red[strip][w][0][0][l]);
+      acc[0].x = __uint_as_float(x);
+    }
+    if (ok) {
+      float *o = out + ((int64_t)br * 16 + g * 4) * k + cb;
+      const float f = acc[0].x;
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        __builtin_nontemporal_store(v4f{f, f, f, f},
+                                    reinterpret_cast<v4f *>(o + v * k));
+    }
+    return;
   }
   if constexpr (SPL > 1) {
     if (sp > 0) {
@@ -550,7 +630,83 @@ int bsr_entry(const int32_t *block_row_offsets,
                            block_size, o, sw::as_stream(stream), mfma);
 }
 
+// The slab floor: the MFMA kernel launch_bsr would run for these operands,
+// in its FLOOR form.
+template <typename T, typename TO>
+int launch_slab_floor(const int32_t *bro, const int32_t *bcol, const T *bval,
+                      const T *rhs, TO *out, int64_t rows, int64_t k,
+                      hipStream_t st) {
+  if (rows == 0 || k == 0)
+    return SW_OK;
+  const int nbr = (int)(rows / 16);
+  if constexpr (sizeof(T) == 4) {
+    const int64_t strips = std::min<int64_t>(kF32Strips, sw::ceil_div(k, 64));
+    const int64_t gy = sw::ceil_div(k, 64 * strips);
+    if (gy > 65535)
+      return sw::fail(SW_ERR_INVALID_SHAPE, "rhs has too many columns");
+    hipLaunchKernelGGL((bsr16_mfma_f32_x4<kF32Batch, kF32Split, true>),
+                       dim3((unsigned)nbr, (unsigned)gy),
+                       dim3((unsigned)(64 * strips * kF32Split)), 0, st, bro,
+                       bcol, bval, rhs, out, k, nbr);
+  } else {
+    const int64_t gy = sw::ceil_div(k, 128);
+    if (gy > 65535)
+      return sw::fail(SW_ERR_INVALID_SHAPE, "rhs has too many columns");
+    hipLaunchKernelGGL((bsr16_mfma_bf16_x8<kBf16Batch, kBf16Split, TO, true>),
+                       dim3((unsigned)nbr, (unsigned)gy), dim3(64 * kBf16Split),
+                       0, st, bro, bcol, bval, rhs, out, k, nbr);
+  }
+  return sw::launch_check("BSR slab floor kernel");
+}
+
 } // namespace
+
+extern "C" int sw_bsr_slab_floor(const int32_t *block_row_offsets,
+                                 const int32_t *block_column_indices,
+                                 const void *block_values, const void *rhs,
+                                 void *output, int64_t rows, int64_t cols,
+                                 int64_t nnzb, int64_t k, int value_bytes,
+                                 int output_bytes, void *stream) {
+  sw::clear_error();
+  int rc = check_bsr(block_row_offsets, block_column_indices, block_values,
+                     rhs, output, rows, cols, nnzb, k, 16);
+  if (rc)
+    return rc;
+  const bool f32 = value_bytes == 4 && output_bytes == 4;
+  const bool b16 = value_bytes == 2 && (output_bytes == 2 || output_bytes == 4);
+  if (!f32 && !b16)
+    return sw::fail(SW_ERR_INVALID_ARGUMENT,
+                    "slab floor value / output bytes must be 4 / 4, 2 / 2 or "
+                    "2 / 4, but got %d / %d", value_bytes, output_bytes);
+  // the floor runs where the MFMA kernels run: 16-byte aligned rhs and
+  // output, block values aligned to four elements, k % 4 (fp32) or k % 8
+  const uintptr_t va = reinterpret_cast<uintptr_t>(block_values);
+  if (k % (f32 ? 4 : 8) != 0 || !sw::aligned16(rhs) ||
+      !sw::aligned16(output) || (va & (4u * value_bytes - 1)) != 0)
+    return sw::fail(SW_ERR_INVALID_ARGUMENT,
+                    "the slab floor needs the MFMA kernels' shapes: k a "
+                    "multiple of %d, 16-byte aligned rhs and output, block "
+                    "values aligned to %d bytes", f32 ? 4 : 8,
+                    4 * value_bytes);
+  hipStream_t st = sw::as_stream(stream);
+  if (f32)
+    return launch_slab_floor<float, float>(
+        block_row_offsets, block_column_indices,
+        static_cast<const float *>(block_values),
+        static_cast<const float *>(rhs), static_cast<float *>(output), rows,
+        k, st);
+  if (output_bytes == 2)
+    return launch_slab_floor<uint16_t, uint16_t>(
+        block_row_offsets, block_column_indices,
+        static_cast<const uint16_t *>(block_values),
+        static_cast<const uint16_t *>(rhs), static_cast<uint16_t *>(output),
+        rows, k, st);
+  return launch_slab_floor<uint16_t, float>(
+      block_row_offsets, block_column_indices,
+      static_cast<const uint16_t *>(block_values),
+      static_cast<const uint16_t *>(rhs), static_cast<float *>(output), rows,
+      k, st);
+}
 
 extern "C" int sw_bsr_spmm_f32(const int32_t *block_row_offsets,
                                const int32_t *block_column_indices,

@@ -332,3 +332,22 @@ def test_csr_nnz_limit():
         rc = lib.sw_sddmm_csr_bf16(fake, fake, fake, fake, fake, fake, 4, 4,
                                    nnz, 4, 0, 1.0, 0.0, None, None)
         assert rc == -2
+
+
+def test_slab_floor_rejects_shapes_it_does_not_run():
+    """sw_bsr_slab_floor runs where the MFMA kernels run: 16-byte aligned
+    rhs and output, k % 4 (fp32) or k % 8 (bf16), and a known element
+    width pair; anything else fails before a launch."""
+    lib = sw.load_library()
+    P = ctypes.c_void_p
+    ok = P(64)
+    args = (ok, ok, ok, ok, ok, 32, 32, 2)
+    assert lib.sw_bsr_slab_floor(*args, 8, 4, 2, None) == -3   # fp32 / bf16
+    assert lib.sw_bsr_slab_floor(*args, 8, 3, 3, None) == -3
+    assert lib.sw_bsr_slab_floor(*args, 12, 2, 2, None) == -3  # bf16, k % 8
+    assert b"multiple of 8" in lib.sw_last_error()
+    assert lib.sw_bsr_slab_floor(ok, ok, ok, P(72), ok, 32, 32, 2, 8, 4, 4,
+                                 None) == -3                  # rhs alignment
+    assert lib.sw_bsr_slab_floor(ok, ok, ok, ok, ok, 30, 32, 2, 8, 4, 4,
+                                 None) == -2                  # rows % 16
+
