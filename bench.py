@@ -472,6 +472,9 @@ def main():
         "spmv-mapping=block-per-row spmv-block-size=128",
         "spmv-mapping=thread-per-row",
         "spmv-mapping=wave-per-position",
+        # the deterministic row-owner extension (no atomics, no fill)
+        "spmv-mapping=wave-per-row-balanced spmv-positions-per-lane=4 "
+        "spmv-block-size=64",
     ]
     if args.only_headline:
         mappings = mappings[:3]
