@@ -66,7 +66,7 @@ def parse():
                              "bsr-bf16-floor", "bsr-bf16-f32out-floor",
                              "attention", "attention-bf16",
                              "attention-floor", "attention-bf16-floor",
-                             "sddmm", "sddmm-bf16", "copy",
+                             "sddmm", "sddmm-bf16", "copy", "bundle",
                              "reference-sweep"],
                     help="run one workload --steps times with no timing or "
                          "JSON (for rocprofv3 kernel-trace / pmc runs)")
@@ -209,6 +209,22 @@ def profile(args):
             out = torch.empty((csr.rows, args.k), device=dev)
             for _ in range(n):
                 sw.spmm(ro, col, val, rhs, out, options=o)
+    elif w == "bundle":
+        # the configuration-3 lrrt bundle (K = 4, built in-tree), launched as
+        # lrrt does: launch(n = rows, args)
+        from sparsewavecomp_amd import bundle as BU
+        from sparsewavecomp_amd.bundle.runtime import Bundle
+        csr, _ = W.config2(seed=0)
+        bun = Bundle(BU.CONFIG3_BUNDLE)
+        ro, col, val = T(csr.row_offsets), T(csr.column_indices), T(csr.values)
+        rhs = T(W.config3_rhs(csr.cols, 4, seed=0))
+        out = torch.empty((csr.rows, 4), device=dev)
+        ptrs = {"rowOffsets": ro.data_ptr(), "columnIndices": col.data_ptr(),
+                "values": val.data_ptr(), "rhs": rhs.data_ptr(),
+                "output": out.data_ptr()}
+        st = torch.cuda.current_stream().cuda_stream
+        for _ in range(n):
+            bun.launch("spmm", csr.rows, ptrs, stream=st)
     elif w.startswith("bsr"):
         # bsr, bsr-bf16, bsr-bf16-f32out; "-floor" runs the slab floor
         floor = w.endswith("-floor")
