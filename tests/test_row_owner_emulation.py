@@ -216,3 +216,36 @@ def test_row_owner_emulation_catches_a_dropped_carry(orc):
                 True, drop_carry=True)
     with pytest.raises(AssertionError):
         assert_within_bound(y, ref, bound)
+
+
+def test_row_owner_emulation_random_shapes(orc):
+    """Property check over random ragged matrices: row lengths from a mix of
+    empty, short and step-spanning rows, every positions-per-lane value and
+    1-3 steps per chunk; the emulation must stay in range, write each row
+    once and match the oracle."""
+    from hypothesis import given, settings, strategies as st
+
+    @settings(max_examples=60, deadline=None, derandomize=True)
+    @given(lengths=st.lists(st.one_of(st.just(0), st.integers(1, 6),
+                                      st.integers(60, 700)),
+                            min_size=1, max_size=40),
+           P=st.sampled_from([1, 2, 4, 8, 16]),
+           steps=st.integers(1, 3), seed=st.integers(0, 2 ** 16))
+    def check(lengths, P, steps, seed):
+        rng = np.random.default_rng(seed)
+        cols = 800
+        ro = np.zeros(len(lengths) + 1, np.int32)
+        np.cumsum(lengths, out=ro[1:])
+        col = (np.concatenate([np.sort(rng.choice(cols, n, replace=False))
+                               for n in lengths]).astype(np.int32)
+               if ro[-1] else np.zeros(0, np.int32))
+        val = rng.uniform(-1, 1, col.size).astype(np.float32)
+        x = rng.uniform(-1, 1, cols).astype(np.float32)
+        if col.size == 0:
+            return  # the launcher fills the output instead (nnz == 0)
+        y = emulate(ro, col, val, x, P, steps, vec=P >= 4)
+        ref = orc.spmv(ro, col, val, x)
+        bound = orc.spmv_abs_bound(ro, col, val, x)
+        assert_within_bound(y, ref, bound)
+
+    check()
