@@ -793,6 +793,39 @@ def main():
                     workloads["attention_config5"][key]["tile_floor"] = {
                         "ms": msf, "kernel_over_floor": ms / msf}
                     log(f"  tile floor {msf * 1e3:.1f} us")
+            if dname == "fp32":
+                # the configuration-5 lrrt attention bundle (the six
+                # reference kernels at seq 8192, built in-tree by
+                # __graft_entry__.build()), launched in order as a runtime
+                # does: launch(n = rows, args), n = rows * dv for the output
+                try:
+                    from sparsewavecomp_amd import bundle as BU
+                    from sparsewavecomp_amd.bundle.runtime import Bundle
+                    bun = Bundle(BU.CONFIG5_BUNDLE)
+                    names = ("rowOffsets", "columnIndices", "maskValues",
+                             "query", "transposedKey", "value")
+                    ptrs = {nm: t.data_ptr() for nm, t in zip(names, att)}
+                    ptrs.update(scores=scores.data_ptr(),
+                                rowMaximum=rmax.data_ptr(),
+                                rowSum=rsum.data_ptr(),
+                                output=outa.data_ptr())
+                    st = torch.cuda.current_stream().cuda_stream
+
+                    def chain():
+                        for nm in BU.ATTENTION_ORDER:
+                            bun.launch(nm, mask.rows * 64
+                                       if nm == "sparse_attention_output"
+                                       else mask.rows, ptrs, stream=st)
+                    log("attention lrrt bundle (six kernels, launch(n, args))")
+                    ms = time_steps(chain, K, Wm, WARM_MS)
+                    workloads["attention_config5"][
+                        "lrrt bundle: six kernels (launch(n, args))"] = {
+                        "ms": ms, "GFLOP/s": 4 * mask.nnz * 64 / ms / 1e6}
+                    log(f"  {ms * 1e3:.1f} us")
+                    bun.close()
+                except Exception as e:  # reported when it was built
+                    workloads["attention_config5"][
+                        "lrrt bundle error"] = str(e)
             # the chain's first op on its own: scores = alpha Q K^T on the
             # mask's positions
             for opts in ["", "sddmm-mapping=row-tile-mfma"]:

@@ -348,6 +348,33 @@ def build_config3_bundle() -> Path:
     return CONFIG3_BUNDLE
 
 
+# Benchmark configuration 5 (sparse attention, seq 8192, d = dv = 64,
+# alpha = 1/8) as the six-kernel attention bundle, built in-tree like the
+# configuration-3 SpMM bundle.
+CONFIG5_SEQ = 8192
+CONFIG5_HEAD_DIM = 64
+CONFIG5_BUNDLE = Path(__file__).resolve().parent / "prebuilt" / \
+    "attention_config5"
+
+
+def build_config5_bundle() -> Path:
+    """(Re)build the configuration-5 attention bundle in place."""
+    if CONFIG5_BUNDLE.exists():
+        shutil.rmtree(CONFIG5_BUNDLE)
+    build_attention_bundle(CONFIG5_BUNDLE, rows=CONFIG5_SEQ,
+                           key_rows=CONFIG5_SEQ, head_dim=CONFIG5_HEAD_DIM,
+                           value_cols=CONFIG5_HEAD_DIM)
+    verify_bundle(CONFIG5_BUNDLE)
+    return CONFIG5_BUNDLE
+
+
+# The order in which a runtime runs the attention bundle's kernels (the
+# manifest lists them sorted by name and records no order).
+ATTENTION_ORDER = ["sparse_attention_scores", "sparse_attention_row_max",
+                   "sparse_attention_exp", "sparse_attention_row_sum",
+                   "sparse_attention_normalize", "sparse_attention_output"]
+
+
 def attention_buffers(rows, key_rows, head_dim, value_cols) -> dict:
     """The ten-buffer ABI with dtype/shape/kind (sparsewave_bundle_ir.py:82-93,
     specialised shapes as parse_sparse_attention_ir_text records them)."""

@@ -43,37 +43,66 @@ def test_spmm_bundle_matches_oracle(dev, orc, tmp_path, tile):
     assert_within_bound(out.cpu().numpy(), ref, bound)
 
 
-def test_attention_bundle_matches_oracle(dev, orc, tmp_path):
-    mask, q, kt, v, alpha = W.config5(seed=0, seq=512, d=64)
-    v = v[:, :32].copy()
-    B.build_attention_bundle(tmp_path / "b", rows=512, key_rows=512,
-                             head_dim=64, value_cols=32, alpha=alpha)
+def _attention_case(case):
+    """(mask, q, kt, v, alpha) for the attention bundle tests: block masks
+    whose 64-row tiles hold the prefix column structure (the scores kernel's
+    matrix-core tiles), a partial last tile, 32-row blocks that straddle
+    the 64-row tiles and ragged masks (its row-by-row path), and head dims
+    of 64, 128 and 32 (no tiles at 32)."""
+    if case in ("config5", "d128", "d32"):
+        d = {"config5": 64, "d128": 128, "d32": 32}[case]
+        mask, q, kt, v, alpha = W.config5(seed=0, seq=512, d=d)
+        return mask, q, kt, np.ascontiguousarray(v[:, :32]), alpha
+    if case == "partial":
+        mask = W.attention_mask(seq=300, block=64, window=3,
+                                random_blocks=1, seed=4)
+    elif case == "block32":
+        mask = W.attention_mask(seq=448, block=32, window=4,
+                                random_blocks=2, seed=5)
+    else:
+        from tests.test_gpu_fuzz_attention import _mask
+        mask, _ = _mask({"ragged0": 0, "ragged2": 2}[case])
+    rng = np.random.default_rng(len(case))
+    q = rng.standard_normal((mask.rows, 64)).astype(np.float32)
+    kt = rng.standard_normal((64, mask.cols)).astype(np.float32)
+    v = rng.standard_normal((mask.cols, 48)).astype(np.float32)
+    mask = W.CSR(mask.rows, mask.cols, mask.row_offsets, mask.column_indices,
+                 rng.uniform(-1, 1, mask.nnz).astype(np.float32))
+    return mask, q, kt, v, 0.125
+
+
+@pytest.mark.parametrize("case", ["config5", "partial", "block32", "ragged0",
+                                  "ragged2", "d128", "d32"])
+def test_attention_bundle_matches_oracle(dev, orc, tmp_path, case):
+    mask, q, kt, v, alpha = _attention_case(case)
+    rows, d, dv = mask.rows, q.shape[1], v.shape[1]
+    beta = 0.0 if case in ("config5", "d128", "d32") else 0.5
+    B.build_attention_bundle(tmp_path / "b", rows=rows, key_rows=mask.cols,
+                             head_dim=d, value_cols=dv, alpha=alpha,
+                             beta=beta)
     B.verify_bundle(tmp_path / "b")
     bun = Bundle(tmp_path / "b")
+    nan = float("nan")
     bufs = {"rowOffsets": G.t(mask.row_offsets),
             "columnIndices": G.t(mask.column_indices),
             "maskValues": G.t(mask.values), "query": G.t(q),
             "transposedKey": G.t(kt), "value": G.t(v),
-            "scores": torch.empty(mask.nnz, device=G.DEV),
-            "rowMaximum": torch.empty(512, device=G.DEV),
-            "rowSum": torch.empty(512, device=G.DEV),
-            "output": torch.full((512, 32), float("nan"), device=G.DEV)}
+            "scores": torch.full((mask.nnz,), nan, device=G.DEV),
+            "rowMaximum": torch.full((rows,), nan, device=G.DEV),
+            "rowSum": torch.full((rows,), nan, device=G.DEV),
+            "output": torch.full((rows, dv), nan, device=G.DEV)}
     ptrs = {k: t.data_ptr() for k, t in bufs.items()}
     # the runtime executor's order (the manifest deliberately has none)
-    order = ["sparse_attention_scores", "sparse_attention_row_max",
-             "sparse_attention_exp", "sparse_attention_row_sum",
-             "sparse_attention_normalize", "sparse_attention_output"]
-    G.say("bundle attention")
-    for name in order:
-        n = 512 * 32 if name == "sparse_attention_output" else 512
-        bun.launch(name, n, ptrs)
+    G.say(f"bundle attention {case} rows={rows} nnz={mask.nnz} d={d}")
+    for name in B.ATTENTION_ORDER:
+        bun.launch(name, rows * dv if name == "sparse_attention_output"
+                   else rows, ptrs)
     torch.cuda.synchronize()
     bun.close()
     # the chain's bounds derived from the per-op bars
-    check_attention_f32(orc, mask, mask.values, q, kt, v, alpha, 0.0,
+    check_attention_f32(orc, mask, mask.values, q, kt, v, alpha, beta,
                         *(bufs[k].cpu().numpy() for k in (
                             "scores", "rowMaximum", "rowSum", "output")))
-    assert math.isfinite(float(bufs["rowSum"].sum()))
 
 
 def test_config3_bundle_at_full_size(dev, orc):
@@ -112,3 +141,38 @@ def test_config3_bundle_at_full_size(dev, orc):
                                sub.values, rhs)
     assert_within_bound(got[rows], ref, bound)
 
+
+
+def test_config5_bundle_at_full_size(dev, orc):
+    """The in-tree attention bundle of configuration 5 (seq 8192, d = dv =
+    64, alpha = 1/8), its six kernels launched in order as a runtime does,
+    n = rows (output elements for the output kernel): every output of the
+    chain against the oracle with the bounds derived from the per-op bars."""
+    if not (B.CONFIG5_BUNDLE / "manifest.json").exists():
+        pytest.fail("the configuration-5 bundle is not built "
+                    "(__graft_entry__.build() writes it)")
+    B.verify_bundle(B.CONFIG5_BUNDLE)
+    mask, q, kt, v, alpha = W.config5(seed=0)
+    assert mask.rows == B.CONFIG5_SEQ and q.shape[1] == B.CONFIG5_HEAD_DIM
+    assert alpha == 1.0 / math.sqrt(B.CONFIG5_HEAD_DIM)
+    rows, dv = mask.rows, v.shape[1]
+    nan = float("nan")
+    bufs = {"rowOffsets": G.t(mask.row_offsets),
+            "columnIndices": G.t(mask.column_indices),
+            "maskValues": G.t(mask.values), "query": G.t(q),
+            "transposedKey": G.t(kt), "value": G.t(v),
+            "scores": torch.full((mask.nnz,), nan, device=G.DEV),
+            "rowMaximum": torch.full((rows,), nan, device=G.DEV),
+            "rowSum": torch.full((rows,), nan, device=G.DEV),
+            "output": torch.full((rows, dv), nan, device=G.DEV)}
+    ptrs = {k: t.data_ptr() for k, t in bufs.items()}
+    bun = Bundle(B.CONFIG5_BUNDLE)
+    G.say("configuration-5 attention bundle, seq 8192")
+    for name in B.ATTENTION_ORDER:
+        bun.launch(name, rows * dv if name == "sparse_attention_output"
+                   else rows, ptrs)
+    torch.cuda.synchronize()
+    bun.close()
+    check_attention_f32(orc, mask, mask.values, q, kt, v, alpha, 0.0,
+                        *(bufs[k].cpu().numpy() for k in (
+                            "scores", "rowMaximum", "rowSum", "output")))
