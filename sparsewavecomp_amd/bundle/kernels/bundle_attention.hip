@@ -39,12 +39,10 @@ __device__ __forceinline__ int work_item() {
 // position order).
 constexpr int kDeep = 16;
 
+// arith.maximumf: NaN if either operand is NaN, and +0 above -0 -- the
+// IEEE 754-2019 maximum, one v_maximum_f32
 __device__ __forceinline__ float maximumf(float a, float b) {
-  if (a != a || b != b)
-    return __builtin_nanf("");
-  if (a == b)
-    return __float_as_int(a) < 0 ? b : a;
-  return a > b ? a : b;
+  return __builtin_elementwise_maximum(a, b);
 }
 
 #if SW_ATTENTION_ROLE == 1
@@ -300,97 +298,155 @@ SW_KERNEL sparse_attention_scores(const int32_t *__restrict__ rowOffsets,
                scores, r);
 }
 #endif
-#elif SW_ATTENTION_ROLE == 2
-SW_KERNEL sparse_attention_row_max(const int32_t *__restrict__ rowOffsets,
-                                   const float *__restrict__ scores,
-                                   float *__restrict__ rowMaximum) {
+#elif SW_ATTENTION_ROLE >= 2 && SW_ATTENTION_ROLE <= 5
+// The row kernels: one work-item per row, kRowDeep of its entries in flight
+// per step; the row's last partial step loads kRowDeep entries too, from
+// positions clamped to its last entry, and selects the ones in the row (no
+// entry-by-entry tail, each entry of which would be a memory round trip).
+constexpr int kRowDeep = 32;
+
+#if SW_ATTENTION_ROLE == 2 || SW_ATTENTION_ROLE == 4
+// row maximum (identity -inf, the NaN-propagating maximum) or row sum
+// (identity 0, entries added in position order)
+#if SW_ATTENTION_ROLE == 2
+#define SW_ROW_REDUCE_NAME sparse_attention_row_max
+#define SW_ROW_REDUCE_OUT rowMaximum
+#else
+#define SW_ROW_REDUCE_NAME sparse_attention_row_sum
+#define SW_ROW_REDUCE_OUT rowSum
+#endif
+SW_KERNEL SW_ROW_REDUCE_NAME(const int32_t *__restrict__ rowOffsets,
+                             const float *__restrict__ scores,
+                             float *__restrict__ SW_ROW_REDUCE_OUT) {
+  constexpr bool kMax = SW_ATTENTION_ROLE == 2;
   const int r = work_item();
   if (r >= SW_ROWS)
     return;
-  float m = -INFINITY;
+  float a = kMax ? -INFINITY : 0.0f;
   const int32_t e = rowOffsets[r + 1];
   int32_t p = rowOffsets[r];
-  for (; p + kDeep <= e; p += kDeep) {
-    float v[kDeep];
+  for (; p + kRowDeep <= e; p += kRowDeep) {
+    float v[kRowDeep];
 #pragma unroll
-    for (int u = 0; u < kDeep; ++u)
+    for (int u = 0; u < kRowDeep; ++u)
       v[u] = scores[p + u];
 #pragma unroll
-    for (int u = 0; u < kDeep; ++u)
-      m = maximumf(m, v[u]);
+    for (int u = 0; u < kRowDeep; ++u)
+      a = kMax ? maximumf(a, v[u]) : a + v[u];
   }
-  for (; p < e; ++p)
-    m = maximumf(m, scores[p]);
-  rowMaximum[r] = m;
+  if (p < e) {
+    float v[kRowDeep];
+#pragma unroll
+    for (int u = 0; u < kRowDeep; ++u)
+      v[u] = scores[p + u < e ? p + u : e - 1];
+#pragma unroll
+    for (int u = 0; u < kRowDeep; ++u)
+      if (kMax)
+        a = p + u < e ? maximumf(a, v[u]) : a;
+      else
+        a = p + u < e ? a + v[u] : a;
+  }
+  SW_ROW_REDUCE_OUT[r] = a;
 }
-#elif SW_ATTENTION_ROLE == 3
-SW_KERNEL sparse_attention_exp(const int32_t *__restrict__ rowOffsets,
-                               const float *__restrict__ rowMaximum,
-                               float *scores) {
+#else
+// exp(s - row maximum) or s / row sum, in place
+#if SW_ATTENTION_ROLE == 3
+#define SW_ROW_MAP_NAME sparse_attention_exp
+#define SW_ROW_MAP_IN rowMaximum
+#else
+#define SW_ROW_MAP_NAME sparse_attention_normalize
+#define SW_ROW_MAP_IN rowSum
+#endif
+SW_KERNEL SW_ROW_MAP_NAME(const int32_t *__restrict__ rowOffsets,
+                          const float *__restrict__ SW_ROW_MAP_IN,
+                          float *scores) {
+  constexpr bool kExp = SW_ATTENTION_ROLE == 3;
   const int r = work_item();
   if (r >= SW_ROWS)
     return;
-  const float m = rowMaximum[r];
+  const float m = SW_ROW_MAP_IN[r];
   const int32_t e = rowOffsets[r + 1];
   int32_t p = rowOffsets[r];
-  for (; p + kDeep <= e; p += kDeep) {
-    float v[kDeep];
+  for (; p + kRowDeep <= e; p += kRowDeep) {
+    float v[kRowDeep];
 #pragma unroll
-    for (int u = 0; u < kDeep; ++u)
+    for (int u = 0; u < kRowDeep; ++u)
       v[u] = scores[p + u];
 #pragma unroll
-    for (int u = 0; u < kDeep; ++u)
-      scores[p + u] = expf(v[u] - m);
+    for (int u = 0; u < kRowDeep; ++u)
+      scores[p + u] = kExp ? expf(v[u] - m) : v[u] / m;
   }
-  for (; p < e; ++p)
-    scores[p] = expf(scores[p] - m);
-}
-#elif SW_ATTENTION_ROLE == 4
-SW_KERNEL sparse_attention_row_sum(const int32_t *__restrict__ rowOffsets,
-                                   const float *__restrict__ scores,
-                                   float *__restrict__ rowSum) {
-  const int r = work_item();
-  if (r >= SW_ROWS)
-    return;
-  float s = 0.0f;
-  const int32_t e = rowOffsets[r + 1];
-  int32_t p = rowOffsets[r];
-  for (; p + kDeep <= e; p += kDeep) {
-    float v[kDeep];
+  if (p < e) {
+    float v[kRowDeep];
 #pragma unroll
-    for (int u = 0; u < kDeep; ++u)
-      v[u] = scores[p + u];
+    for (int u = 0; u < kRowDeep; ++u)
+      v[u] = scores[p + u < e ? p + u : e - 1];
 #pragma unroll
-    for (int u = 0; u < kDeep; ++u)
-      s += v[u];
+    for (int u = 0; u < kRowDeep; ++u)
+      if (p + u < e)
+        scores[p + u] = kExp ? expf(v[u] - m) : v[u] / m;
   }
-  for (; p < e; ++p)
-    s += scores[p];
-  rowSum[r] = s;
 }
-#elif SW_ATTENTION_ROLE == 5
-SW_KERNEL sparse_attention_normalize(const int32_t *__restrict__ rowOffsets,
-                                     const float *__restrict__ rowSum,
-                                     float *scores) {
-  const int r = work_item();
-  if (r >= SW_ROWS)
-    return;
-  const float s = rowSum[r];
-  const int32_t e = rowOffsets[r + 1];
-  int32_t p = rowOffsets[r];
-  for (; p + kDeep <= e; p += kDeep) {
-    float v[kDeep];
-#pragma unroll
-    for (int u = 0; u < kDeep; ++u)
-      v[u] = scores[p + u];
-#pragma unroll
-    for (int u = 0; u < kDeep; ++u)
-      scores[p + u] = v[u] / s;
-  }
-  for (; p < e; ++p)
-    scores[p] = scores[p] / s;
-}
+#endif
 #elif SW_ATTENTION_ROLE == 6
+#if SW_VALUE_COLS % 64 == 0
+// One wave per 64 output columns of one row (the launch is one work-item
+// per output element): the row's column indices and probabilities are the
+// same in every lane, so they come through scalar loads, kOutDeep entries
+// at a time, and each lane gathers its V column; products are added in
+// position order, as one work-item per element does.
+constexpr int kOutDeep = 32;
+
+SW_KERNEL sparse_attention_output(const int32_t *__restrict__ rowOffsets,
+                                  const int32_t *__restrict__ columnIndices,
+                                  const float *__restrict__ scores,
+                                  const float *__restrict__ value,
+                                  float *__restrict__ output) {
+  const int e0 = blockIdx.x * 64; // the wave's first output element
+  const int r = e0 / SW_VALUE_COLS;
+  const int c = e0 - r * SW_VALUE_COLS + (int)__builtin_amdgcn_workitem_id_x();
+  if (r >= SW_ROWS)
+    return;
+  const int32_t pe = rowOffsets[r + 1];
+  int32_t p = rowOffsets[r];
+  float acc = 0.0f;
+  for (; p + kOutDeep <= pe; p += kOutDeep) {
+    int32_t cc[kOutDeep];
+    float sv[kOutDeep], vv[kOutDeep];
+#pragma unroll
+    for (int u = 0; u < kOutDeep; ++u) {
+      cc[u] = columnIndices[p + u];
+      sv[u] = scores[p + u];
+    }
+#pragma unroll
+    for (int u = 0; u < kOutDeep; ++u)
+      vv[u] = value[(int64_t)cc[u] * SW_VALUE_COLS + c];
+#pragma unroll
+    for (int u = 0; u < kOutDeep; ++u)
+      acc = __builtin_fmaf(sv[u], vv[u], acc);
+  }
+  // the row's last partial step: positions clamped to its last entry, the
+  // products past it skipped (selected, not multiplied by zero: V may hold
+  // inf)
+  if (p < pe) {
+    int32_t cc[kOutDeep];
+    float sv[kOutDeep], vv[kOutDeep];
+#pragma unroll
+    for (int u = 0; u < kOutDeep; ++u) {
+      const int32_t q = p + u < pe ? p + u : pe - 1;
+      cc[u] = columnIndices[q];
+      sv[u] = scores[q];
+    }
+#pragma unroll
+    for (int u = 0; u < kOutDeep; ++u)
+      vv[u] = value[(int64_t)cc[u] * SW_VALUE_COLS + c];
+#pragma unroll
+    for (int u = 0; u < kOutDeep; ++u)
+      acc = p + u < pe ? __builtin_fmaf(sv[u], vv[u], acc) : acc;
+  }
+  output[(int64_t)r * SW_VALUE_COLS + c] = acc;
+}
+#else
 SW_KERNEL sparse_attention_output(const int32_t *__restrict__ rowOffsets,
                                   const int32_t *__restrict__ columnIndices,
                                   const float *__restrict__ scores,
@@ -424,6 +480,7 @@ SW_KERNEL sparse_attention_output(const int32_t *__restrict__ rowOffsets,
                          acc);
   output[e] = acc;
 }
+#endif
 #else
 #error "unknown SW_ATTENTION_ROLE"
 #endif
