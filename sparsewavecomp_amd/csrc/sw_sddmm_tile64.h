@@ -1,0 +1,211 @@
+// A wave's 64 consecutive rows of an fp32 SDDMM as one matrix-core tile.
+//
+// Shared by the library's thread-per-row SDDMM (sw_attention.hip: one
+// work-item per row, so each wave holds 64 consecutive rows) and the lrrt
+// attention bundle's scores kernel (bundle/kernels/bundle_attention.hip,
+// whose manifest fixes the same launch).  When every row's column list is
+// a prefix of the tile's last row's -- true for block masks, causal
+// diagonal blocks included, whose blocks line up with the 64-row tiles --
+// the tile's entries are the dense products of its lhs rows with the rhs
+// columns of the last row's entries, 16 entries (a chunk) at a time:
+//   S^T = K_chunk Q^T with v_mfma_f32_16x16x4_f32,
+// the gathered rhs columns as the A operand and four 16-row lhs tiles as B
+// operands, so that lane (i, g) holds row 16 R + i's dot products at
+// entries t0 + 4g .. t0 + 4g + 3.  The next chunk's rhs gathers and sample
+// values are in flight over a chunk's products; each buffer is named (a
+// buffer indexed by a run-time variable becomes indexed register moves
+// behind a wait for every load).
+//
+// The structure check reads every column index of the tile once: each row
+// against the last row's columns, which the wave stages in its LDS slice,
+// 8 rows' loads per batch, every load from a clamped valid position.  A tile
+// that fails it, or whose last row has more than kTileCols entries, stores
+// nothing and the function returns false; the caller computes those rows
+// another way.  Sums are formed by the matrix cores (the dot's order
+// differs from a sequential loop's, within the fp32 bound).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace sw_tile64 {
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr int kTileCols = 512; // the last row's entries held in LDS
+constexpr int kCheckRows = 8;  // rows whose columns one check batch loads
+
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Rows r0 .. r0 + 63 (those below `rows`) of
+//   out[p] = combine(sample[p] (0 when sample is null), lhs row . rhs col)
+// with kdim = 64 KB; lcol is this wave's LDS slice of kTileCols entries.
+// Every lane of the wave calls it with the same r0.
+template <int KB, typename Combine>
+__device__ __forceinline__ bool sddmm_tile64(
+    const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
+    const float *sample, const float *__restrict__ lhs,
+    const float *__restrict__ rhs, float *out, int64_t rows, int64_t cols,
+    int64_t r0, int32_t *lcol, Combine combine) {
+  constexpr int kdim = 64 * KB;
+  const int l = __lane_id();
+  const int i = l & 15, g = l >> 4;
+  const int nt = rows - r0 < 64 ? (int)(rows - r0) : 64; // >= 1
+  const int64_t rr = r0 + (l < nt ? l : nt - 1);
+  const int32_t rb = ro[rr];
+  const int32_t rlen = l < nt ? ro[rr + 1] - rb : 0;
+  const int32_t bl = __builtin_amdgcn_readlane(rb, nt - 1);
+  const int32_t len_last = __builtin_amdgcn_readlane(rlen, nt - 1);
+  if (len_last > kTileCols)
+    return false;
+  if (len_last == 0) {
+    // an empty last row: a prefix tile only when every row is empty (and
+    // bl may then be the arrays' end, so nothing is loaded)
+    return __builtin_amdgcn_ballot_w64(rlen > 0) == 0;
+  }
+  {
+    // entries past the last row's end repeat its final column, so that a
+    // chunk's lanes read valid columns without a check
+    const int span = (len_last + 15) & ~15;
+    for (int t = l; t < span; t += 64)
+      lcol[t] = col[bl + (t < len_last ? t : len_last - 1)];
+    wave_sync();
+    // every load unconditional, from a clamped valid position (a row's last
+    // entry, or the last row's first for an empty row), so that no branch
+    // splits a batch; the compare then selects the entries in range
+    bool mine = rlen <= len_last;
+    for (int i0 = 0; i0 < nt; i0 += kCheckRows) {
+      int32_t x[kCheckRows][kTileCols / 64];
+#pragma unroll
+      for (int j = 0; j < kCheckRows; ++j) {
+        const int row = i0 + j < nt ? i0 + j : nt - 1;
+        const int32_t b = __builtin_amdgcn_readlane(rb, row);
+        const int32_t n = __builtin_amdgcn_readlane(rlen, row);
+#pragma unroll
+        for (int u = 0; u < kTileCols / 64; ++u) {
+          const int t = l + 64 * u;
+          x[j][u] = col[n > 0 ? b + (t < n ? t : n - 1) : bl];
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < kCheckRows; ++j) {
+        const int row = i0 + j < nt ? i0 + j : nt - 1;
+        const int32_t n = __builtin_amdgcn_readlane(rlen, row);
+#pragma unroll
+        for (int u = 0; u < kTileCols / 64; ++u) {
+          const int t = l + 64 * u;
+          mine &= !(t < n && t < len_last) || x[j][u] == lcol[t];
+        }
+      }
+    }
+    if (__builtin_amdgcn_ballot_w64(!mine) != 0)
+      return false;
+  }
+  // row 16 R + i's first position and length, each 16-row tile's longest
+  // row, and its lhs rows (B operand of step st: elements 64 kb + 16 g + st)
+  int32_t rbR[4], lenR[4], maxR[4];
+  float qb[4][16 * KB];
+#pragma unroll
+  for (int R = 0; R < 4; ++R) {
+    const int src = 16 * R + i;
+    rbR[R] = __builtin_amdgcn_ds_bpermute(src << 2, rb);
+    lenR[R] = __builtin_amdgcn_ds_bpermute(src << 2, rlen);
+    int m = lenR[R];
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) {
+      const int other = __builtin_amdgcn_ds_bpermute((l ^ o) << 2, m);
+      m = other > m ? other : m;
+    }
+    maxR[R] = __builtin_amdgcn_readlane(m, 16 * R);
+    const int64_t qr = r0 + src < rows ? r0 + src : rows - 1;
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        v4f v;
+        __builtin_memcpy(&v, lhs + qr * kdim + 64 * kb + 16 * g + 4 * u,
+                         sizeof v);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          qb[R][16 * kb + 4 * u + e] = v[e];
+      }
+  }
+  // one chunk's rhs gathers (A operand of step st: rhs[64 kb + 16 g + st]
+  // at the column of entry t0 + i) and the samples of the entries its lanes
+  // store, each from a clamped valid position (selected afterwards)
+  auto load = [&](int t0, float (&a)[16 * KB], float (&mv)[4][4])
+      __attribute__((always_inline)) {
+    const int64_t c = lcol[t0 + i];
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+      for (int st = 0; st < 16; ++st)
+        a[16 * kb + st] = rhs[(int64_t)(64 * kb + 16 * g + st) * cols + c];
+#pragma unroll
+    for (int R = 0; R < 4; ++R)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int t = t0 + 4 * g + v;
+        const int32_t p = lenR[R] > 0
+                              ? rbR[R] + (t < lenR[R] ? t : lenR[R] - 1)
+                              : bl;
+        mv[R][v] = sample != nullptr ? sample[p] : 0.0f;
+      }
+  };
+  // a chunk's products and its entries' stores (one 16-byte store when the
+  // lane's four entries are all in its row)
+  auto compute = [&](int t0, const float (&a)[16 * KB],
+                     const float (&mv)[4][4]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int R = 0; R < 4; ++R) {
+      if (t0 >= maxR[R]) // wave-uniform
+        continue;
+      // two independent chains of products (even and odd steps)
+      v4f acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int st = 0; st < 16 * KB; st += 2) {
+        acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a[st], qb[R][st], acc0,
+                                                    0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a[st + 1], qb[R][st + 1],
+                                                    acc1, 0, 0, 0);
+      }
+      const v4f acc = acc0 + acc1;
+      v4f sc;
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        sc[v] = combine(mv[R][v], acc[v]);
+      const int t = t0 + 4 * g;
+      float *dst = out + rbR[R] + t;
+      if (t + 3 < lenR[R]) {
+        __builtin_memcpy(dst, &sc, sizeof sc);
+      } else {
+#pragma unroll
+        for (int v = 0; v < 3; ++v)
+          if (t + v < lenR[R])
+            dst[v] = sc[v];
+      }
+    }
+  };
+  // chunks in pairs, each buffer named: the next chunk's loads fly over a
+  // chunk's products
+  float a0[16 * KB], a1[16 * KB], m0[4][4], m1[4][4];
+  load(0, a0, m0);
+  for (int t0 = 0; t0 < len_last; t0 += 32) {
+    if (t0 + 16 < len_last)
+      load(t0 + 16, a1, m1);
+    compute(t0, a0, m0);
+    if (t0 + 16 >= len_last)
+      break;
+    if (t0 + 32 < len_last)
+      load(t0 + 32, a0, m0);
+    compute(t0 + 16, a1, m1);
+  }
+  return true;
+}
+
+} // namespace sw_tile64

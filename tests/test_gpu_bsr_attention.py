@@ -670,12 +670,17 @@ def _check_attention(orc, csr, scores, rmax, rsum, out, refs, v, inputs):
                         rsum.cpu().numpy(), out.cpu().numpy(), refs)
 
 
+@pytest.mark.parametrize("opts", ["sddmm-mapping=row-tile-mfma",
+                                  # thread-per-row: 64-row wave tiles
+                                  "", "sddmm-block-size=128",
+                                  "sddmm-block-size=64"])
 @pytest.mark.parametrize("in_place", [False, True])
 @pytest.mark.parametrize("kdim", [64, 128, 32])
-def test_sddmm_tile_mfma_block_mask(dev, orc, kdim, in_place):
-    """Block-structured masks take the 16-row MFMA tiles; with the output in
-    place of the sample values the tiles read each entry's sample before
-    writing it."""
+def test_sddmm_tile_mfma_block_mask(dev, orc, kdim, in_place, opts):
+    """Block-structured masks take the 16-row MFMA tiles (row-tile-mfma) or
+    the 64-row wave tiles (thread-per-row, fp32, kdim 64 or 128); with the
+    output in place of the sample values the tiles read each entry's sample
+    before writing it."""
     mask = W.attention_mask(seq=2048, block=64, window=4, random_blocks=2,
                             seed=3)
     rng = np.random.default_rng(kdim)
@@ -684,10 +689,10 @@ def test_sddmm_tile_mfma_block_mask(dev, orc, kdim, in_place):
     vals = rng.uniform(-1, 1, mask.nnz).astype(np.float32)
     vt = G.t(vals)
     out = vt if in_place else torch.empty(mask.nnz, device=G.DEV)
-    G.say(f"sddmm tile mfma kdim={kdim} in_place={in_place}")
+    G.say(f"sddmm tile kdim={kdim} in_place={in_place} opts='{opts}'")
     sw.sddmm(G.t(mask.row_offsets), G.t(mask.column_indices), vt,
              G.t(lhs), G.t(rhs), out, sw.SDDMM_AFFINE, 0.125, 0.5,
-             options="sddmm-mapping=row-tile-mfma")
+             options=opts or None)
     torch.cuda.synchronize()
     ref = orc.sddmm(mask.row_offsets, mask.column_indices, vals, lhs, rhs,
                     sw.SDDMM_AFFINE, 0.125, 0.5)
