@@ -92,11 +92,11 @@ __device__ __forceinline__ float map_value(int kind, float v, float rv) {
 }
 
 // ---- SDDMM -----------------------------------------------------------------
-// Thread-per-row (the reference's mapping and launch).  TKB > 0 (fp32, kdim
-// = 64 TKB, a block size that is a multiple of 64, which the host checks):
-// each wave first tries its 64 consecutive rows as one matrix-core tile
-// (sw_sddmm_tile64.h); rows of a tile without the shared column prefix are
-// then computed by their own threads as below.
+// Thread-per-row (the reference's mapping and launch).  TKB > 0 (kdim = 64
+// TKB, a block size that is a multiple of 64, for bf16 a 16-byte aligned
+// lhs, which the host checks): each wave first tries its 64 consecutive
+// rows as one matrix-core tile (sw_sddmm_tile64.h); rows of a tile without
+// the shared column prefix are then computed by their own threads as below.
 template <typename T, int RP, int LB, int TKB = 0>
 __global__ __launch_bounds__(LB) void sddmm_thread_per_row(
     const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
@@ -104,13 +104,12 @@ __global__ __launch_bounds__(LB) void sddmm_thread_per_row(
     const T *__restrict__ rhs, T *__restrict__ out, int32_t rows,
     int64_t cols, int32_t kdim, int kind, float alpha, float beta) {
   if constexpr (TKB > 0) {
-    static_assert(std::is_same_v<T, float>, "matrix-core tiles are fp32");
     __shared__ int32_t lcol[LB / kWave][sw_tile64::kTileCols];
     const int64_t r0 = (int64_t)blockIdx.x * blockDim.x +
                        (int64_t)wave_in_group() * kWave;
     if (r0 >= rows)
       return; // wave-uniform
-    if (sw_tile64::sddmm_tile64<TKB>(
+    if (sw_tile64::sddmm_tile64<T, TKB>(
             ro, col, val, lhs, rhs, out, rows, cols, r0,
             lcol[wave_in_group()], [&](float sample, float dot) {
               return combine_sddmm(kind, sample, dot, alpha, beta);
@@ -1828,13 +1827,13 @@ int launch_sddmm(const int32_t *ro, const int32_t *col, const T *val,
       return rc;
     // 16 positions per step where a workgroup of at most 512 threads lets a
     // lane hold 256 registers (configuration 5, fp32: 602 -> 478 us with 256
-    // threads); four under the 1024-thread bound.  fp32 with kdim 64 or 128
-    // and whole waves of at most 256-thread workgroups (one wave per SIMD,
-    // so the tile and the per-row steps have 512 registers without spills):
-    // 64-row matrix-core tiles first
-    bool tiles = false;
-    if constexpr (std::is_same_v<T, float>) {
-      tiles = (kdim == 64 || kdim == 128) && B % kWave == 0 && B <= 256;
+    // threads); four under the 1024-thread bound.  kdim 64 or 128 and whole
+    // waves of at most 256-thread workgroups (one wave per SIMD, so the tile
+    // and the per-row steps have 512 registers without spills; bf16 also a
+    // 16-byte aligned lhs): 64-row matrix-core tiles first
+    const bool tiles = (kdim == 64 || kdim == 128) && B % kWave == 0 &&
+                       B <= 256 && (sizeof(T) == 4 || aligned16(lhs));
+    {
       if (tiles && kdim == 64)
         hipLaunchKernelGGL((sddmm_thread_per_row<T, 16, 256, 1>),
                            dim3((unsigned)grid), dim3((unsigned)B), 0, st, ro,

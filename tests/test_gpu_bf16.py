@@ -112,11 +112,17 @@ def test_bf16_sddmm(dev, orc, golden, opts):
             _sddmm_check(orc, csr, csr.values, lhs, rhs, kind, 0.3, 0.7, got)
 
 
+# the 16-row tiles (row-tile-mfma) and thread-per-row, whose waves take
+# their 64 rows as one matrix-core tile at kdim 64 and 128
+TILE_OPTS = ["sddmm-mapping=row-tile-mfma", "", "sddmm-block-size=128"]
+
+
+@pytest.mark.parametrize("opts", TILE_OPTS)
 @pytest.mark.parametrize("kdim", [64, 128, 256])
 @pytest.mark.parametrize("shape", ["block", "structure", "long"])
-def test_bf16_sddmm_tiles(dev, orc, kdim, shape):
+def test_bf16_sddmm_tiles(dev, orc, kdim, shape, opts):
     """The bf16 matrix-core SDDMM tiles on a block mask, on tiles that take
-    its row-by-row fallback, and on tiles whose last rows hold 512, 513 and
+    their row-by-row fallback, and on tiles whose last rows hold 512, 513 and
     700 entries, for each combine kind."""
     from tests.test_gpu_bsr_attention import (_long_prefix_csr,
                                               _tile_structure_csr)
@@ -131,13 +137,13 @@ def test_bf16_sddmm_tiles(dev, orc, kdim, shape):
     for kind, alpha, beta in ((sw.SDDMM_AFFINE, 0.125, 0.5),
                               (sw.SDDMM_MUL, 1.0, 0.0),
                               (sw.SDDMM_DOT, 0.3, 0.7)):
-        got = _sddmm(csr, vals, lhs, rhs, kind, alpha, beta,
-                     "sddmm-mapping=row-tile-mfma")
+        got = _sddmm(csr, vals, lhs, rhs, kind, alpha, beta, opts)
         _sddmm_check(orc, csr, vals, lhs, rhs, kind, alpha, beta, got)
 
 
+@pytest.mark.parametrize("opts", TILE_OPTS)
 @pytest.mark.parametrize("kdim", [64, 128])
-def test_bf16_sddmm_tiles_in_place(dev, orc, kdim):
+def test_bf16_sddmm_tiles_in_place(dev, orc, kdim, opts):
     """Output in place of the sample values: each entry's sample is read
     before it is written."""
     csr = W.attention_mask(seq=2048, block=64, window=4, random_blocks=2,
@@ -147,10 +153,9 @@ def test_bf16_sddmm_tiles_in_place(dev, orc, kdim):
     rhs = rng.standard_normal((kdim, csr.cols)).astype(np.float32)
     vals = rng.uniform(-1, 1, csr.nnz).astype(np.float32)
     vt = b16(vals)
-    G.say(f"bf16 sddmm in place kdim={kdim}")
+    G.say(f"bf16 sddmm in place kdim={kdim} opts='{opts}'")
     sw.sddmm(G.t(csr.row_offsets), G.t(csr.column_indices), vt, b16(lhs),
-             b16(rhs), vt, sw.SDDMM_AFFINE, 0.125, 0.5,
-             options="sddmm-mapping=row-tile-mfma")
+             b16(rhs), vt, sw.SDDMM_AFFINE, 0.125, 0.5, options=opts or None)
     torch.cuda.synchronize()
     _sddmm_check(orc, csr, vals, lhs, rhs, sw.SDDMM_AFFINE, 0.125, 0.5,
                  host(vt))
