@@ -67,7 +67,7 @@ def parse():
                              "attention", "attention-bf16",
                              "attention-floor", "attention-bf16-floor",
                              "sddmm", "sddmm-bf16", "copy", "bundle",
-                             "reference-sweep"],
+                             "attention-bundle", "reference-sweep"],
                     help="run one workload --steps times with no timing or "
                          "JSON (for rocprofv3 kernel-trace / pmc runs)")
     ap.add_argument("--opts", default="",
@@ -225,6 +225,28 @@ def profile(args):
         st = torch.cuda.current_stream().cuda_stream
         for _ in range(n):
             bun.launch("spmm", csr.rows, ptrs, stream=st)
+    elif w == "attention-bundle":
+        # the configuration-5 lrrt attention bundle (built in-tree), its six
+        # kernels launched in order as a runtime does
+        from sparsewavecomp_amd import bundle as BU
+        from sparsewavecomp_amd.bundle.runtime import Bundle
+        mask, q, kt, v, alpha = W.config5(seed=0)
+        bufs = {"rowOffsets": T(mask.row_offsets),
+                "columnIndices": T(mask.column_indices),
+                "maskValues": T(mask.values), "query": T(q),
+                "transposedKey": T(kt), "value": T(v),
+                "scores": torch.empty(mask.nnz, device=dev),
+                "rowMaximum": torch.empty(mask.rows, device=dev),
+                "rowSum": torch.empty(mask.rows, device=dev),
+                "output": torch.empty((mask.rows, v.shape[1]), device=dev)}
+        ptrs = {k: t.data_ptr() for k, t in bufs.items()}
+        bun = Bundle(BU.CONFIG5_BUNDLE)
+        st = torch.cuda.current_stream().cuda_stream
+        for _ in range(n):
+            for name in BU.ATTENTION_ORDER:
+                bun.launch(name, mask.rows * v.shape[1]
+                           if name == "sparse_attention_output"
+                           else mask.rows, ptrs, stream=st)
     elif w.startswith("bsr"):
         # bsr, bsr-bf16, bsr-bf16-f32out; "-floor" runs the slab floor
         floor = w.endswith("-floor")

@@ -109,11 +109,15 @@ __global__ __launch_bounds__(LB) void sddmm_thread_per_row(
                        (int64_t)wave_in_group() * kWave;
     if (r0 >= rows)
       return; // wave-uniform
-    if (sw_tile64::sddmm_tile64<T, TKB>(
-            ro, col, val, lhs, rhs, out, rows, cols, r0,
-            lcol[wave_in_group()], [&](float sample, float dot) {
-              return combine_sddmm(kind, sample, dot, alpha, beta);
-            }))
+    auto combine = [&](float sample, float dot) {
+      return combine_sddmm(kind, sample, dot, alpha, beta);
+    };
+    if (val != nullptr ? sw_tile64::sddmm_tile64<T, TKB, true>(
+                             ro, col, val, lhs, rhs, out, rows, cols, r0,
+                             lcol[wave_in_group()], combine)
+                       : sw_tile64::sddmm_tile64<T, TKB, false>(
+                             ro, col, val, lhs, rhs, out, rows, cols, r0,
+                             lcol[wave_in_group()], combine))
       return;
   }
   int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -369,8 +373,10 @@ __global__ __launch_bounds__(1024) void row_reduce_thread(
   const int32_t e = ro[r + 1];
   int32_t p = ro[r];
   // sixteen loads in flight while that many remain (as unaligned vector
-  // loads), then four, combined in position order (a thread's row is a
-  // chain of memory trips)
+  // loads), combined in position order (a thread's row is a chain of memory
+  // trips); the last partial step loads sixteen too, from positions clamped
+  // to the row's last entry, and selects the ones in the row (one trip
+  // instead of one per remaining entry)
   for (; p + 15 < e; p += 16) {
     T v[16];
     __builtin_memcpy(v, val + p, sizeof v);
@@ -378,17 +384,18 @@ __global__ __launch_bounds__(1024) void row_reduce_thread(
     for (int u = 0; u < 16; ++u)
       acc = MAX ? maximumf(acc, tof(v[u])) : acc + tof(v[u]);
   }
-  for (; p + 3 < e; p += 4) {
-    float v[4];
+  if (p < e) {
+    float v[16];
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
-      v[u] = ldv(val + p + u);
+    for (int u = 0; u < 16; ++u)
+      v[u] = ldv(val + (p + u < e ? p + u : e - 1));
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
-      acc = MAX ? maximumf(acc, v[u]) : acc + v[u];
+    for (int u = 0; u < 16; ++u)
+      if (MAX)
+        acc = p + u < e ? maximumf(acc, v[u]) : acc;
+      else
+        acc = p + u < e ? acc + v[u] : acc;
   }
-  for (; p < e; ++p)
-    acc = MAX ? maximumf(acc, ldv(val + p)) : acc + ldv(val + p);
   stv(out + r, acc);
 }
 
@@ -460,8 +467,18 @@ __global__ __launch_bounds__(1024) void rowwise_map_thread(
     __builtin_memcpy(out + p, v, sizeof v);
     p += 16;
   }
-  for (; p < e; ++p)
-    stv(out + p, map_value(kind, ldv(val + p), rv));
+  // the last partial step: sixteen loads from positions clamped to the row's
+  // last entry (one trip), then the stores of the entries in the row
+  if (p < e) {
+    float v[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u)
+      v[u] = ldv(val + (p + u < e ? p + u : e - 1));
+#pragma unroll
+    for (int u = 0; u < 16; ++u)
+      if (p + u < e)
+        stv(out + p + u, map_value(kind, v[u], rv));
+  }
 }
 
 template <typename T>
