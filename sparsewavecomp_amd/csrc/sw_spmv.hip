@@ -535,66 +535,28 @@ __device__ __forceinline__ void owner_step_loads(
   }
 }
 
-// ---------------------------------------------------------------------------
-// wave-per-row-balanced: row-owner SpMV (Wave64 extension).
-//
-// The nonzeros are cut into chunks of C = 64 * P * S positions, and wave w
-// owns the rows whose first position lies in chunk w (ro[r] in
-// [wC, (w+1)C); rows beginning at or past the last chunk's start belong to
-// the last wave).  So every output row has exactly one writer, which stores
-// it with a plain store: no zero fill and no atomics, and the work stays
-// balanced by nonzeros (a wave's rows hold C positions give or take the row
-// that straddles each chunk end).  Waves run in XCD-contiguous order, so the
-// short row ranges that neighbouring waves store share one XCD's L2.
-//
-// A wave finds its first row (a wave-uniform binary search) and the first
-// row of the next chunk (a gallop from there), then walks its positions
-// [ro[r_lo], ro[r_hi]) in steps of 64 * P: lane l takes P consecutive
-// positions, finds the row of its first position in an LDS window of 64 row
-// ends, and walks them as the position kernel does -- rows that begin and end
-// inside the lane are stored directly, a lane's first and last rows are
-// joined across lanes by the DPP segmented scan.  A row still open at the
-// end of a step is carried, wave-uniform, into the next step's lane 0.
-// Rows with no entries, which no position reaches, are stored as zero by a
-// pass over the wave's rows.
-//
-// Every sum is formed in a fixed order (a lane's positions in sequence, the
-// scan's fixed DPP steps, the carry), so repeated calls give bit-identical
-// outputs, which the atomic position mappings do not.  It costs time: on
-// configuration 2 (P = 4, S = 4) 235 us against the position kernel's
-// 207 us; S = 1 248 us, S = 2 240 us; loading each step's values one step
-// ahead measured no faster (237 us).  A wave's rows run to the end of the
-// row that straddles its chunk end, so the few waves holding the start of a
-// row of thousands of entries finish last.
+// Rows r_lo .. r_hi - 1 of the SpMV by one wave: their positions
+// [ro[r_lo], ro[r_hi]) in steps of 64 * P, lane l taking P consecutive
+// positions; a lane finds the row of its first position in an LDS window
+// of 64 row ends (win: the wave's 64-entry slice), walks its positions
+// storing the rows that begin and end inside it, and the DPP segmented scan
+// joins the rows that cross lanes; a row still open at the end of a step is
+// carried, wave-uniform, into the next step's lane 0; rows with no entries
+// are stored as zero by a pass over the rows.  Every row is stored once,
+// by a plain store, with its sum formed in a fixed order.  Every lane of the
+// wave calls it with the same rows.
 template <int P, bool VEC>
-__global__ __launch_bounds__(256) void spmv_row_owner(
+__device__ __forceinline__ void owner_rows(
     const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
     const float *__restrict__ val, const float *__restrict__ x,
-    float *__restrict__ y, int32_t rows, int32_t nnz, int64_t chunk,
-    int64_t waves) {
+    float *__restrict__ y, int r_lo, int r_hi, int32_t nnz, int32_t *win) {
   const int lane = lane_id();
-  const int64_t wave =
-      xcd_contiguous(blockIdx.x, gridDim.x) * (blockDim.x / kWave) +
-      wave_in_group();
-  if (wave >= waves)
-    return; // wave-uniform
-  const int r_lo =
-      wave == 0 ? 0
-                : row_search_uniform(ro, 0u, (uint32_t)rows + 1u,
-                                     (int32_t)(wave * chunk - 1)) + 1;
-  const int r_hi =
-      wave == waves - 1
-          ? rows
-          : row_search_gallop(ro, (uint32_t)r_lo, (uint32_t)rows + 1u,
-                              (int32_t)((wave + 1) * chunk - 1)) + 1;
   if (r_lo >= r_hi)
-    return; // no row begins in this chunk
+    return; // no rows
   // positions of the owned rows, kept inside [0, nnz]
   const int32_t p_beg = std::min(std::max(ro[r_lo], 0), nnz);
   const int32_t p_end = std::min(std::max(ro[r_hi], p_beg), nnz);
 
-  __shared__ int32_t window[256 / kWave][kWave];
-  int32_t *win = window[wave_in_group()];
   constexpr int32_t kStep = kWave * P;
   const int32_t a0 = VEC ? (p_beg & ~3) : p_beg;
   int r_cur = r_lo;          // row of the step's first position
@@ -697,6 +659,110 @@ __global__ __launch_bounds__(256) void spmv_row_owner(
   for (int r = r_lo + lane; r < r_hi; r += kWave)
     if (ro[r] == ro[r + 1])
       y[r] = 0.0f;
+}
+
+// ---------------------------------------------------------------------------
+// wave-per-row-balanced: row-owner SpMV (Wave64 extension).
+//
+// The nonzeros are cut into chunks of C = 64 * P * S positions, and wave w
+// owns the rows whose first position lies in chunk w (ro[r] in
+// [wC, (w+1)C); rows beginning at or past the last chunk's start belong to
+// the last wave).  So every output row has exactly one writer, which stores
+// it with a plain store: no zero fill and no atomics, and the work stays
+// balanced by nonzeros (a wave's rows hold C positions give or take the row
+// that straddles each chunk end).  Waves run in XCD-contiguous order, so the
+// short row ranges that neighbouring waves store share one XCD's L2.
+//
+// A wave finds its first row (a wave-uniform binary search) and the first
+// row of the next chunk (a gallop from there), then walks its positions
+// [ro[r_lo], ro[r_hi]) in steps of 64 * P: lane l takes P consecutive
+// positions, finds the row of its first position in an LDS window of 64 row
+// ends, and walks them as the position kernel does -- rows that begin and end
+// inside the lane are stored directly, a lane's first and last rows are
+// joined across lanes by the DPP segmented scan.  A row still open at the
+// end of a step is carried, wave-uniform, into the next step's lane 0.
+// Rows with no entries, which no position reaches, are stored as zero by a
+// pass over the wave's rows.
+//
+// Every sum is formed in a fixed order (a lane's positions in sequence, the
+// scan's fixed DPP steps, the carry), so repeated calls give bit-identical
+// outputs, which the atomic position mappings do not.  It costs time: on
+// configuration 2 (P = 4, S = 4) 235 us against the position kernel's
+// 207 us; S = 1 248 us, S = 2 240 us; loading each step's values one step
+// ahead measured no faster (237 us).  A wave's rows run to the end of the
+// row that straddles its chunk end, so the few waves holding the start of a
+// row of thousands of entries finish last.
+template <int P, bool VEC>
+__global__ __launch_bounds__(256) void spmv_row_owner(
+    const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
+    const float *__restrict__ val, const float *__restrict__ x,
+    float *__restrict__ y, int32_t rows, int32_t nnz, int64_t chunk,
+    int64_t waves) {
+  const int64_t wave =
+      xcd_contiguous(blockIdx.x, gridDim.x) * (blockDim.x / kWave) +
+      wave_in_group();
+  if (wave >= waves)
+    return; // wave-uniform
+  const int r_lo =
+      wave == 0 ? 0
+                : row_search_uniform(ro, 0u, (uint32_t)rows + 1u,
+                                     (int32_t)(wave * chunk - 1)) + 1;
+  const int r_hi =
+      wave == waves - 1
+          ? rows
+          : row_search_gallop(ro, (uint32_t)r_lo, (uint32_t)rows + 1u,
+                              (int32_t)((wave + 1) * chunk - 1)) + 1;
+  __shared__ int32_t window[256 / kWave][kWave];
+  owner_rows<P, VEC>(ro, col, val, x, y, r_lo, r_hi, nnz,
+                     window[wave_in_group()]);
+}
+
+// ---------------------------------------------------------------------------
+// thread-per-row with whole-wave workgroups: the reference's launch (one
+// thread per row); a wave whose rows are very uneven takes its 64
+// consecutive rows together through owner_rows -- the rows' positions
+// spread evenly over the lanes, so a row of thousands of entries no longer
+// holds its wave for hundreds of dependent steps.  Each row is stored once,
+// its sum formed in a fixed order (in such waves not the reference's
+// sequential order: within the fp32 bound).
+template <int P, bool VEC, bool NARROW>
+__global__ __launch_bounds__(1024) void spmv_thread_per_row_waves(
+    const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
+    const float *__restrict__ val, const float *__restrict__ x,
+    float *__restrict__ y, int32_t rows, int32_t nnz) {
+  const int64_t r0 = (int64_t)blockIdx.x * blockDim.x +
+                     (int64_t)wave_in_group() * kWave;
+  if (r0 >= rows)
+    return; // wave-uniform
+  const int r_hi = (int)std::min<int64_t>(r0 + kWave, rows);
+  // A wave whose longest row takes a thread at most kWalkFactor times the
+  // steps of the shared walk (64 P positions a step) sums each row in its
+  // own lane, as the reference does: the walk pays off only where one row
+  // holds most of the wave's positions (longest row above 8x the wave's
+  // mean at P = 4).  Factor 1 / 2 / 4: configuration 2 254.7 / 268.9 /
+  // 301.7 us, the harness's skewed/32 matrix 21.3 / 9.3 / 9.2 us, skewed/256
+  // 126.4 / 78.5 / 78.5 us, uniform rows (configuration 1, uniform/32,
+  // uniform/256) no different; the walk always: uniform/256 138 us against
+  // 50 us one row per lane.
+  const int64_t r = r0 + lane_id();
+  const int nt = r_hi - (int)r0; // rows of this wave, 1 .. 64
+  const int32_t s = ro[r0 + std::min<int64_t>(lane_id(), nt - 1)];
+  const int32_t e = r < rows ? ro[r + 1] : s;
+  // the wave's positions from its first and last lanes, and one ballot:
+  // does a row need more than kWalkFactor times the walk's steps?
+  constexpr int kWalkFactor = 2;
+  const int32_t total = __builtin_amdgcn_readlane(e, nt - 1) -
+                        __builtin_amdgcn_readlane(s, 0);
+  const int32_t steps = (total + kWave * P - 1) / (kWave * P);
+  if (__builtin_amdgcn_ballot_w64(e - s > kThreadRowDeep * kWalkFactor *
+                                              steps) == 0) {
+    if (r < rows)
+      y[r] = strided_dot<NARROW, kThreadRowDeep>(col, val, x, s, e, 1, 0.0f);
+    return;
+  }
+  __shared__ int32_t window[1024 / kWave][kWave];
+  owner_rows<P, VEC>(ro, col, val, x, y, (int)r0, r_hi, nnz,
+                     window[wave_in_group()]);
 }
 
 // ---------------------------------------------------------------------------
@@ -944,6 +1010,22 @@ int launch_spmv(const int32_t *ro, const int32_t *col, const float *val,
   if (streq(o.spmv_mapping, "thread-per-row")) {
     int64_t grid = std::max<int64_t>(ceil_div(rows, B), 1);
     dim3 g((unsigned)grid), b((unsigned)B);
+    // whole-wave workgroups: uneven waves take their 64 rows together
+    // (configuration 2, 256-thread blocks: 438 -> 269 us)
+    if (B % kWave == 0) {
+      const bool vec = aligned16(col) && aligned16(val) && narrow &&
+                       narrow_offsets(nnz, 1);
+      if (vec)
+        hipLaunchKernelGGL((spmv_thread_per_row_waves<4, true, true>), g, b,
+                           0, st, ro, col, val, x, y, n, (int32_t)nnz);
+      else if (narrow)
+        hipLaunchKernelGGL((spmv_thread_per_row_waves<4, false, true>), g, b,
+                           0, st, ro, col, val, x, y, n, (int32_t)nnz);
+      else
+        hipLaunchKernelGGL((spmv_thread_per_row_waves<4, false, false>), g, b,
+                           0, st, ro, col, val, x, y, n, (int32_t)nnz);
+      return launch_check("thread-per-row SpMV kernel");
+    }
     if (narrow)
       hipLaunchKernelGGL(spmv_thread_per_row<true>, g, b, 0, st, ro, col, val,
                          x, y, n);
