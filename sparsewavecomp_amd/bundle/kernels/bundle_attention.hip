@@ -96,10 +96,12 @@ __device__ __forceinline__ void scores_row(
   }
 }
 
-#if SW_HEAD_DIM == 64 || SW_HEAD_DIM == 128
+#if (SW_HEAD_DIM == 64 || SW_HEAD_DIM == 128) && \
+    4LL * SW_HEAD_DIM * SW_KEY_ROWS <= 0xFFFFFFFFLL
 // The workgroup's 64 rows (one wave: the launch is one work-item per row, 64
 // per workgroup) as one matrix-core tile when they share the column prefix
-// structure of block masks (the library's code, csrc/sw_sddmm_tile64.h);
+// structure of block masks (the library's code, csrc/sw_sddmm_tile64.h,
+// whose lane offsets into the transposed key fit 32 bits);
 // otherwise each row by its own work-item.
 #include "../../csrc/sw_sddmm_tile64.h"
 

@@ -1847,23 +1847,22 @@ int launch_sddmm(const int32_t *ro, const int32_t *col, const T *val,
     // threads); four under the 1024-thread bound.  kdim 64 or 128 and whole
     // waves of at most 256-thread workgroups (one wave per SIMD, so the tile
     // and the per-row steps have 512 registers without spills; bf16 also a
-    // 16-byte aligned lhs): 64-row matrix-core tiles first
+    // 16-byte aligned lhs), with the rhs's bytes within 32 bits (the
+    // tile's lane offsets): 64-row matrix-core tiles first
     const bool tiles = (kdim == 64 || kdim == 128) && B % kWave == 0 &&
-                       B <= 256 && (sizeof(T) == 4 || aligned16(lhs));
-    {
-      if (tiles && kdim == 64)
-        hipLaunchKernelGGL((sddmm_thread_per_row<T, 16, 256, 1>),
-                           dim3((unsigned)grid), dim3((unsigned)B), 0, st, ro,
-                           col, val, lhs, rhs, out, (int32_t)rows, cols,
-                           (int32_t)kdim, kind, alpha, beta);
-      else if (tiles)
-        hipLaunchKernelGGL((sddmm_thread_per_row<T, 16, 256, 2>),
-                           dim3((unsigned)grid), dim3((unsigned)B), 0, st, ro,
-                           col, val, lhs, rhs, out, (int32_t)rows, cols,
-                           (int32_t)kdim, kind, alpha, beta);
-    }
-    if (tiles) {
-    } else if (B <= 512)
+                       B <= 256 && (sizeof(T) == 4 || aligned16(lhs)) &&
+                       (int64_t)sizeof(T) * kdim * cols <= (int64_t)UINT32_MAX;
+    if (tiles && kdim == 64)
+      hipLaunchKernelGGL((sddmm_thread_per_row<T, 16, 256, 1>),
+                         dim3((unsigned)grid), dim3((unsigned)B), 0, st, ro,
+                         col, val, lhs, rhs, out, (int32_t)rows, cols,
+                         (int32_t)kdim, kind, alpha, beta);
+    else if (tiles)
+      hipLaunchKernelGGL((sddmm_thread_per_row<T, 16, 256, 2>),
+                         dim3((unsigned)grid), dim3((unsigned)B), 0, st, ro,
+                         col, val, lhs, rhs, out, (int32_t)rows, cols,
+                         (int32_t)kdim, kind, alpha, beta);
+    else if (B <= 512)
       hipLaunchKernelGGL((sddmm_thread_per_row<T, 16, 512>),
                          dim3((unsigned)grid), dim3((unsigned)B), 0, st, ro,
                          col, val, lhs, rhs, out, (int32_t)rows, cols,

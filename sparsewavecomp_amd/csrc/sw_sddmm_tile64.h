@@ -15,14 +15,14 @@
 // the gathered rhs columns as the A operand and four 16-row lhs tiles as B
 // operands, so that lane (i, g) holds row 16 R + i's dot products at
 // entries t0 + 4g .. t0 + 4g + 3 (both products leave that layout).  A bf16
-// result is rounded to bf16 once, as it is stored.  The next chunk's rhs
-// gathers and sample values are in flight over a chunk's products; each
+// result is rounded to bf16 once, as it is stored.  The next two chunks'
+// rhs gathers and sample values are in flight over a chunk's products; each
 // buffer is named (a buffer indexed by a run-time variable becomes indexed
 // register moves behind a wait for every load).
 //
 // The structure check reads every column index of the tile once: each row
 // against the last row's columns, which the wave stages in its LDS slice,
-// 8 rows' loads per batch, every load from a clamped valid position.  A tile
+// 16 rows' 16-byte loads per batch, every load from a valid window.  A tile
 // that fails it, or whose last row has more than kTileCols entries, stores
 // nothing and the function returns false; the caller computes those rows
 // another way.  Sums are formed by the matrix cores (the dot's order
@@ -40,10 +40,11 @@ namespace sw_tile64 {
 
 using swd::v2u;
 using swd::v4f;
+using swd::v4i;
 using swd::v4u;
 
 constexpr int kTileCols = 512; // the last row's entries held in LDS
-constexpr int kCheckRows = 8;  // rows whose columns one check batch loads
+constexpr int kCheckRows = 32; // rows whose columns one check batch loads
 
 __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -55,7 +56,14 @@ __device__ __forceinline__ void wave_sync() {
 //   out[p] = combine(sample[p] (0 without samples), lhs row . rhs col)
 // with kdim = 64 KB; T is float or uint16_t (bf16 bits; lhs then 16-byte
 // aligned); lcol is this wave's LDS slice of kTileCols entries.  Every lane
-// of the wave calls it with the same r0.  SAMPLES: sample is not null (a
+// of the wave calls it with the same r0.  The caller guarantees that
+// sizeof(T) kdim cols fits 32 bits, and a tile whose positions end past
+// 2^32 / 4 takes the rows' own path: every gather, sample load and store
+// takes a wave-uniform base (scalar registers) and a 32-bit lane byte
+// offset, the form the memory instructions take directly, so no lane
+// computes a 64-bit address (with 64-bit addresses the address registers of
+// three chunks in flight pushed the wave to reuse the registers of loads
+// still in flight, a full wait every three chunks).  SAMPLES: sample is not null (a
 // compile-time flag: a run-time test beside each sample load became a
 // branch around it, which split the chunk's batch of loads: 78 -> 90 us
 // on configuration 5's bundle).
@@ -75,11 +83,12 @@ __device__ __forceinline__ bool sddmm_tile64(
   const int i = l & 15, g = l >> 4;
   const int nt = rows - r0 < 64 ? (int)(rows - r0) : 64; // >= 1
   const int64_t rr = r0 + (l < nt ? l : nt - 1);
-  const int32_t rb = ro[rr];
-  const int32_t rlen = l < nt ? ro[rr + 1] - rb : 0;
+  const int32_t rb = ro[rr], re = ro[rr + 1]; // one trip: no load is guarded
+  const int32_t rlen = l < nt ? re - rb : 0;
   const int32_t bl = __builtin_amdgcn_readlane(rb, nt - 1);
   const int32_t len_last = __builtin_amdgcn_readlane(rlen, nt - 1);
-  if (len_last > kTileCols)
+  if (len_last > kTileCols ||
+      (int64_t)bl + len_last > (int64_t)(UINT32_MAX / 4))
     return false;
   if (len_last == 0) {
     // an empty last row: a prefix tile only when every row is empty (and
@@ -88,36 +97,69 @@ __device__ __forceinline__ bool sddmm_tile64(
   }
   {
     // entries past the last row's end repeat its final column, so that a
-    // chunk's lanes read valid columns without a check
-    const int span = (len_last + 15) & ~15;
-    for (int t = l; t < span; t += 64)
-      lcol[t] = col[bl + (t < len_last ? t : len_last - 1)];
-    wave_sync();
-    // every load unconditional, from a clamped valid position (a row's last
-    // entry, or the last row's first for an empty row), so that no branch
-    // splits a batch; the compare then selects the entries in range
-    bool mine = rlen <= len_last;
-    for (int i0 = 0; i0 < nt; i0 += kCheckRows) {
-      int32_t x[kCheckRows][kTileCols / 64];
+    // chunk's lanes read valid columns without a check; one batch of
+    // clamped loads for all kTileCols slots (a loop up to the row's end
+    // waited for each load before its store)
+    {
+      int32_t y[kTileCols / 64];
 #pragma unroll
-      for (int j = 0; j < kCheckRows; ++j) {
-        const int row = i0 + j < nt ? i0 + j : nt - 1;
-        const int32_t b = __builtin_amdgcn_readlane(rb, row);
-        const int32_t n = __builtin_amdgcn_readlane(rlen, row);
-#pragma unroll
-        for (int u = 0; u < kTileCols / 64; ++u) {
-          const int t = l + 64 * u;
-          x[j][u] = col[n > 0 ? b + (t < n ? t : n - 1) : bl];
-        }
+      for (int u = 0; u < kTileCols / 64; ++u) {
+        const int t = l + 64 * u;
+        y[u] = *swd::at_bytes(
+            col, 4u * (uint32_t)(bl + (t < len_last ? t : len_last - 1)));
       }
 #pragma unroll
-      for (int j = 0; j < kCheckRows; ++j) {
-        const int row = i0 + j < nt ? i0 + j : nt - 1;
-        const int32_t n = __builtin_amdgcn_readlane(rlen, row);
+      for (int u = 0; u < kTileCols / 64; ++u)
+        lcol[l + 64 * u] = y[u];
+    }
+    wave_sync();
+    // Every row but the last against the last row's columns, kCheckRows
+    // rows per batch: lane l compares entries t = 4l .. 4l + 3 and
+    // 256 + 4l .. + 3 of each row, read as two element-aligned 16-byte
+    // loads (one wave per CU, as both callers launch it, keeps only its own
+    // loads in flight: 4-byte loads, 8 rows per batch, made this check half
+    // of the tile's time).  Every load is unconditional: the window of
+    // entry t of a row starting at b is read from min(b + t, te - 4), te
+    // the end of the tile's positions, so it lies inside the tile; entries
+    // past a row's end read the next rows' columns and are compared with
+    // nothing.  A window holding a compared entry is never moved: a row
+    // before the last ends at or before the last row's start bl, so its
+    // window starts at b + t < bl <= te - 4 when the last row holds at
+    // least four entries (a tile whose last row holds fewer takes the rows'
+    // own path).
+    if (len_last < 4)
+      return false;
+    const int64_t te = (int64_t)bl + len_last;
+    bool mine = rlen <= len_last;
+    for (int i0 = 0; i0 < nt - 1; i0 += kCheckRows) {
+      v4i x[kCheckRows][2];
 #pragma unroll
-        for (int u = 0; u < kTileCols / 64; ++u) {
-          const int t = l + 64 * u;
-          mine &= !(t < n && t < len_last) || x[j][u] == lcol[t];
+      for (int j = 0; j < kCheckRows; ++j) {
+        const int row = i0 + j < nt - 1 ? i0 + j : nt - 1;
+        const int64_t b = __builtin_amdgcn_readlane(rb, row);
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int64_t w = std::min<int64_t>(b + 4 * l + 256 * u, te - 4);
+          __builtin_memcpy(&x[j][u], swd::at_bytes(col, 4u * (uint32_t)w),
+                           sizeof(v4i));
+        }
+      }
+      // the batch's loads stay together (the scheduler otherwise moves each
+      // next to its compare, a wait between every few loads)
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int j = 0; j < kCheckRows; ++j) {
+        const int row = i0 + j < nt - 1 ? i0 + j : nt - 1;
+        const int32_t n = __builtin_amdgcn_readlane(rlen, row);
+        const int32_t lim = n < len_last ? n : len_last; // wave-uniform
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int t = 4 * l + 256 * u;
+          v4i ref;
+          __builtin_memcpy(&ref, lcol + t, sizeof ref);
+#pragma unroll
+          for (int m = 0; m < 4; ++m)
+            mine &= !(t + m < lim) || x[j][u][m] == ref[m];
         }
       }
     }
@@ -165,22 +207,33 @@ __device__ __forceinline__ bool sddmm_tile64(
   // at the column of entry t0 + i in fp32; rhs[32 st + 8 g + e], e = 0..7,
   // as four bf16 pairs in bf16) and the samples of the entries its lanes
   // store, each from a clamped valid position (selected afterwards)
+  const __amdgpu_buffer_rsrc_t krs =
+      swd::buffer_rsrc(rhs, (uint32_t)(sizeof(T) * kdim * cols));
   auto load = [&](int t0, Op (&a)[S], float (&mv)[4][4])
       __attribute__((always_inline)) {
-    const int64_t c = lcol[t0 + i];
+    const uint32_t c = lcol[t0 + i];
+    // buffer loads over rhs: the lane's rows (16 g, or 8 g in bf16) and
+    // column c as its offset, rhs row 64 kb + st (32 st + e) as the
+    // wave-uniform offset, so that one lane offset serves every step (as
+    // global loads each step's row base took a 64-bit lane address)
     if constexpr (kF32) {
+      const uint32_t ko = 4u * (16u * g * (uint32_t)cols + c);
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
         for (int st = 0; st < 16; ++st)
-          a[16 * kb + st] = rhs[(int64_t)(64 * kb + 16 * g + st) * cols + c];
+          a[16 * kb + st] = swd::buffer_load_f32(
+              krs, ko, 4u * (uint32_t)(64 * kb + st) * (uint32_t)cols);
     } else {
+      const uint32_t ko = 2u * (8u * g * (uint32_t)cols + c);
 #pragma unroll
       for (int st = 0; st < S; ++st) {
         uint32_t x[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e)
-          x[e] = rhs[(int64_t)(32 * st + 8 * g + e) * cols + c];
+          x[e] = __builtin_amdgcn_raw_buffer_load_b16(
+              krs, (int)ko, (int)(2u * (uint32_t)(32 * st + e) * (uint32_t)cols),
+              0);
         a[st] = v4u{x[0] | (x[1] << 16), x[2] | (x[3] << 16),
                     x[4] | (x[5] << 16), x[6] | (x[7] << 16)};
       }
@@ -193,7 +246,9 @@ __device__ __forceinline__ bool sddmm_tile64(
         const int32_t p = lenR[R] > 0
                               ? rbR[R] + (t < lenR[R] ? t : lenR[R] - 1)
                               : bl;
-        mv[R][v] = SAMPLES ? swd::tof(sample[p]) : 0.0f;
+        mv[R][v] = SAMPLES ? swd::tof(*swd::at_bytes(
+                                 sample, (uint32_t)(sizeof(T) * p)))
+                           : 0.0f;
       }
   };
   // a chunk's products and its entries' stores (one 16-byte store when the
@@ -227,7 +282,7 @@ __device__ __forceinline__ bool sddmm_tile64(
       for (int v = 0; v < 4; ++v)
         sc[v] = combine(mv[R][v], acc[v]);
       const int t = t0 + 4 * g;
-      T *dst = out + rbR[R] + t;
+      T *dst = swd::at_bytes(out, (uint32_t)(sizeof(T) * (rbR[R] + t)));
       if (t + 3 < lenR[R]) {
         if constexpr (kF32) {
           __builtin_memcpy(dst, &sc, sizeof sc);
@@ -244,20 +299,33 @@ __device__ __forceinline__ bool sddmm_tile64(
       }
     }
   };
-  // chunks in pairs, each buffer named: the next chunk's loads fly over a
-  // chunk's products
-  Op a0[S], a1[S];
-  float m0[4][4], m1[4][4];
-  load(0, a0, m0);
-  for (int t0 = 0; t0 < len_last; t0 += 32) {
-    if (t0 + 16 < len_last)
-      load(t0 + 16, a1, m1);
-    compute(t0, a0, m0);
-    if (t0 + 16 >= len_last)
+  // three chunks in flight, each buffer named: the loads of chunks j + 1
+  // and j + 2 fly over chunk j's products.  Every chunk's loads are issued
+  // unconditionally -- those of the (at most two) chunks past the last
+  // repeat the last chunk's -- so that the compiler's wait before a chunk's
+  // products counts the later chunks' loads as outstanding; a load inside a
+  // branch made it wait for them too.
+  const int nch = (len_last + 15) >> 4; // >= 1
+  auto t_of = [&](int j) __attribute__((always_inline)) {
+    return 16 * (j < nch ? j : nch - 1);
+  };
+  Op a0[S], a1[S], a2[S];
+  float m0[4][4], m1[4][4], m2[4][4];
+  load(t_of(0), a0, m0);
+  load(t_of(1), a1, m1);
+  for (int j = 0;; j += 3) {
+    load(t_of(j + 2), a2, m2);
+    compute(16 * j, a0, m0);
+    if (j + 1 >= nch)
       break;
-    if (t0 + 32 < len_last)
-      load(t0 + 32, a0, m0);
-    compute(t0 + 16, a1, m1);
+    load(t_of(j + 3), a0, m0);
+    compute(16 * (j + 1), a1, m1);
+    if (j + 2 >= nch)
+      break;
+    load(t_of(j + 4), a1, m1);
+    compute(16 * (j + 2), a2, m2);
+    if (j + 3 >= nch)
+      break;
   }
   return true;
 }

@@ -329,6 +329,73 @@ def test_block_per_row_short_and_long_rows(dev, orc, block):
     assert y[0] == 0.0 and not np.signbit(y[0])
 
 
+def _walking_waves(ro, rows_per_wave=64, positions_per_step=256, deep=16,
+                   factor=2):
+    """Waves (64 consecutive rows) for which thread-per-row in whole-wave
+    workgroups walks the rows together: a row longer than factor * deep
+    times the wave's steps of positions_per_step positions.  Used only to
+    show that a test matrix reaches both forms."""
+    out = []
+    rows = len(ro) - 1
+    for w in range(0, rows, rows_per_wave):
+        hi = min(w + rows_per_wave, rows)
+        lens = np.diff(ro[w:hi + 1])
+        steps = -(-int(ro[hi] - ro[w]) // positions_per_step)
+        out.append(bool((lens > deep * factor * steps).any()))
+    return out
+
+
+@pytest.mark.parametrize("block", [64, 256, 1024])
+@pytest.mark.parametrize("aligned", [True, False])
+def test_thread_per_row_uneven_waves(dev, orc, block, aligned):
+    """thread-per-row in whole-wave workgroups: a wave whose longest row
+    holds far more than the wave's mean sums its 64 rows together (the
+    row-owner walk), other waves one row per lane.  Waves with the long row
+    first, last or in the middle, among empty and one-entry rows, a wave of
+    empty rows, a row just under and just over the walk's threshold, and a
+    long row in the final partial wave; 16-byte aligned and element-aligned
+    col / val (vector and scalar loads)."""
+    rng = np.random.default_rng(block + aligned)
+    lengths = []
+    lengths += [3000] + [0] * 63                       # long row at lane 0
+    lengths += [1] * 63 + [2500]                       # long row at lane 63
+    lengths += [20] * 64                               # even: one per lane
+    lengths += [0] * 30 + [4096] + [0] * 33            # long row mid-wave
+    lengths += [0] * 64                                # no entries at all
+    # 63 rows of 4 and one row of L: steps = ceil((252 + L) / 256); the
+    # walk when L > 32 steps -- L = 64 stays per lane, L = 65 walks
+    lengths += [4] * 63 + [64]
+    lengths += [4] * 63 + [65]
+    lengths += [7] * 36 + [1800]                       # partial last wave
+    rows, cols = len(lengths), 6000
+    ro = np.zeros(rows + 1, np.int32)
+    np.cumsum(lengths, out=ro[1:])
+    walks = _walking_waves(ro)
+    assert walks == [True, True, False, True, False, False, True, True]
+    col = np.concatenate([np.sort(rng.choice(cols, n, replace=False))
+                          for n in lengths]).astype(np.int32)
+    val = rng.uniform(-1, 1, col.size).astype(np.float32)
+    x = rng.uniform(-1, 1, cols).astype(np.float32)
+    csr = W.CSR(rows, cols, ro, col, val)
+    opts = f"spmv-mapping=thread-per-row spmv-block-size={block}"
+    if aligned:
+        y = G.spmv(csr, x, opts)
+    else:
+        G.say(f"thread-per-row uneven waves, element-aligned, B={block}")
+        colp = torch.zeros(csr.nnz + 1, dtype=torch.int32, device=G.DEV)
+        valp = torch.zeros(csr.nnz + 1, dtype=torch.float32, device=G.DEV)
+        colp[1:] = G.t(col)
+        valp[1:] = G.t(val)
+        assert colp[1:].data_ptr() % 16 != 0
+        yt = torch.full((rows,), float("nan"), device=G.DEV)
+        sw.spmv(G.t(ro), colp[1:], valp[1:], G.t(x), yt, options=opts)
+        torch.cuda.synchronize()
+        y = yt.cpu().numpy()
+    _check(orc, csr, x, y)
+    empty = np.asarray(lengths) == 0
+    assert (y[empty] == 0.0).all()
+
+
 def test_repeat_is_stable(dev, orc):
     """Position mappings zero the output on every call (no accumulation
     across calls)."""
