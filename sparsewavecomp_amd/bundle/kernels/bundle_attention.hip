@@ -229,23 +229,20 @@ SW_KERNEL SW_ROW_MAP_NAME(const int32_t *__restrict__ rowOffsets,
 #endif
 #elif SW_ATTENTION_ROLE == 6
 #if SW_VALUE_COLS % 64 == 0
-// One wave per 64 output columns of one row (the launch is one work-item
-// per output element): the row's column indices and probabilities are the
-// same in every lane, so they come through scalar loads, kOutDeep entries
-// at a time, and each lane gathers its V column; products are added in
-// position order, as one work-item per element does.
+#include "../../csrc/sw_device.h"
+
+// Row r's 64 output columns c0 .. c0 + 63 by one wave (lane l: column
+// c0 + l): the row's column indices and probabilities are the same in
+// every lane, so they come through scalar loads, kOutDeep entries at a
+// time, and each lane gathers its V column; products are added in position
+// order, as one work-item per element does.
 constexpr int kOutDeep = 32;
 
-SW_KERNEL sparse_attention_output(const int32_t *__restrict__ rowOffsets,
-                                  const int32_t *__restrict__ columnIndices,
-                                  const float *__restrict__ scores,
-                                  const float *__restrict__ value,
-                                  float *__restrict__ output) {
-  const int e0 = blockIdx.x * 64; // the wave's first output element
-  const int r = e0 / SW_VALUE_COLS;
-  const int c = e0 - r * SW_VALUE_COLS + (int)__builtin_amdgcn_workitem_id_x();
-  if (r >= SW_ROWS)
-    return;
+__device__ __forceinline__ void output_row(
+    const int32_t *__restrict__ rowOffsets,
+    const int32_t *__restrict__ columnIndices,
+    const float *__restrict__ scores, const float *__restrict__ value,
+    float *__restrict__ output, int r, int c) {
   const int32_t pe = rowOffsets[r + 1];
   int32_t p = rowOffsets[r];
   float acc = 0.0f;
@@ -284,6 +281,204 @@ SW_KERNEL sparse_attention_output(const int32_t *__restrict__ rowOffsets,
       acc = p + u < pe ? __builtin_fmaf(sv[u], vv[u], acc) : acc;
   }
   output[(int64_t)r * SW_VALUE_COLS + c] = acc;
+}
+
+// Rows r0 .. r0 + 15 (those below SW_ROWS), output columns nb .. nb + 63, by
+// one wave on the matrix cores, when every row's columns are a prefix of
+// the tile's last row's (block masks) and the last row holds 4 to
+// kOutTileCols entries: C = P V over the last row's entries, 16 at a time
+// (four v_mfma_f32_16x16x4_f32 steps per 16-column output tile), lane
+// (i, g) supplying P[row i][t0 + 4g + st] (zero past row i's end) and lane
+// (j, g) V[c_{t0+4g+st}][nb + 4j + n] for the four output tiles n, whose
+// columns interleave (tile n's column j is output column nb + 4j + n) so
+// that one 16-byte load of a V row feeds all four.  Each V row a chunk
+// reads serves the tile's 16 rows (one wave per row and 64 columns read it
+// once per row: 724 MB of V rows from L2 on configuration 5).  Returns
+// false (nothing stored) for other tiles; every output stored is checked
+// and a tile with an inf or NaN output returns false too, as an inf or NaN
+// V row that a shorter row leaves out reaches that row as 0 * inf.
+constexpr int kOutTileCols = 512;
+constexpr int kOutSub = 2; // 16-entry chunks per load step (three in flight)
+
+__device__ __forceinline__ bool output_tile16(
+    const int32_t *__restrict__ rowOffsets,
+    const int32_t *__restrict__ columnIndices,
+    const float *__restrict__ scores, const float *__restrict__ value,
+    float *__restrict__ output, int r0, int nb, int32_t *lcol) {
+  using swd::at_bytes;
+  using swd::v4f;
+  typedef int v4i __attribute__((ext_vector_type(4)));
+  const int l = __lane_id(), i = l & 15, g = l >> 4;
+  const int nt = SW_ROWS - r0 < 16 ? SW_ROWS - r0 : 16;
+  // lanes 0 .. nt hold rowOffsets[r0 .. r0 + nt] (one trip)
+  const int32_t my_ro = rowOffsets[r0 + (l < nt ? l : nt)];
+  const int32_t bl = __builtin_amdgcn_readlane(my_ro, nt - 1);
+  const int32_t te = __builtin_amdgcn_readlane(my_ro, nt);
+  const int32_t len_last = te - bl;
+  if (len_last < 4 || len_last > kOutTileCols ||
+      (int64_t)te > (int64_t)(UINT32_MAX / 4))
+    return false;
+  // row i's first position and length (lanes of rows past nt: length 0)
+  const int ic = i < nt ? i : nt - 1;
+  const int32_t ra = __builtin_amdgcn_ds_bpermute(ic << 2, my_ro);
+  const int32_t la =
+      i < nt ? __builtin_amdgcn_ds_bpermute((ic + 1) << 2, my_ro) - ra : 0;
+  // the last row's columns in LDS, slots past its end repeating its final
+  // column; then every row but the last against them: lane l compares
+  // entries 4l .. 4l + 3 and 256 + 4l .. + 3, read as element-aligned
+  // 16-byte windows from min(b + t, te - 4) (a window holding a compared
+  // entry never moves: such a row ends at or before bl <= te - 4)
+  {
+    int32_t y[kOutTileCols / 64];
+#pragma unroll
+    for (int u = 0; u < kOutTileCols / 64; ++u) {
+      const int t = l + 64 * u;
+      y[u] = *at_bytes(columnIndices,
+                       4u * (uint32_t)(bl + (t < len_last ? t : len_last - 1)));
+    }
+    v4i x[15][2];
+#pragma unroll
+    for (int j = 0; j < 15; ++j) {
+      const int row = j < nt - 1 ? j : nt - 1;
+      const int32_t b = __builtin_amdgcn_readlane(my_ro, row);
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int32_t w = std::min(b + 4 * l + 256 * u, te - 4);
+        __builtin_memcpy(&x[j][u], at_bytes(columnIndices, 4u * (uint32_t)w),
+                         sizeof(v4i));
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < kOutTileCols / 64; ++u)
+      lcol[l + 64 * u] = y[u];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    bool mine = true;
+#pragma unroll
+    for (int j = 0; j < 15; ++j) {
+      const int row = j < nt - 1 ? j : nt - 1;
+      const int32_t b = __builtin_amdgcn_readlane(my_ro, row);
+      const int32_t n = __builtin_amdgcn_readlane(my_ro, row + 1) - b;
+      mine &= n <= len_last;
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int t = 4 * l + 256 * u;
+        v4i ref;
+        __builtin_memcpy(&ref, lcol + t, sizeof ref);
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+          mine &= !(t + m < n) || x[j][u][m] == ref[m];
+      }
+    }
+    if (__builtin_amdgcn_ballot_w64(!mine) != 0)
+      return false;
+  }
+  // one step's operands (kOutSub 16-entry chunks): P for entries
+  // t0 + 16h + 4g .. + 3 of row i (positions clamped into the row, or the
+  // last row's first for an empty row; zero past the row), and the V rows
+  // of those entries' columns
+  auto load = [&](int t0, float (&a)[kOutSub][4], v4f (&bv)[kOutSub][4])
+      __attribute__((always_inline)) {
+#pragma unroll
+    for (int h = 0; h < kOutSub; ++h)
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        const int t = t0 + 16 * h + 4 * g + st;
+        const int32_t q = la > 0 ? ra + (t < la ? t : la - 1) : bl;
+        a[h][st] = *at_bytes(scores, 4u * (uint32_t)q);
+        const uint32_t c = lcol[t];
+        bv[h][st] = *reinterpret_cast<const v4f *>(
+            value + (int64_t)c * SW_VALUE_COLS + nb + 4 * i);
+      }
+  };
+  v4f acc[4];
+#pragma unroll
+  for (int n = 0; n < 4; ++n)
+    acc[n] = v4f{0.f, 0.f, 0.f, 0.f};
+  auto compute = [&](int t0, const float (&a)[kOutSub][4],
+                     const v4f (&bv)[kOutSub][4])
+      __attribute__((always_inline)) {
+#pragma unroll
+    for (int h = 0; h < kOutSub; ++h)
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        const float pa = t0 + 16 * h + 4 * g + st < la ? a[h][st] : 0.0f;
+#pragma unroll
+        for (int n = 0; n < 4; ++n)
+          acc[n] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa, bv[h][st][n],
+                                                        acc[n], 0, 0, 0);
+      }
+  };
+  // three steps in flight, every step's loads unconditional (steps past
+  // the last re-read the last), each buffer named.  The loop body has no
+  // exit between its three steps, so that it is one block and a scheduling
+  // barrier after each step's loads keeps them where they are issued (the
+  // scheduler sank the P loads to their products, and an exit between the
+  // steps let the compiler move a step's loads past the next step's
+  // products): up to two steps past the last are computed, with P zero (a
+  // step's entries past the last row hold P = 0; an inf or NaN in the V row
+  // they repeat makes the tile take the row-by-row path).
+  constexpr int kStep = 16 * kOutSub;
+  const int nch = (len_last + kStep - 1) / kStep; // steps
+  auto t_of = [&](int k) __attribute__((always_inline)) {
+    return kStep * (k < nch ? k : nch - 1);
+  };
+  float a0[kOutSub][4], a1[kOutSub][4], a2[kOutSub][4];
+  v4f b0[kOutSub][4], b1[kOutSub][4], b2[kOutSub][4];
+  load(t_of(0), a0, b0);
+  load(t_of(1), a1, b1);
+  for (int k = 0; k < nch; k += 3) {
+    load(t_of(k + 2), a2, b2);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(kStep * k, a0, b0);
+    load(t_of(k + 3), a0, b0);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(kStep * (k + 1), a1, b1);
+    load(t_of(k + 4), a1, b1);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(kStep * (k + 2), a2, b2);
+  }
+  // lane (j, g) holds C[4g + v][4j + n] in acc[n][v]
+  bool nonfinite = false;
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const v4f o = {acc[0][v], acc[1][v], acc[2][v], acc[3][v]};
+    nonfinite |= !(__builtin_isfinite(o.x) && __builtin_isfinite(o.y) &&
+                   __builtin_isfinite(o.z) && __builtin_isfinite(o.w));
+    const int rr = 4 * g + v;
+    if (rr < nt)
+      *reinterpret_cast<v4f *>(output + (int64_t)(r0 + rr) * SW_VALUE_COLS +
+                               nb + 4 * i) = o;
+  }
+  return __builtin_amdgcn_ballot_w64(nonfinite) == 0;
+}
+
+// The launch has one work-item per output element, 64 per workgroup: the
+// first (SW_ROWS / 16) (SW_VALUE_COLS / 64) one-wave workgroups each take a
+// 16-row tile of 64 output columns (XCD-spread, as workgroups are dealt to
+// the XCDs in turn) and the rest return; a tile that is not a prefix tile
+// is computed row by row by its wave.
+SW_KERNEL sparse_attention_output(const int32_t *__restrict__ rowOffsets,
+                                  const int32_t *__restrict__ columnIndices,
+                                  const float *__restrict__ scores,
+                                  const float *__restrict__ value,
+                                  float *__restrict__ output) {
+  constexpr int kBlocks = SW_VALUE_COLS / 64;
+  constexpr int kTiles = (SW_ROWS + 15) / 16 * kBlocks;
+  const int wv = blockIdx.x;
+  if (wv >= kTiles)
+    return;
+  __shared__ int32_t lcol[kOutTileCols];
+  const int r0 = wv / kBlocks * 16, nb = wv % kBlocks * 64;
+  if (output_tile16(rowOffsets, columnIndices, scores, value, output, r0, nb,
+                    lcol))
+    return;
+  const int nt = SW_ROWS - r0 < 16 ? SW_ROWS - r0 : 16;
+  for (int r = r0; r < r0 + nt; ++r)
+    output_row(rowOffsets, columnIndices, scores, value, output, r,
+               nb + (int)__builtin_amdgcn_workitem_id_x());
 }
 #else
 SW_KERNEL sparse_attention_output(const int32_t *__restrict__ rowOffsets,

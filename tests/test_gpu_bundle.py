@@ -48,7 +48,23 @@ def _attention_case(case):
     whose 64-row tiles hold the prefix column structure (the scores kernel's
     matrix-core tiles), a partial last tile, 32-row blocks that straddle
     the 64-row tiles and ragged masks (its row-by-row path), and head dims
-    of 64, 128 and 32 (no tiles at 32)."""
+    of 64, 128 and 32 (no tiles at 32).  The "_dv64" / "_dv128" cases give V
+    64 or 128 columns, which the output kernel computes as 16-row
+    matrix-core tiles (prefix tiles) or row by row (the ragged masks);
+    "inf_dv64" puts an inf in a V row that only the last row of a 16-row
+    tile reads, so that the tile's other rows meet 0 * inf and the tile is
+    recomputed row by row."""
+    if case.endswith("_dv64") or case.endswith("_dv128"):
+        base, wide = case.rsplit("_dv", 1)
+        mask, q, kt, v, alpha = _attention_case(base)
+        rng = np.random.default_rng(len(case) + 100)
+        v = rng.standard_normal((mask.cols, int(wide))).astype(np.float32)
+        if base == "inf":
+            v[31, 5] = np.inf  # column 31: row 31, the last of rows 16-31
+        return mask, q, kt, v, alpha
+    if case == "inf":
+        mask, q, kt, v, alpha = W.config5(seed=1, seq=256, d=64)
+        return mask, q, kt, v, alpha
     if case in ("config5", "d128", "d32"):
         d = {"config5": 64, "d128": 128, "d32": 32}[case]
         mask, q, kt, v, alpha = W.config5(seed=0, seq=512, d=d)
@@ -72,11 +88,15 @@ def _attention_case(case):
 
 
 @pytest.mark.parametrize("case", ["config5", "partial", "block32", "ragged0",
-                                  "ragged2", "d128", "d32"])
+                                  "ragged2", "d128", "d32", "config5_dv64",
+                                  "partial_dv64", "block32_dv128",
+                                  "ragged0_dv64", "ragged2_dv64", "d128_dv64",
+                                  "inf_dv64"])
 def test_attention_bundle_matches_oracle(dev, orc, tmp_path, case):
     mask, q, kt, v, alpha = _attention_case(case)
     rows, d, dv = mask.rows, q.shape[1], v.shape[1]
-    beta = 0.0 if case in ("config5", "d128", "d32") else 0.5
+    beta = 0.0 if case.split("_dv")[0] in ("config5", "d128", "d32",
+                                           "inf") else 0.5
     B.build_attention_bundle(tmp_path / "b", rows=rows, key_rows=mask.cols,
                              head_dim=d, value_cols=dv, alpha=alpha,
                              beta=beta)
@@ -100,9 +120,18 @@ def test_attention_bundle_matches_oracle(dev, orc, tmp_path, case):
     torch.cuda.synchronize()
     bun.close()
     # the chain's bounds derived from the per-op bars
+    refs = orc.sparse_attention(mask.row_offsets, mask.column_indices,
+                                mask.values, q, kt, v, alpha, beta)
+    out = bufs["output"].cpu().numpy()
     check_attention_f32(orc, mask, mask.values, q, kt, v, alpha, beta,
                         *(bufs[k].cpu().numpy() for k in (
-                            "scores", "rowMaximum", "rowSum", "output")))
+                            "scores", "rowMaximum", "rowSum")), out, refs)
+    # non-finite outputs in the reference's places and classes
+    ref = np.asarray(refs[3])
+    for cls in (np.isnan, np.isposinf, np.isneginf):
+        assert np.array_equal(cls(out), cls(ref)), cls.__name__
+    if case == "inf_dv64":
+        assert np.isposinf(ref).any() and np.isfinite(ref[16:31]).all()
 
 
 def test_config3_bundle_at_full_size(dev, orc):
