@@ -112,7 +112,7 @@ SW_KERNEL sparse_attention_scores(const int32_t *__restrict__ rowOffsets,
                                   const float *__restrict__ transposedKey,
                                   float *__restrict__ scores) {
   __shared__ int32_t lcol[sw_tile64::kTileCols];
-  if (sw_tile64::sddmm_tile64<float, SW_HEAD_DIM / 64, true>(
+  if (sw_tile64::sddmm_tile64<float, SW_HEAD_DIM / 64, true, false>(
           rowOffsets, columnIndices, maskValues, query, transposedKey, scores,
           SW_ROWS, SW_KEY_ROWS, (int64_t)blockIdx.x * 64, lcol,
           [](float mask, float dot) {

@@ -112,10 +112,10 @@ __global__ __launch_bounds__(LB) void sddmm_thread_per_row(
     auto combine = [&](float sample, float dot) {
       return combine_sddmm(kind, sample, dot, alpha, beta);
     };
-    if (val != nullptr ? sw_tile64::sddmm_tile64<T, TKB, true>(
+    if (val != nullptr ? sw_tile64::sddmm_tile64<T, TKB, true, true>(
                              ro, col, val, lhs, rhs, out, rows, cols, r0,
                              lcol[wave_in_group()], combine)
-                       : sw_tile64::sddmm_tile64<T, TKB, false>(
+                       : sw_tile64::sddmm_tile64<T, TKB, false, false>(
                              ro, col, val, lhs, rhs, out, rows, cols, r0,
                              lcol[wave_in_group()], combine))
       return;

@@ -66,8 +66,12 @@ __device__ __forceinline__ void wave_sync() {
 // still in flight, a full wait every three chunks).  SAMPLES: sample is not null (a
 // compile-time flag: a run-time test beside each sample load became a
 // branch around it, which split the chunk's batch of loads: 78 -> 90 us
-// on configuration 5's bundle).
-template <typename T, int KB, bool SAMPLES, typename Combine>
+// on configuration 5's bundle).  WIDE: each row group's four samples of a
+// lane as one element-aligned window (16 bytes fp32, 8 bytes bf16) instead
+// of four loads (thread-per-row SDDMM in 256-thread workgroups, four tile
+// waves per CU: 69.5 -> 64.7 us on configuration 5; the bundle's one wave
+// per CU: 48.2 -> 50.4 us, so it keeps the four loads).
+template <typename T, int KB, bool SAMPLES, bool WIDE, typename Combine>
 __device__ __forceinline__ bool sddmm_tile64(
     const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
     const T *sample, const T *__restrict__ lhs, const T *__restrict__ rhs,
@@ -87,6 +91,7 @@ __device__ __forceinline__ bool sddmm_tile64(
   const int32_t rlen = l < nt ? re - rb : 0;
   const int32_t bl = __builtin_amdgcn_readlane(rb, nt - 1);
   const int32_t len_last = __builtin_amdgcn_readlane(rlen, nt - 1);
+  const int64_t te = (int64_t)bl + len_last; // the end of the tile's positions
   if (len_last > kTileCols ||
       (int64_t)bl + len_last > (int64_t)(UINT32_MAX / 4))
     return false;
@@ -129,7 +134,6 @@ __device__ __forceinline__ bool sddmm_tile64(
     // own path).
     if (len_last < 4)
       return false;
-    const int64_t te = (int64_t)bl + len_last;
     bool mine = rlen <= len_last;
     for (int i0 = 0; i0 < nt - 1; i0 += kCheckRows) {
       v4i x[kCheckRows][2];
@@ -238,18 +242,48 @@ __device__ __forceinline__ bool sddmm_tile64(
                     x[4] | (x[5] << 16), x[6] | (x[7] << 16)};
       }
     }
+    if constexpr (SAMPLES && WIDE) {
+      // the window of entries t0 + 4g .. + 3 of row 16 R + i read from
+      // min(e, te - 4), e its first position: only the last row's can move
+      // (by d = 1..3; a row before the last ends at or before bl <= te - 4),
+      // and then entry v sits in element v + d
 #pragma unroll
-    for (int R = 0; R < 4; ++R)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int t = t0 + 4 * g + v;
-        const int32_t p = lenR[R] > 0
-                              ? rbR[R] + (t < lenR[R] ? t : lenR[R] - 1)
-                              : bl;
-        mv[R][v] = SAMPLES ? swd::tof(*swd::at_bytes(
-                                 sample, (uint32_t)(sizeof(T) * p)))
-                           : 0.0f;
+      for (int R = 0; R < 4; ++R) {
+        const uint32_t e = (uint32_t)(rbR[R] + t0 + 4 * g);
+        const uint32_t w = std::min(e, (uint32_t)(te - 4));
+        const uint32_t d = e - w;
+        float x[4];
+        if constexpr (kF32) {
+          v4f y;
+          __builtin_memcpy(&y, swd::at_bytes(sample, 4u * w), sizeof y);
+          x[0] = y.x, x[1] = y.y, x[2] = y.z, x[3] = y.w;
+        } else {
+          v2u y;
+          __builtin_memcpy(&y, swd::at_bytes(sample, 2u * w), sizeof y);
+          x[0] = swd::tof((uint16_t)(y.x & 0xFFFFu));
+          x[1] = swd::tof((uint16_t)(y.x >> 16));
+          x[2] = swd::tof((uint16_t)(y.y & 0xFFFFu));
+          x[3] = swd::tof((uint16_t)(y.y >> 16));
+        }
+        mv[R][0] = d == 0 ? x[0] : d == 1 ? x[1] : d == 2 ? x[2] : x[3];
+        mv[R][1] = d == 0 ? x[1] : d == 1 ? x[2] : x[3];
+        mv[R][2] = d == 0 ? x[2] : x[3];
+        mv[R][3] = x[3];
       }
+    } else {
+#pragma unroll
+      for (int R = 0; R < 4; ++R)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int t = t0 + 4 * g + v;
+          const int32_t p = lenR[R] > 0
+                                ? rbR[R] + (t < lenR[R] ? t : lenR[R] - 1)
+                                : bl;
+          mv[R][v] = SAMPLES ? swd::tof(*swd::at_bytes(
+                                   sample, (uint32_t)(sizeof(T) * p)))
+                             : 0.0f;
+        }
+    }
   };
   // a chunk's products and its entries' stores (one 16-byte store when the
   // lane's four entries are all in its row)
