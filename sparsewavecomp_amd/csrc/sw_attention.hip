@@ -65,19 +65,6 @@ __device__ __forceinline__ float as_stored(float v) {
     return bf16_to_f32(f32_to_bf16(v));
 }
 
-// exp(x) in the fused chains, as the hardware base-2 exponential of
-// x log2 e (v_exp_f32): rounding the product adds at most
-// 2^-24 |x log2 e| ln 2 relative error (1.2e-6 at x = -20, beside
-// v_exp_f32's own ulp), about 2 instructions instead of the library expf's
-// 10.  A softmax's arguments are x = s - max <= 0, so nothing overflows;
-// -inf gives 0 and NaN stays NaN, as with expf.  Unlike expf, v_exp_f32
-// flushes a result below 2^-126 to zero: for x < -87.3 the exponential is 0
-// where expf gives a subnormal, an absolute error below 2^-126 in each
-// probability (the row sum is at least 1).
-__device__ __forceinline__ float exp_by_exp2(float x) {
-  return __builtin_amdgcn_exp2f(x * 1.44269504088896341f);
-}
-
 __device__ __forceinline__ float map_value(int kind, float v, float rv) {
   switch (kind) {
   case SW_MAP_EXP_SUB:

@@ -155,6 +155,21 @@ __device__ __forceinline__ uint64_t ballot(bool p) {
   return __builtin_amdgcn_ballot_w64(p);
 }
 
+// ---- softmax arithmetic -----------------------------------------------------
+// exp(x) as the hardware base-2 exponential of x log2 e (v_exp_f32), used by
+// the fused attention kernels and the lrrt bundle's exponentials: rounding
+// the product adds at most 2^-24 |x log2 e| ln 2 relative error (1.2e-6 at
+// x = -20, beside v_exp_f32's own ulp), 2 vector instructions instead of
+// the library expf's 13 (range reduction, ldexp and range checks).  A
+// softmax's arguments are x = s - max <= 0, so nothing overflows; -inf gives
+// 0 and NaN stays NaN, as with expf.  Unlike expf, v_exp_f32 flushes a
+// result below 2^-126 to zero: for x < -87.3 the exponential is 0 where expf
+// gives a subnormal, an absolute error below 2^-126 in each probability (the
+// row sum is at least 1).
+__device__ __forceinline__ float exp_by_exp2(float x) {
+  return __builtin_amdgcn_exp2f(x * 1.44269504088896341f);
+}
+
 // ---- loads ---------------------------------------------------------------
 // Operands streamed once per launch (CSR columns and values, BSR blocks).
 // A plain load: with the non-temporal hint the CSR SpMV/SpMM and BSR kernels
