@@ -53,7 +53,10 @@ def _attention_case(case):
     matrix-core tiles (prefix tiles) or row by row (the ragged masks);
     "inf_dv64" puts an inf in a V row that only the last row of a 16-row
     tile reads, so that the tile's other rows meet 0 * inf and the tile is
-    recomputed row by row."""
+    recomputed row by row.  "wide" spreads the scores over 100 below their
+    row maxima, so that the exponential kernel's v_exp_f32 runs over a wide
+    range of arguments and flushes the results below 2^-126 that expf
+    gives as subnormals (the checker's absolute 2^-126 per probability)."""
     if case.endswith("_dv64") or case.endswith("_dv128"):
         base, wide = case.rsplit("_dv", 1)
         mask, q, kt, v, alpha = _attention_case(base)
@@ -65,6 +68,10 @@ def _attention_case(case):
     if case == "inf":
         mask, q, kt, v, alpha = W.config5(seed=1, seq=256, d=64)
         return mask, q, kt, v, alpha
+    if case == "wide":
+        # scores spread over 100 below their row maxima (alpha = 1.6)
+        mask, q, kt, v, _ = W.config5(seed=0, seq=1024)
+        return mask, q, kt, v, 1.6
     if case in ("config5", "d128", "d32"):
         d = {"config5": 64, "d128": 128, "d32": 32}[case]
         mask, q, kt, v, alpha = W.config5(seed=0, seq=512, d=d)
@@ -91,12 +98,12 @@ def _attention_case(case):
                                   "ragged2", "d128", "d32", "config5_dv64",
                                   "partial_dv64", "block32_dv128",
                                   "ragged0_dv64", "ragged2_dv64", "d128_dv64",
-                                  "inf_dv64"])
+                                  "inf_dv64", "wide"])
 def test_attention_bundle_matches_oracle(dev, orc, tmp_path, case):
     mask, q, kt, v, alpha = _attention_case(case)
     rows, d, dv = mask.rows, q.shape[1], v.shape[1]
     beta = 0.0 if case.split("_dv")[0] in ("config5", "d128", "d32",
-                                           "inf") else 0.5
+                                           "inf", "wide") else 0.5
     B.build_attention_bundle(tmp_path / "b", rows=rows, key_rows=mask.cols,
                              head_dim=d, value_cols=dv, alpha=alpha,
                              beta=beta)
@@ -132,6 +139,9 @@ def test_attention_bundle_matches_oracle(dev, orc, tmp_path, case):
         assert np.array_equal(cls(out), cls(ref)), cls.__name__
     if case == "inf_dv64":
         assert np.isposinf(ref).any() and np.isfinite(ref[16:31]).all()
+    if case == "wide":
+        p_ref = np.asarray(refs[0])
+        assert float(np.log(p_ref[p_ref > 0]).min()) < -95.0
 
 
 def test_config3_bundle_at_full_size(dev, orc):
