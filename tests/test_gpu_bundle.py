@@ -53,7 +53,8 @@ def _attention_case(case):
     matrix-core tiles (prefix tiles) or row by row (the ragged masks);
     "inf_dv64" puts an inf in a V row that only the last row of a 16-row
     tile reads, so that the tile's other rows meet 0 * inf and the tile is
-    recomputed row by row.  "wide" spreads the scores over 100 below their
+    recomputed row by row.  "masked" sets a fifth of the mask values, and
+    one row's whole, to -inf.  "wide" spreads the scores over 100 below their
     row maxima, so that the exponential kernel's v_exp_f32 runs over a wide
     range of arguments and flushes the results below 2^-126 that expf
     gives as subnormals (the checker's absolute 2^-126 per probability)."""
@@ -72,6 +73,19 @@ def _attention_case(case):
         # scores spread over 100 below their row maxima (alpha = 1.6)
         mask, q, kt, v, _ = W.config5(seed=0, seq=1024)
         return mask, q, kt, v, 1.6
+    if case == "masked":
+        # a fifth of the mask values -inf (entries masked out) and one row
+        # masked whole: probability 0, and -inf maximum with NaN sum,
+        # probabilities and output for the dead row
+        mask, q, kt, v, _ = W.config5(seed=2, seq=512)
+        rng = np.random.default_rng(78)
+        vals = rng.uniform(-1, 1, mask.nnz).astype(np.float32)
+        vals[rng.random(mask.nnz) < 0.2] = -np.inf
+        dead = int(np.flatnonzero(np.diff(mask.row_offsets) > 20)[3])
+        vals[mask.row_offsets[dead]:mask.row_offsets[dead + 1]] = -np.inf
+        mask = W.CSR(mask.rows, mask.cols, mask.row_offsets,
+                     mask.column_indices, vals)
+        return mask, q, kt, v, 0.125
     if case in ("config5", "d128", "d32"):
         d = {"config5": 64, "d128": 128, "d32": 32}[case]
         mask, q, kt, v, alpha = W.config5(seed=0, seq=512, d=d)
@@ -98,7 +112,7 @@ def _attention_case(case):
                                   "ragged2", "d128", "d32", "config5_dv64",
                                   "partial_dv64", "block32_dv128",
                                   "ragged0_dv64", "ragged2_dv64", "d128_dv64",
-                                  "inf_dv64", "wide"])
+                                  "inf_dv64", "wide", "masked"])
 def test_attention_bundle_matches_oracle(dev, orc, tmp_path, case):
     mask, q, kt, v, alpha = _attention_case(case)
     rows, d, dv = mask.rows, q.shape[1], v.shape[1]
@@ -139,6 +153,12 @@ def test_attention_bundle_matches_oracle(dev, orc, tmp_path, case):
         assert np.array_equal(cls(out), cls(ref)), cls.__name__
     if case == "inf_dv64":
         assert np.isposinf(ref).any() and np.isfinite(ref[16:31]).all()
+    if case == "masked":
+        m_ref, sum_ref = np.asarray(refs[1]), np.asarray(refs[2])
+        dead = np.flatnonzero(np.isneginf(m_ref))
+        assert dead.size >= 1 and np.isnan(sum_ref[dead]).all()
+        assert np.isnan(bufs["rowSum"].cpu().numpy()[dead]).all()
+        assert np.isnan(out[dead]).all()
     if case == "wide":
         p_ref = np.asarray(refs[0])
         assert float(np.log(p_ref[p_ref > 0]).min()) < -95.0
