@@ -8,6 +8,8 @@ on it (the option lists of tests/test_gpu_spmv.py and test_gpu_spmm.py), and
 every output must meet the fp32 bound |y - y_ref| <= 1e-5 sum |a x|; SpMM
 runs K of 1, 3, 4, 17 and 64.  The same matrices as COO (row-sorted and
 shuffled, with repeated coordinates) check the COO kernels."""
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -21,7 +23,8 @@ from tests.test_gpu_spmv import MAPPINGS as SPMV_MAPPINGS
 
 pytestmark = pytest.mark.gpu
 
-SEEDS = list(range(6))
+# SW_FUZZ_SEEDS=N runs seeds 0 .. N-1 instead (a longer one-off run)
+SEEDS = list(range(int(os.environ.get("SW_FUZZ_SEEDS", "6"))))
 
 
 def _matrix(seed):

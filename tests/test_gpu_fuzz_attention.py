@@ -21,6 +21,8 @@ through the fp32 and bf16 BSR kernels.
 Bars: the fp32 op bars (1e-5 sum |terms|), the attention bounds derived from
 them (tests/_attention_check.py), and for bf16 the fp32 bar plus one
 rounding, and rel-L2 <= 1e-2."""
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -39,7 +41,8 @@ from tests.test_gpu_bsr_attention import (ATT_OPTS, BSR_OPTS, ROW_OPTS,
 
 pytestmark = pytest.mark.gpu
 
-SEEDS = list(range(5))
+# SW_FUZZ_SEEDS=N runs seeds 0 .. N-1 instead (a longer one-off run)
+SEEDS = list(range(int(os.environ.get("SW_FUZZ_SEEDS", "5"))))
 
 
 def _mask(seed):
@@ -234,3 +237,46 @@ def test_fuzz_bsr(dev, orc, seed):
                                     what=f"seed {seed} {opts}")
             if np.any(ref):
                 assert rel_l2(got, ref) <= BF16_REL_L2
+
+
+@pytest.mark.parametrize("seed", SEEDS)
+def test_fuzz_attention_bundle(dev, orc, tmp_path, seed):
+    """The lrrt attention bundle built for each fuzz mask's shapes (its
+    kernels specialise rows, key rows, d and dv), its six kernels launched in
+    order as a runtime does, against the oracle with the chain's derived
+    bounds.  The masks' 16-row tiles give the output kernel prefix tiles,
+    fallback tiles and empty tiles; the scores kernel's 64-row tiles mostly
+    take its rows' own path, and d of 64 and 128 its matrix-core tiles."""
+    from sparsewavecomp_amd import bundle as B
+    from sparsewavecomp_amd.bundle.runtime import Bundle
+    csr, rng = _mask(seed)
+    d, dv = _widths(seed)
+    q, kt, v, alpha, beta = _inputs(csr, rng, d, dv)
+    B.build_attention_bundle(tmp_path / "b", rows=csr.rows, key_rows=csr.cols,
+                             head_dim=d, value_cols=dv, alpha=alpha,
+                             beta=beta)
+    bun = Bundle(tmp_path / "b")
+    nan = float("nan")
+    bufs = {"rowOffsets": G.t(csr.row_offsets),
+            "columnIndices": G.t(csr.column_indices),
+            "maskValues": G.t(csr.values), "query": G.t(q),
+            "transposedKey": G.t(kt), "value": G.t(v),
+            "scores": torch.full((max(csr.nnz, 1),), nan, device=G.DEV),
+            "rowMaximum": torch.full((csr.rows,), nan, device=G.DEV),
+            "rowSum": torch.full((csr.rows,), nan, device=G.DEV),
+            "output": torch.full((csr.rows, dv), nan, device=G.DEV)}
+    ptrs = {k: t.data_ptr() for k, t in bufs.items()}
+    G.say(f"fuzz attention bundle seed {seed} rows={csr.rows} "
+          f"nnz={csr.nnz} d={d} dv={dv}")
+    for name in B.ATTENTION_ORDER:
+        bun.launch(name, csr.rows * dv if name == "sparse_attention_output"
+                   else csr.rows, ptrs)
+    torch.cuda.synchronize()
+    bun.close()
+    refs = orc.sparse_attention(csr.row_offsets, csr.column_indices,
+                                csr.values, q, kt, v, alpha, beta)
+    check_attention_f32(orc, csr, csr.values, q, kt, v, alpha, beta,
+                        bufs["scores"].cpu().numpy()[:csr.nnz],
+                        bufs["rowMaximum"].cpu().numpy(),
+                        bufs["rowSum"].cpu().numpy(),
+                        bufs["output"].cpu().numpy(), refs)
