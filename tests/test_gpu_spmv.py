@@ -58,9 +58,10 @@ def _check(orc, csr, x, y):
     assert_within_bound(y, ref, bound)
 
 
+@pytest.mark.parametrize("case", ["spmv", "spmv_sparse_tensor"])
 @pytest.mark.parametrize("opts", MAPPINGS)
-def test_golden(dev, golden, opts):
-    g = golden["spmv"]
+def test_golden(dev, golden, opts, case):
+    g = golden[case]
     csr = W.CSR(g["rows"], g["cols"], np.array(g["row_offsets"], np.int32),
                 np.array(g["column_indices"], np.int32),
                 np.array(g["values"], np.float32))

@@ -31,8 +31,9 @@ def _scipy(csr):
 # ---- golden vectors ------------------------------------------------------
 
 
-def test_golden_spmv(orc, golden):
-    g = golden["spmv"]
+@pytest.mark.parametrize("case", ["spmv", "spmv_sparse_tensor"])
+def test_golden_spmv(orc, golden, case):
+    g = golden[case]
     ro, col, val = _csr(g)
     y = orc.spmv(ro, col, val, np.array(g["vector"], np.float32))
     np.testing.assert_array_equal(y, np.array(g["expected"], np.float32))
