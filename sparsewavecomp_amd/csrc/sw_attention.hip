@@ -92,7 +92,7 @@ __global__ __launch_bounds__(LB) void sddmm_thread_per_row(
     int64_t cols, int32_t kdim, int kind, float alpha, float beta) {
   if constexpr (TKB > 0) {
     __shared__ int32_t lcol[LB / kWave][sw_tile64::kTileCols];
-    const int64_t r0 = (int64_t)blockIdx.x * blockDim.x +
+    const int64_t r0 = block_id() * blockDim.x +
                        (int64_t)wave_in_group() * kWave;
     if (r0 >= rows)
       return; // wave-uniform
@@ -107,7 +107,7 @@ __global__ __launch_bounds__(LB) void sddmm_thread_per_row(
                              lcol[wave_in_group()], combine))
       return;
   }
-  int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int64_t r = block_id() * blockDim.x + threadIdx.x;
   if (r >= rows)
     return;
   const T *a = lhs + r * kdim;
@@ -234,7 +234,7 @@ __global__ __launch_bounds__(256) void sddmm_wave_per_row(
     const T *__restrict__ val, const T *__restrict__ lhs,
     const T *__restrict__ rhs, T *__restrict__ out, int32_t rows,
     int64_t cols, int32_t kdim, int kind, float alpha, float beta) {
-  const int64_t r = (int64_t)blockIdx.x * (blockDim.x / kWave) +
+  const int64_t r = block_id() * (blockDim.x / kWave) +
                     wave_in_group();
   if (r >= rows)
     return; // wave-uniform
@@ -263,7 +263,9 @@ __global__ __launch_bounds__(64 * W) void sddmm_tile_mfma(
     const float *__restrict__ val, const float *__restrict__ lhs,
     const float *__restrict__ rhs, float *__restrict__ out, int32_t rows,
     int64_t cols, int32_t kdim, int kind, float alpha, float beta) {
-  const int r0 = blockIdx.x * 16;
+  if (block_id() * 16 >= rows)
+    return; // a folded grid's surplus workgroup (workgroup-uniform)
+  const int r0 = (int)block_id() * 16;
   const int nt = std::min(16, rows - r0);
   const int wave = wave_in_group();
   const int l = lane_id(), i = l & 15, g = l >> 4;
@@ -353,7 +355,7 @@ template <bool MAX, typename T>
 __global__ __launch_bounds__(1024) void row_reduce_thread(
     const int32_t *__restrict__ ro, const T *__restrict__ val,
     T *__restrict__ out, int32_t rows) {
-  int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int64_t r = block_id() * blockDim.x + threadIdx.x;
   if (r >= rows)
     return;
   float acc = MAX ? -INFINITY : 0.0f;
@@ -400,7 +402,7 @@ template <bool MAX, typename T>
 __global__ __launch_bounds__(256) void row_reduce_wave(
     const int32_t *__restrict__ ro, const T *__restrict__ val,
     T *__restrict__ out, int32_t rows) {
-  const int64_t r = (int64_t)blockIdx.x * (blockDim.x / kWave) +
+  const int64_t r = block_id() * (blockDim.x / kWave) +
                     wave_in_group();
   if (r >= rows)
     return;
@@ -421,7 +423,7 @@ __global__ __launch_bounds__(1024) void rowwise_map_thread(
     const int32_t *__restrict__ ro, const T *val,
     const T *__restrict__ rowv, T *out, int32_t rows) {
   constexpr int kind = KIND;
-  int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int64_t r = block_id() * blockDim.x + threadIdx.x;
   if (r >= rows)
     return;
   const float rv = ldv(rowv + r);
@@ -472,7 +474,7 @@ template <typename T>
 __global__ __launch_bounds__(256) void rowwise_map_wave(
     const int32_t *__restrict__ ro, const T *val,
     const T *__restrict__ rowv, T *out, int32_t rows, int kind) {
-  const int64_t r = (int64_t)blockIdx.x * (blockDim.x / kWave) +
+  const int64_t r = block_id() * (blockDim.x / kWave) +
                     wave_in_group();
   if (r >= rows)
     return;
@@ -493,7 +495,7 @@ template <typename T>
 __global__ __launch_bounds__(256) void row_softmax_wave(
     const int32_t *__restrict__ ro, T *scores, T *__restrict__ rmax,
     T *__restrict__ rsum, int32_t rows) {
-  const int64_t r = (int64_t)blockIdx.x * (blockDim.x / kWave) +
+  const int64_t r = block_id() * (blockDim.x / kWave) +
                     wave_in_group();
   if (r >= rows)
     return;
@@ -664,7 +666,9 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused(
   __shared__ int32_t lcol[kFusedCols];   // the last row's columns
   __shared__ int wshared[W]; // each wave's rows share the last row's columns
   __shared__ int v_nonfinite; // an output of the tile is inf or NaN
-  const int r0 = blockIdx.x * 16;
+  if (block_id() * 16 >= rows)
+    return; // a folded grid's surplus workgroup (workgroup-uniform)
+  const int r0 = (int)block_id() * 16;
   const int nt = std::min(16, rows - r0);
   const int wave = wave_in_group();
   const int l = lane_id(), i = l & 15, g = l >> 4;
@@ -1176,7 +1180,9 @@ __global__ __launch_bounds__(64 * W) void sddmm_tile_mfma_bf16(
     int32_t rows, int64_t cols, int32_t kdim, int kind, float alpha,
     float beta) {
   constexpr int S = 2 * KB; // 32-deep K steps
-  const int r0 = blockIdx.x * 16;
+  if (block_id() * 16 >= rows)
+    return; // a folded grid's surplus workgroup (workgroup-uniform)
+  const int r0 = (int)block_id() * 16;
   const int nt = std::min(16, rows - r0);
   const int wave = wave_in_group();
   const int l = lane_id(), i = l & 15, g = l >> 4;
@@ -1300,7 +1306,9 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused_bf16(
   __shared__ float wred[2][W][16];       // [max, sum][wave][row]
   __shared__ int wshared[W]; // each wave's rows share the last row's columns
   __shared__ int v_nonfinite;
-  const int r0 = blockIdx.x * 16;
+  if (block_id() * 16 >= rows)
+    return; // a folded grid's surplus workgroup (workgroup-uniform)
+  const int r0 = (int)block_id() * 16;
   const int nt = std::min(16, rows - r0);
   const int wave = wave_in_group();
   const int l = lane_id(), i = l & 15, g = l >> 4;
@@ -1715,7 +1723,8 @@ __global__ __launch_bounds__(64 * W, 4) void attention_tile_fused_bf16(
 int grid_for(int64_t work, int64_t per_block, const char *what,
              int64_t *grid) {
   *grid = std::max<int64_t>(sw::ceil_div(work, per_block), 1);
-  return sw::check_grid(*grid, what);
+  // (every kernel launched with it has at most 1024 work-items a workgroup)
+  return sw::check_grid(*grid, 1024, what);
 }
 
 } // namespace
@@ -1744,7 +1753,7 @@ int launch_sddmm(const int32_t *ro, const int32_t *col, const T *val,
           (val == nullptr || out + nnz <= val || val + nnz <= out)) {
 #define SW_SDDMM_FUSED(KB, NS)                                                \
   hipLaunchKernelGGL((attention_tile_fused<KB, kFusedWaves, false, true, NS>),\
-                     dim3((unsigned)grid), dim3(64 * kFusedWaves), 0, st, ro, \
+                     sw::grid_dim(grid, 64 * kFusedWaves), dim3(64 * kFusedWaves), 0, st, ro, \
                      col, val, lhs, rhs, nullptr, out, nullptr, nullptr,      \
                      nullptr, (int32_t)rows, cols, (int32_t)kdim, (int64_t)0, \
                      alpha, beta, (uint32_t)(nnz - 4), kind)
@@ -1761,7 +1770,7 @@ int launch_sddmm(const int32_t *ro, const int32_t *col, const T *val,
       }
 #define SW_SDDMM_TILE(KB)                                                     \
   hipLaunchKernelGGL((sddmm_tile_mfma<KB, kSddmmTileWaves>),                  \
-                     dim3((unsigned)grid), dim3(64 * kSddmmTileWaves), 0, st, \
+                     sw::grid_dim(grid, 64 * kSddmmTileWaves), dim3(64 * kSddmmTileWaves), 0, st, \
                      ro, col, val, lhs, rhs, out, (int32_t)rows, cols,        \
                      (int32_t)kdim, kind, alpha, beta)
       if (kb == 1)
@@ -1785,7 +1794,7 @@ int launch_sddmm(const int32_t *ro, const int32_t *col, const T *val,
           (val == nullptr || out + nnz <= val || val + nnz <= out)) {
 #define SW_SDDMM_FUSED(KB, NS)                                                \
   hipLaunchKernelGGL((attention_tile_fused_bf16<KB, kFusedWaves, true, NS>),  \
-                     dim3((unsigned)grid), dim3(64 * kFusedWaves), 0, st, ro, \
+                     sw::grid_dim(grid, 64 * kFusedWaves), dim3(64 * kFusedWaves), 0, st, ro, \
                      col, val, lhs, rhs, nullptr, out, nullptr, nullptr,      \
                      nullptr, (int32_t)rows, cols, (int32_t)kdim, (int64_t)0, \
                      alpha, beta, (uint32_t)(nnz - 4), kind)
@@ -1802,7 +1811,7 @@ int launch_sddmm(const int32_t *ro, const int32_t *col, const T *val,
       }
 #define SW_SDDMM_TILE(KB)                                                     \
   hipLaunchKernelGGL((sddmm_tile_mfma_bf16<KB, kSddmmTileWaves>),             \
-                     dim3((unsigned)grid), dim3(64 * kSddmmTileWaves), 0, st, \
+                     sw::grid_dim(grid, 64 * kSddmmTileWaves), dim3(64 * kSddmmTileWaves), 0, st, \
                      ro, col, val, lhs, rhs, out, (int32_t)rows, cols,        \
                      (int32_t)kdim, kind, alpha, beta)
       if (kb == 1)
@@ -1821,7 +1830,7 @@ int launch_sddmm(const int32_t *ro, const int32_t *col, const T *val,
     int rc = grid_for(rows, 4, "SDDMM", &grid);
     if (rc)
       return rc;
-    hipLaunchKernelGGL(sddmm_wave_per_row<T>, dim3((unsigned)grid), dim3(256),
+    hipLaunchKernelGGL(sddmm_wave_per_row<T>, sw::grid_dim(grid, 256), dim3(256),
                        0, st, ro, col, val, lhs, rhs, out, (int32_t)rows, cols,
                        (int32_t)kdim, kind, alpha, beta);
   } else {
@@ -1841,22 +1850,22 @@ int launch_sddmm(const int32_t *ro, const int32_t *col, const T *val,
                        (int64_t)sizeof(T) * kdim * cols <= (int64_t)UINT32_MAX;
     if (tiles && kdim == 64)
       hipLaunchKernelGGL((sddmm_thread_per_row<T, 16, 256, 1>),
-                         dim3((unsigned)grid), dim3((unsigned)B), 0, st, ro,
+                         sw::grid_dim(grid, (unsigned)B), dim3((unsigned)B), 0, st, ro,
                          col, val, lhs, rhs, out, (int32_t)rows, cols,
                          (int32_t)kdim, kind, alpha, beta);
     else if (tiles)
       hipLaunchKernelGGL((sddmm_thread_per_row<T, 16, 256, 2>),
-                         dim3((unsigned)grid), dim3((unsigned)B), 0, st, ro,
+                         sw::grid_dim(grid, (unsigned)B), dim3((unsigned)B), 0, st, ro,
                          col, val, lhs, rhs, out, (int32_t)rows, cols,
                          (int32_t)kdim, kind, alpha, beta);
     else if (B <= 512)
       hipLaunchKernelGGL((sddmm_thread_per_row<T, 16, 512>),
-                         dim3((unsigned)grid), dim3((unsigned)B), 0, st, ro,
+                         sw::grid_dim(grid, (unsigned)B), dim3((unsigned)B), 0, st, ro,
                          col, val, lhs, rhs, out, (int32_t)rows, cols,
                          (int32_t)kdim, kind, alpha, beta);
     else
       hipLaunchKernelGGL((sddmm_thread_per_row<T, 4, 1024>),
-                         dim3((unsigned)grid), dim3((unsigned)B), 0, st, ro,
+                         sw::grid_dim(grid, (unsigned)B), dim3((unsigned)B), 0, st, ro,
                          col, val, lhs, rhs, out, (int32_t)rows, cols,
                          (int32_t)kdim, kind, alpha, beta);
   }
@@ -1872,10 +1881,10 @@ int launch_row_reduce(const int32_t *ro, const T *val, T *out, int64_t rows,
     if (rc)
       return rc;
     if (is_max)
-      hipLaunchKernelGGL((row_reduce_wave<true, T>), dim3((unsigned)grid),
+      hipLaunchKernelGGL((row_reduce_wave<true, T>), sw::grid_dim(grid, 256),
                          dim3(256), 0, st, ro, val, out, (int32_t)rows);
     else
-      hipLaunchKernelGGL((row_reduce_wave<false, T>), dim3((unsigned)grid),
+      hipLaunchKernelGGL((row_reduce_wave<false, T>), sw::grid_dim(grid, 256),
                          dim3(256), 0, st, ro, val, out, (int32_t)rows);
   } else {
     const int64_t B = o.row_reduction_block_size;
@@ -1883,10 +1892,10 @@ int launch_row_reduce(const int32_t *ro, const T *val, T *out, int64_t rows,
     if (rc)
       return rc;
     if (is_max)
-      hipLaunchKernelGGL((row_reduce_thread<true, T>), dim3((unsigned)grid),
+      hipLaunchKernelGGL((row_reduce_thread<true, T>), sw::grid_dim(grid, (unsigned)B),
                          dim3((unsigned)B), 0, st, ro, val, out, (int32_t)rows);
     else
-      hipLaunchKernelGGL((row_reduce_thread<false, T>), dim3((unsigned)grid),
+      hipLaunchKernelGGL((row_reduce_thread<false, T>), sw::grid_dim(grid, (unsigned)B),
                          dim3((unsigned)B), 0, st, ro, val, out, (int32_t)rows);
   }
   return launch_check("CSR row reduction kernel");
@@ -1901,7 +1910,7 @@ int launch_rowwise_map(const int32_t *ro, const T *val, const T *rowv, T *out,
     int rc = grid_for(rows, 4, "CSR row-wise map", &grid);
     if (rc)
       return rc;
-    hipLaunchKernelGGL(rowwise_map_wave<T>, dim3((unsigned)grid), dim3(256), 0,
+    hipLaunchKernelGGL(rowwise_map_wave<T>, sw::grid_dim(grid, 256), dim3(256), 0,
                        st, ro, val, rowv, out, (int32_t)rows, kind);
   } else {
     const int64_t B = o.rowwise_map_block_size;
@@ -1909,7 +1918,7 @@ int launch_rowwise_map(const int32_t *ro, const T *val, const T *rowv, T *out,
     if (rc)
       return rc;
 #define SW_MAP_THREAD(KIND)                                                   \
-  hipLaunchKernelGGL((rowwise_map_thread<T, KIND>), dim3((unsigned)grid),     \
+  hipLaunchKernelGGL((rowwise_map_thread<T, KIND>), sw::grid_dim(grid, B),   \
                      dim3((unsigned)B), 0, st, ro, val, rowv, out,            \
                      (int32_t)rows)
     switch (kind) {
@@ -2042,7 +2051,7 @@ bool launch_fused_attention(const int32_t *ro, const int32_t *col,
   const bool il = dv % 64 == 0 && aligned16(v) && aligned16(out);
 #define SW_FUSED(KB, IL)                                                      \
   hipLaunchKernelGGL((attention_tile_fused<KB, kFusedWaves, IL, false>),      \
-                     dim3((unsigned)grid), dim3(64 * kFusedWaves), 0, st, ro, \
+                     sw::grid_dim(grid, 64 * kFusedWaves), dim3(64 * kFusedWaves), 0, st, ro, \
                      col, mask, q, kt, v, scores, rmax, rsum, out,            \
                      (int32_t)rows, cols, (int32_t)d, dv, alpha, beta,        \
                      (uint32_t)(nnz - 4), (int)SW_SDDMM_AFFINE)
@@ -2079,7 +2088,7 @@ bool launch_fused_attention(const int32_t *ro, const int32_t *col,
     return true;
 #define SW_FUSED(KB)                                                          \
   hipLaunchKernelGGL((attention_tile_fused_bf16<KB, kFusedWaves, false>),     \
-                     dim3((unsigned)grid), dim3(64 * kFusedWaves), 0, st, ro, \
+                     sw::grid_dim(grid, 64 * kFusedWaves), dim3(64 * kFusedWaves), 0, st, ro, \
                      col, mask, q, kt, v, scores, rmax, rsum, out,            \
                      (int32_t)rows, cols, (int32_t)d, dv, alpha, beta,        \
                      (uint32_t)(nnz - 4), (int)SW_SDDMM_AFFINE)
@@ -2113,7 +2122,7 @@ bool launch_attention_floor(const int32_t *ro, const int32_t *col,
 #define SW_FLOOR(KB, IL)                                                      \
   hipLaunchKernelGGL(                                                         \
       (attention_tile_fused<KB, kFusedWaves, IL, false, false, true>),        \
-      dim3((unsigned)grid), dim3(64 * kFusedWaves), 0, st, ro, col, mask, q,  \
+      sw::grid_dim(grid, 64 * kFusedWaves), dim3(64 * kFusedWaves), 0, st, ro, col, mask, q,  \
       kt, v, scores, rmax, rsum, out, (int32_t)rows, cols, (int32_t)d, dv,    \
       1.0f, 0.0f, (uint32_t)(nnz - 4), (int)SW_SDDMM_AFFINE)
   if (d == 64 && il)
@@ -2150,7 +2159,7 @@ bool launch_attention_floor(const int32_t *ro, const int32_t *col,
 #define SW_FLOOR(KB)                                                          \
   hipLaunchKernelGGL(                                                         \
       (attention_tile_fused_bf16<KB, kFusedWaves, false, false, true>),       \
-      dim3((unsigned)grid), dim3(64 * kFusedWaves), 0, st, ro, col, mask, q,  \
+      sw::grid_dim(grid, 64 * kFusedWaves), dim3(64 * kFusedWaves), 0, st, ro, col, mask, q,  \
       kt, v, scores, rmax, rsum, out, (int32_t)rows, cols, (int32_t)d, dv,    \
       1.0f, 0.0f, (uint32_t)(nnz - 4), (int)SW_SDDMM_AFFINE)
   if (d == 64)
@@ -2247,10 +2256,10 @@ int attention_entry(const int32_t *row_offsets, const int32_t *column_indices,
   if (o.sddmm_lanes_per_row == 64) {
     // wave row ops: the four softmax ops run as one kernel
     int64_t grid = std::max<int64_t>(ceil_div(rows, 4), 1);
-    rc = check_grid(grid, "attention softmax");
+    rc = check_grid(grid, 256, "attention softmax");
     if (rc)
       return rc;
-    hipLaunchKernelGGL(row_softmax_wave<T>, dim3((unsigned)grid), dim3(256), 0,
+    hipLaunchKernelGGL(row_softmax_wave<T>, sw::grid_dim(grid, 256), dim3(256), 0,
                        st, row_offsets, scores, row_maximum, row_sum,
                        (int32_t)rows);
     rc = launch_check("attention softmax kernel");

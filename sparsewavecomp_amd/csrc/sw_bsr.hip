@@ -38,7 +38,7 @@ __global__ __launch_bounds__(1024) void bsr_thread_per_output(
     const T *__restrict__ bval, const T *__restrict__ rhs,
     TO *__restrict__ out, int64_t rows, int64_t k, int32_t b_any) {
   const int32_t b = BS > 0 ? BS : b_any;
-  int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int64_t e = block_id() * blockDim.x + threadIdx.x;
   if (e >= rows * k)
     return;
   int64_t r = e / k, c = e - r * k;
@@ -542,6 +542,10 @@ int launch_bsr(const int32_t *bro, const int32_t *bcol, const T *bval,
       const int64_t gy = sw::ceil_div(k, 64 * strips);
       if (gy > 65535)
         return sw::fail(SW_ERR_INVALID_SHAPE, "rhs has too many columns");
+      const int rc = sw::check_flat_grid(nbr, 64 * strips * kF32Split,
+                                         "BSR MFMA kernel");
+      if (rc)
+        return rc;
       hipLaunchKernelGGL((bsr16_mfma_f32_x4<kF32Batch, kF32Split>),
                          dim3((unsigned)nbr, (unsigned)gy),
                          dim3((unsigned)(64 * strips * kF32Split)), 0, st, bro,
@@ -557,6 +561,10 @@ int launch_bsr(const int32_t *bro, const int32_t *bcol, const T *bval,
         const int64_t gy = sw::ceil_div(k, 128);
         if (gy > 65535)
           return sw::fail(SW_ERR_INVALID_SHAPE, "rhs has too many columns");
+        const int rc =
+            sw::check_flat_grid(nbr, 64 * kBf16Split, "BSR MFMA kernel");
+        if (rc)
+          return rc;
         hipLaunchKernelGGL((bsr16_mfma_bf16_x8<kBf16Batch, kBf16Split, TO>),
                            dim3((unsigned)nbr, (unsigned)gy),
                            dim3(64 * kBf16Split), 0, st, bro, bcol, bval,
@@ -569,6 +577,9 @@ int launch_bsr(const int32_t *bro, const int32_t *bcol, const T *bval,
     int64_t gy = sw::ceil_div(k, 128);
     if (gy > 65535)
       return sw::fail(SW_ERR_INVALID_SHAPE, "rhs has too many columns");
+    const int rc = sw::check_flat_grid(nbr, 256, "BSR MFMA kernel");
+    if (rc)
+      return rc;
     dim3 grid((unsigned)nbr, (unsigned)gy);
     if constexpr (sizeof(T) == 4)
       hipLaunchKernelGGL(bsr16_mfma_f32<8>, grid, dim3(256), 0, st, bro, bcol,
@@ -580,13 +591,13 @@ int launch_bsr(const int32_t *bro, const int32_t *bcol, const T *bval,
   }
   const int64_t B = o.spmm_block_size;
   int64_t grid = std::max<int64_t>(sw::ceil_div(rows * k, B), 1);
-  int rc = sw::check_grid(grid, "BSR SpMM");
+  int rc = sw::check_grid(grid, B, "BSR SpMM");
   if (rc)
     return rc;
   const bool row = k % 64 == 0 && B % 64 == 0 && rows <= INT32_MAX;
 #define SW_BSR_TPO(BS, ROW)                                                   \
   hipLaunchKernelGGL((bsr_thread_per_output<T, TO, BS, ROW>),                 \
-                     dim3((unsigned)grid), dim3((unsigned)B), 0, st, bro,     \
+                     sw::grid_dim(grid, B), dim3((unsigned)B), 0, st, bro,   \
                      bcol, bval, rhs, out, rows, k, (int32_t)b)
   if (b == 16 && row)
     SW_BSR_TPO(16, true);
@@ -644,6 +655,10 @@ int launch_slab_floor(const int32_t *bro, const int32_t *bcol, const T *bval,
     const int64_t gy = sw::ceil_div(k, 64 * strips);
     if (gy > 65535)
       return sw::fail(SW_ERR_INVALID_SHAPE, "rhs has too many columns");
+    const int rc = sw::check_flat_grid(nbr, 64 * strips * kF32Split,
+                                       "BSR slab floor kernel");
+    if (rc)
+      return rc;
     hipLaunchKernelGGL((bsr16_mfma_f32_x4<kF32Batch, kF32Split, true>),
                        dim3((unsigned)nbr, (unsigned)gy),
                        dim3((unsigned)(64 * strips * kF32Split)), 0, st, bro,
@@ -652,6 +667,10 @@ int launch_slab_floor(const int32_t *bro, const int32_t *bcol, const T *bval,
     const int64_t gy = sw::ceil_div(k, 128);
     if (gy > 65535)
       return sw::fail(SW_ERR_INVALID_SHAPE, "rhs has too many columns");
+    const int rc =
+        sw::check_flat_grid(nbr, 64 * kBf16Split, "BSR slab floor kernel");
+    if (rc)
+      return rc;
     hipLaunchKernelGGL((bsr16_mfma_bf16_x8<kBf16Batch, kBf16Split, TO, true>),
                        dim3((unsigned)nbr, (unsigned)gy), dim3(64 * kBf16Split),
                        0, st, bro, bcol, bval, rhs, out, k, nbr);

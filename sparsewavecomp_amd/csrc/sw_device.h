@@ -25,6 +25,17 @@ typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 __device__ __forceinline__ int lane_id() { return __lane_id(); }
+// The workgroup's index in the launch and the launch's workgroup count: a
+// 1-D launch of more than 2^32 - 1 work-items is folded into an (x, y) grid
+// (one dimension's work-item count is 32 bits), numbered row by row; the
+// last row's surplus workgroups return from their kernel's index checks.
+// Both values are wave-uniform (scalar registers).
+__device__ __forceinline__ int64_t block_id() {
+  return (int64_t)blockIdx.y * gridDim.x + blockIdx.x;
+}
+__device__ __forceinline__ int64_t grid_blocks() {
+  return (int64_t)gridDim.x * gridDim.y;
+}
 // The wave's index in its workgroup, in a scalar register: it is the same in
 // every lane, but as threadIdx.x / 64 the compiler keeps it per lane and
 // makes every test and product on it a vector instruction.

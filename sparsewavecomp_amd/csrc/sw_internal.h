@@ -41,13 +41,48 @@ inline bool narrow_offsets(int64_t n, int64_t w) {
   return n >= 0 && w >= 0 && (w == 0 || n <= (int64_t)(UINT32_MAX / 4) / w);
 }
 
-// Largest grid dimension x we launch in one go.
+// Grid limits.  The dispatch packet holds each dimension's work-item count
+// in 32 bits, and a launch whose x dimension passes 2^32 - 1 work-items is
+// cut short without an error (a thread-per-position SpMM over 2^31 - 2^16
+// nonzeros at K = 4, 8.6e9 work-items, left its last rows unwritten).
+// grid_dim therefore folds a 1-D launch of `blocks` workgroups of `threads`
+// work-items into (x, y) when x alone cannot hold it; its kernels read their
+// workgroup as swd::block_id() (y * gridDim.x + x), and the up to y - 1
+// surplus workgroups of the last row return from their kernels' own index
+// checks.  Below 2^32 work-items the grid stays 1-D, as before.
 constexpr int64_t kMaxGridX = 2147483647;
+constexpr int64_t kMaxGridY = 65535;
 
-inline int check_grid(int64_t grid, const char *what) {
-  if (grid > kMaxGridX)
+// Workgroups of `threads` work-items that one grid row (x) holds.
+inline int64_t grid_row(int64_t threads) {
+  const int64_t t = threads > 0 ? threads : 1;
+  const int64_t n = (int64_t)UINT32_MAX / t;
+  return n < kMaxGridX ? n : kMaxGridX;
+}
+
+inline dim3 grid_dim(int64_t blocks, int64_t threads) {
+  const int64_t row = grid_row(threads);
+  if (blocks <= row)
+    return dim3((unsigned)blocks);
+  const int64_t gy = ceil_div(blocks, row);
+  return dim3((unsigned)ceil_div(blocks, gy), (unsigned)gy);
+}
+
+// A launch of `grid` workgroups of `threads` that grid_dim can fold.
+inline int check_grid(int64_t grid, int64_t threads, const char *what) {
+  if (grid > grid_row(threads) * kMaxGridY)
     return fail(SW_ERR_INVALID_SHAPE, "%s needs %lld workgroups, more than "
                 "one launch allows", what, (long long)grid);
+  return SW_OK;
+}
+
+// A launch whose kernel indexes its workgroups by blockIdx.x alone (a 1-D
+// grid that is never folded, or the x dimension of a 2-D one).
+inline int check_flat_grid(int64_t grid, int64_t threads, const char *what) {
+  if (grid > grid_row(threads))
+    return fail(SW_ERR_INVALID_SHAPE, "%s needs %lld workgroups of %lld "
+                "work-items, more than one grid dimension holds", what,
+                (long long)grid, (long long)threads);
   return SW_OK;
 }
 

@@ -47,7 +47,7 @@ __global__ __launch_bounds__(1024) void spmm_thread_per_output(
     const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
     const T *__restrict__ val, const T *__restrict__ rhs,
     T *__restrict__ out, int64_t rows, int64_t k) {
-  int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int64_t e = block_id() * blockDim.x + threadIdx.x;
   if (e >= rows * k)
     return;
   int64_t r = e / k, c = e - r * k;
@@ -103,14 +103,15 @@ __global__ __launch_bounds__(1024) void spmm_row_tile(
     int64_t tiles_per_row) {
   const int units_per_block = blockDim.x / G;
   const int64_t unit =
-      xcd_contiguous(blockIdx.x, gridDim.x) * units_per_block + threadIdx.x / G;
+      xcd_contiguous(block_id(), grid_blocks()) * units_per_block +
+      threadIdx.x / G;
   spmm_row_tile_unit<V, CL, G, T>(ro, col, val, rhs, out, rows, k, tile,
                                   tiles_per_row, unit, threadIdx.x & (G - 1));
 }
 
 __global__ __launch_bounds__(1024) void spmm_fill_zero(float *__restrict__ y,
                                                        int64_t n) {
-  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int64_t i = block_id() * blockDim.x + threadIdx.x;
   if (i < n)
     y[i] = 0.0f;
 }
@@ -122,7 +123,7 @@ __global__ __launch_bounds__(1024) void spmm_thread_position(
     const float *__restrict__ val, const float *__restrict__ rhs,
     float *__restrict__ out, int32_t rows, int64_t k, int64_t iterations,
     int64_t chunk) {
-  int64_t w = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int64_t w = block_id() * blockDim.x + threadIdx.x;
   int64_t b = w * chunk;
   if (b >= iterations)
     return;
@@ -156,7 +157,7 @@ __global__ __launch_bounds__(1024) void spmm_wave_position(
   constexpr int PL = kWave / CL;
   const int lane = lane_id();
   const int64_t wave =
-      (int64_t)blockIdx.x * (blockDim.x / kWave) + wave_in_group();
+      block_id() * (blockDim.x / kWave) + wave_in_group();
   if (wave >= chunks * tiles)
     return;
   const int64_t chunk = wave / tiles;
@@ -377,14 +378,14 @@ void launch_wpos(int64_t grid, int64_t B, hipStream_t st, const int32_t *ro,
   if constexpr (V == 4 && CL >= 8) {
     if (store_rows) {
       hipLaunchKernelGGL((spmm_wave_position<V, CL, P, true>),
-                         dim3((unsigned)grid), dim3((unsigned)B), 0, st, ro,
+                         sw::grid_dim(grid, B), dim3((unsigned)B), 0, st, ro,
                          col, val, rhs, out, rows, nnz, k, units, chunks,
                          tiles, vec);
       return;
     }
   }
   hipLaunchKernelGGL((spmm_wave_position<V, CL, P, false>),
-                     dim3((unsigned)grid), dim3((unsigned)B), 0, st, ro, col,
+                     sw::grid_dim(grid, B), dim3((unsigned)B), 0, st, ro, col,
                      val, rhs, out, rows, nnz, k, units, chunks, tiles, vec);
 }
 
@@ -444,7 +445,9 @@ __global__ __launch_bounds__(64 * W) void spmm_tile_mfma(
     float *__restrict__ out, int32_t rows, int64_t k) {
   constexpr int CH = 2; // 16-entry chunks per step
   __shared__ float part[W][4][4][kWave]; // [wave][n tile][v][lane]
-  const int r0 = blockIdx.x * 16;
+  if (block_id() * 16 >= rows)
+    return; // a folded grid's surplus workgroup (workgroup-uniform)
+  const int r0 = (int)block_id() * 16;
   const int nt = std::min(16, rows - r0);
   const int wave = wave_in_group();
   const int l = lane_id(), i = l & 15, g = l >> 4;
@@ -565,7 +568,9 @@ __global__ __launch_bounds__(64 * W) void spmm_tile_mfma_bf16(
     uint16_t *__restrict__ out, int32_t rows, int64_t k) {
   constexpr int CH = 2; // 16-entry chunks per step
   __shared__ float part[W][4][4][kWave]; // [wave][n tile][v][lane]
-  const int r0 = blockIdx.x * 16;
+  if (block_id() * 16 >= rows)
+    return; // a folded grid's surplus workgroup (workgroup-uniform)
+  const int r0 = (int)block_id() * 16;
   const int nt = std::min(16, rows - r0);
   const int wave = wave_in_group();
   const int l = lane_id(), i = l & 15, g = l >> 4;
@@ -677,7 +682,7 @@ __global__ __launch_bounds__(256) void spmm_row_tile_lds(
   constexpr int PL = kWave / CL, U = kLdsTileSteps;
   __shared__ v4f stage[4][U][kWave];
   const int wave = wave_in_group(), l = lane_id();
-  const int64_t unit = (int64_t)blockIdx.x * 4 + wave;
+  const int64_t unit = block_id() * 4 + wave;
   if (unit >= rows * tiles_per_row)
     return; // wave-uniform; the kernel has no workgroup barrier
   const int64_t r = unit / tiles_per_row;
@@ -746,7 +751,7 @@ __global__ __launch_bounds__(256) void spmm_row_owner(
     int64_t chunk, int64_t chunks, int64_t tiles) {
   constexpr int PL = kWave / CL;
   const int64_t wave =
-      (int64_t)blockIdx.x * (blockDim.x / kWave) + wave_in_group();
+      block_id() * (blockDim.x / kWave) + wave_in_group();
   if (wave >= chunks * tiles)
     return;
   const int64_t c = wave / tiles;
@@ -817,7 +822,7 @@ template <int V, int CL, int G, typename T>
 void launch_tile(int64_t grid, int64_t B, hipStream_t st, const int32_t *ro,
                  const int32_t *col, const T *val, const T *rhs, T *out,
                  int64_t rows, int64_t k, int32_t tile, int64_t tpr) {
-  hipLaunchKernelGGL((spmm_row_tile<V, CL, G, T>), dim3((unsigned)grid),
+  hipLaunchKernelGGL((spmm_row_tile<V, CL, G, T>), sw::grid_dim(grid, B),
                      dim3((unsigned)B), 0, st, ro, col, val, rhs, out, rows, k,
                      tile, tpr);
 }
@@ -830,8 +835,8 @@ void dispatch_g(int G, int64_t rows, int64_t tpr, int64_t B, hipStream_t st,
   int64_t units = rows * tpr;
   int64_t grid = std::max<int64_t>(sw::ceil_div(units, B / G), 1);
   *grid_out = grid;
-  if (grid > sw::kMaxGridX)
-    return;
+  if (grid > sw::grid_row(B) * sw::kMaxGridY)
+    return; // the caller's check_grid reports it
 #define SW_TILE_CASE(GG)                                                      \
   case GG:                                                                    \
     if constexpr (GG >= CL)                                                   \
@@ -882,10 +887,10 @@ bool launch_spmm_rows(const int32_t *ro, const int32_t *col, const T *val,
   };
   if (streq(o.spmm_mapping, "thread-per-output")) {
     int64_t grid = std::max<int64_t>(ceil_div(rows * k, B), 1);
-    *rc = check_grid(grid, what);
+    *rc = check_grid(grid, B, what);
     if (*rc)
       return true;
-    dim3 g((unsigned)grid), b((unsigned)B);
+    dim3 g = grid_dim(grid, B), b((unsigned)B);
     const bool row = k % kWave == 0 && B % kWave == 0 && rows <= INT32_MAX;
     if (narrow_offsets(rhs_rows, k) && row)
       hipLaunchKernelGGL((spmm_thread_per_output<true, true, T>), g, b, 0, st,
@@ -906,20 +911,20 @@ bool launch_spmm_rows(const int32_t *ro, const int32_t *col, const T *val,
     int64_t grid = ceil_div(rows, 16);
     if constexpr (sizeof(T) == 4) {
       if (k % 16 == 0) {
-        *rc = check_grid(grid, what);
+        *rc = check_grid(grid, 512, what);
         if (*rc)
           return true;
-        hipLaunchKernelGGL(spmm_tile_mfma<8>, dim3((unsigned)grid), dim3(512),
+        hipLaunchKernelGGL(spmm_tile_mfma<8>, grid_dim(grid, 512), dim3(512),
                            0, st, ro, col, val, rhs, out, (int32_t)rows, k);
         *rc = launch_check("SpMM tile MFMA kernel");
         return true;
       }
     } else {
       if (k % 64 == 0 && vec_ok(rhs) && vec_ok(out)) {
-        *rc = check_grid(grid, what);
+        *rc = check_grid(grid, 512, what);
         if (*rc)
           return true;
-        hipLaunchKernelGGL(spmm_tile_mfma_bf16<8>, dim3((unsigned)grid),
+        hipLaunchKernelGGL(spmm_tile_mfma_bf16<8>, grid_dim(grid, 512),
                            dim3(512), 0, st, ro, col, val, rhs, out,
                            (int32_t)rows, k);
         *rc = launch_check("SpMM tile MFMA kernel");
@@ -937,12 +942,12 @@ bool launch_spmm_rows(const int32_t *ro, const int32_t *col, const T *val,
     // the kernel is compiled for at most 256 threads per workgroup
     const int64_t OB = std::min<int64_t>(B, 256);
     const int64_t grid = ceil_div(chunks * tiles, OB / 64);
-    *rc = check_grid(grid, what);
+    *rc = check_grid(grid, OB, what);
     if (*rc)
       return true;
 #define SW_OWNER(CC)                                                          \
   case CC:                                                                    \
-    hipLaunchKernelGGL((spmm_row_owner<CC, T>), dim3((unsigned)grid),         \
+    hipLaunchKernelGGL((spmm_row_owner<CC, T>), grid_dim(grid, OB),           \
                        dim3((unsigned)OB), 0, st, ro, col, val, rhs, out,     \
                        (int32_t)rows, (int32_t)nnz, k, chunk, chunks, tiles); \
     break;
@@ -959,13 +964,13 @@ bool launch_spmm_rows(const int32_t *ro, const int32_t *col, const T *val,
         Tt % 4 == 0 && aligned16(rhs) && aligned16(out)) {
       const int64_t tpr = ceil_div(k, Tt);
       const int64_t grid = std::max<int64_t>(ceil_div(rows * tpr, 4), 1);
-      *rc = check_grid(grid, what);
+      *rc = check_grid(grid, 256, what);
       if (*rc)
         return true;
       const int CL = next_pow2((int)(Tt / 4));
 #define SW_LDS_TILE(CC)                                                       \
   case CC:                                                                    \
-    hipLaunchKernelGGL(spmm_row_tile_lds<CC>, dim3((unsigned)grid),           \
+    hipLaunchKernelGGL(spmm_row_tile_lds<CC>, grid_dim(grid, 256),            \
                        dim3(256), 0, st, ro, col, val, rhs, out, rows, k,     \
                        (int32_t)Tt, tpr);                                     \
     break;
@@ -1009,7 +1014,7 @@ bool launch_spmm_rows(const int32_t *ro, const int32_t *col, const T *val,
                "no wave-per-row-tile kernel for tile size %d", T_);
     return true;
   }
-  *rc = check_grid(grid, what);
+  *rc = check_grid(grid, B, what);
   if (*rc)
     return true;
   *rc = launch_check("wave-per-row-tile SpMM kernel");
@@ -1029,10 +1034,10 @@ int launch_spmm(const int32_t *ro, const int32_t *col, const float *val,
     int64_t n_out = rows * k;
     if (n_out > 0) {
       int64_t g0 = ceil_div(n_out, o.position_block_size);
-      int rc = check_grid(g0, what);
+      int rc = check_grid(g0, o.position_block_size, what);
       if (rc)
         return rc;
-      hipLaunchKernelGGL(spmm_fill_zero, dim3((unsigned)g0),
+      hipLaunchKernelGGL(spmm_fill_zero, grid_dim(g0, o.position_block_size),
                          dim3((unsigned)o.position_block_size), 0, st, out,
                          n_out);
       rc = launch_check("SpMM output initialisation kernel");
@@ -1044,10 +1049,10 @@ int launch_spmm(const int32_t *ro, const int32_t *col, const float *val,
       return SW_OK;
     int64_t chunk = o.spmm_position_chunk_size;
     int64_t grid = std::max<int64_t>(ceil_div(ceil_div(iters, chunk), B), 1);
-    int rc = check_grid(grid, what);
+    int rc = check_grid(grid, B, what);
     if (rc)
       return rc;
-    hipLaunchKernelGGL(spmm_thread_position, dim3((unsigned)grid),
+    hipLaunchKernelGGL(spmm_thread_position, grid_dim(grid, B),
                        dim3((unsigned)B), 0, st, ro, col, val, rhs, out,
                        (int32_t)rows, k, iters, chunk);
     return launch_check("thread-per-position SpMM kernel");
@@ -1065,7 +1070,7 @@ int launch_spmm(const int32_t *ro, const int32_t *col, const float *val,
     const int64_t chunks = ceil_div(units, PL);
     const int64_t tiles = ceil_div(k, (int64_t)CL * V);
     const int64_t grid = ceil_div(chunks * tiles, B / 64);
-    int rc = check_grid(grid, what);
+    int rc = check_grid(grid, B, what);
     if (rc)
       return rc;
     // rows of at least one 128-byte line are stored; narrower rows go

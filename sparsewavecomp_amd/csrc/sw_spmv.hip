@@ -96,7 +96,7 @@ __global__ __launch_bounds__(1024) void spmv_thread_per_row(
     const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
     const float *__restrict__ val, const float *__restrict__ x,
     float *__restrict__ y, int32_t rows) {
-  int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int64_t r = block_id() * blockDim.x + threadIdx.x;
   if (r >= rows)
     return;
   int32_t s = ro[r], e = ro[r + 1];
@@ -116,7 +116,7 @@ __global__ __launch_bounds__(1024) void spmv_group_per_row(
     const float *__restrict__ val, const float *__restrict__ x,
     float *__restrict__ y, int32_t rows) {
   const int groups_per_block = blockDim.x / G;
-  int64_t r = (int64_t)blockIdx.x * groups_per_block + threadIdx.x / G;
+  int64_t r = block_id() * groups_per_block + threadIdx.x / G;
   const int gl = threadIdx.x & (G - 1);
   float acc = 0.0f;
   if (r < rows) {
@@ -139,7 +139,7 @@ __global__ __launch_bounds__(1024) void spmv_block_per_row(
     const float *__restrict__ val, const float *__restrict__ x,
     float *__restrict__ y, int32_t rows) {
   __shared__ float partial[1024 / kWave];
-  const int64_t r = blockIdx.x;
+  const int64_t r = block_id();
   const int t = threadIdx.x;
   const int B = blockDim.x;
   if (r >= rows)
@@ -182,7 +182,7 @@ __global__ __launch_bounds__(1024) void spmv_block_per_row(
 // output is 16-byte aligned).
 __global__ __launch_bounds__(1024) void fill_zero_f32(float *__restrict__ y,
                                                       int64_t n) {
-  int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  int64_t i = (block_id() * blockDim.x + threadIdx.x) * 4;
   if (i + 4 <= n && (reinterpret_cast<uintptr_t>(y) & 15u) == 0) {
     *reinterpret_cast<v4f *>(y + i) = v4f{0.f, 0.f, 0.f, 0.f};
   } else {
@@ -215,7 +215,7 @@ __device__ __forceinline__ int64_t wave_of_position(int64_t p, int64_t chunk,
 __global__ __launch_bounds__(256) void position_init(
     const int32_t *__restrict__ ro, float *__restrict__ out, int32_t rows,
     int64_t k, int64_t chunk, int64_t P, int64_t units, int64_t waves) {
-  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t r = block_id() * blockDim.x + threadIdx.x;
   if (r >= rows)
     return;
   const int32_t s = ro[r], e = ro[r + 1];
@@ -243,7 +243,7 @@ struct WaveRows {
 __device__ __forceinline__ WaveRows wave_rows(const int32_t *__restrict__ ro,
                                               int32_t rows, int64_t nnz,
                                               int64_t chunk) {
-  const int64_t first = ((int64_t)blockIdx.x * blockDim.x +
+  const int64_t first = (block_id() * blockDim.x +
                          (int64_t)wave_in_group() * kWave) *
                         chunk;
   const int64_t last = std::min(first + (int64_t)kWave * chunk, nnz) - 1;
@@ -263,9 +263,9 @@ __global__ __launch_bounds__(1024) void spmv_thread_position_atomic(
     const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
     const float *__restrict__ val, const float *__restrict__ x,
     float *__restrict__ y, int32_t rows, int32_t nnz, int32_t chunk) {
-  const int64_t w = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t w = block_id() * blockDim.x + threadIdx.x;
   const int64_t b = w * chunk;
-  if ((((int64_t)blockIdx.x * blockDim.x + (int64_t)wave_in_group() * kWave) *
+  if (((block_id() * blockDim.x + (int64_t)wave_in_group() * kWave) *
        chunk) >= nnz)
     return; // wave-uniform: the whole wave is past the positions
   const WaveRows wr = wave_rows(ro, rows, nnz, chunk);
@@ -288,7 +288,7 @@ __global__ __launch_bounds__(1024) void spmv_thread_position_segmented(
     float *__restrict__ y, int32_t rows, int32_t nnz, int32_t chunk) {
   // (the chunk's own search over all row offsets: the wave-range form of
   // the atomic kernel measured 562 -> 596 us here, configuration 2, chunk 8)
-  int64_t w = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int64_t w = block_id() * blockDim.x + threadIdx.x;
   int64_t b = w * chunk;
   if (b >= nnz)
     return;
@@ -339,7 +339,7 @@ __global__ __launch_bounds__(1024) void spmv_wave_position(
     int64_t wave_count) {
   const int lane = lane_id();
   const int64_t wave =
-      (int64_t)blockIdx.x * (blockDim.x / kWave) + wave_in_group();
+      block_id() * (blockDim.x / kWave) + wave_in_group();
   const uint64_t base = (uint64_t)units / (uint64_t)wave_count;
   const uint64_t rem = (uint64_t)units % (uint64_t)wave_count;
   const uint64_t wv = (uint64_t)wave;
@@ -699,7 +699,7 @@ __global__ __launch_bounds__(256) void spmv_row_owner(
     float *__restrict__ y, int32_t rows, int32_t nnz, int64_t chunk,
     int64_t waves) {
   const int64_t wave =
-      xcd_contiguous(blockIdx.x, gridDim.x) * (blockDim.x / kWave) +
+      xcd_contiguous(block_id(), grid_blocks()) * (blockDim.x / kWave) +
       wave_in_group();
   if (wave >= waves)
     return; // wave-uniform
@@ -730,7 +730,7 @@ __global__ __launch_bounds__(1024) void spmv_thread_per_row_waves(
     const int32_t *__restrict__ ro, const int32_t *__restrict__ col,
     const float *__restrict__ val, const float *__restrict__ x,
     float *__restrict__ y, int32_t rows, int32_t nnz) {
-  const int64_t r0 = (int64_t)blockIdx.x * blockDim.x +
+  const int64_t r0 = block_id() * blockDim.x +
                      (int64_t)wave_in_group() * kWave;
   if (r0 >= rows)
     return; // wave-uniform
@@ -806,7 +806,7 @@ __global__ __launch_bounds__(256) void csr_row_at_position_kernel(
     const int32_t *__restrict__ ro, int32_t rows,
     const int64_t *__restrict__ pos, int32_t *__restrict__ out,
     int64_t count) {
-  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int64_t i = block_id() * blockDim.x + threadIdx.x;
   if (i < count)
     out[i] = row_search_lane(ro, 1u, (uint32_t)rows + 1u, (int32_t)pos[i]);
 }
@@ -823,7 +823,7 @@ __global__ __launch_bounds__(1024) void coo_thread_per_nonzero(
     const int32_t *__restrict__ ri, const int32_t *__restrict__ col,
     const float *__restrict__ val, const float *__restrict__ x,
     float *__restrict__ y, int64_t nnz) {
-  const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t p = block_id() * blockDim.x + threadIdx.x;
   if (p < nnz)
     unsafeAtomicAdd(y + ld_nontemporal(ri + p),
                     ld_nontemporal(val + p) * x[ld_nontemporal(col + p)]);
@@ -842,7 +842,7 @@ __global__ __launch_bounds__(1024) void coo_run_segmented(
     const int32_t *__restrict__ ri, const int32_t *__restrict__ col,
     const float *__restrict__ val, const float *__restrict__ x,
     float *__restrict__ y, int64_t nnz) {
-  const int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t u = block_id() * blockDim.x + threadIdx.x;
   const int64_t p0 = u * P;
   const bool active = p0 < nnz;
   const int n = active ? (int)(nnz - p0 < P ? nnz - p0 : P) : 0;
@@ -928,7 +928,7 @@ template <int P, bool VEC>
 void launch_coo_runs(int64_t grid, int64_t B, hipStream_t st,
                      const int32_t *ri, const int32_t *col, const float *val,
                      const float *x, float *y, int64_t nnz) {
-  hipLaunchKernelGGL((coo_run_segmented<P, VEC>), dim3((unsigned)grid),
+  hipLaunchKernelGGL((coo_run_segmented<P, VEC>), sw::grid_dim(grid, B),
                      dim3((unsigned)B), 0, st, ri, col, val, x, y, nnz);
 }
 
@@ -978,10 +978,10 @@ int launch_fill_zero(float *y, int64_t n, int64_t block, hipStream_t st) {
   // kernel's block size (64-lane groups measured 5.2 us for 4 MB)
   block = std::max<int64_t>(block, 256);
   int64_t grid = ceil_div(ceil_div(n, 4), block);
-  int rc = check_grid(grid, "output initialisation");
+  int rc = check_grid(grid, block, "output initialisation");
   if (rc)
     return rc;
-  hipLaunchKernelGGL(fill_zero_f32, dim3((unsigned)grid), dim3((unsigned)block),
+  hipLaunchKernelGGL(fill_zero_f32, grid_dim(grid, block), dim3((unsigned)block),
                      0, st, y, n);
   return launch_check("output initialisation kernel");
 }
@@ -992,10 +992,10 @@ int launch_position_init(const int32_t *ro, float *out, int64_t rows,
   if (rows <= 0 || k <= 0)
     return SW_OK;
   int64_t grid = ceil_div(rows, 256);
-  int rc = check_grid(grid, "output initialisation");
+  int rc = check_grid(grid, 256, "output initialisation");
   if (rc)
     return rc;
-  hipLaunchKernelGGL(position_init, dim3((unsigned)grid), dim3(256), 0, st,
+  hipLaunchKernelGGL(position_init, grid_dim(grid, 256), dim3(256), 0, st,
                      ro, out, (int32_t)rows, k, chunk, P,
                      std::max<int64_t>(units, 1), std::max<int64_t>(waves, 1));
   return launch_check("position output initialisation kernel");
@@ -1009,7 +1009,10 @@ int launch_spmv(const int32_t *ro, const int32_t *col, const float *val,
   const bool narrow = narrow_offsets(cols, 1);
   if (streq(o.spmv_mapping, "thread-per-row")) {
     int64_t grid = std::max<int64_t>(ceil_div(rows, B), 1);
-    dim3 g((unsigned)grid), b((unsigned)B);
+    int rc = check_grid(grid, B, "thread-per-row SpMV");
+    if (rc)
+      return rc;
+    dim3 g = grid_dim(grid, B), b((unsigned)B);
     // whole-wave workgroups: uneven waves take their 64 rows together
     // (configuration 2, 256-thread blocks: 438 -> 269 us)
     if (B % kWave == 0) {
@@ -1037,10 +1040,10 @@ int launch_spmv(const int32_t *ro, const int32_t *col, const float *val,
   if (streq(o.spmv_mapping, "wave-per-row")) {
     const int64_t G = o.spmv_lanes_per_row;
     int64_t grid = std::max<int64_t>(ceil_div(rows, B / G), 1);
-    int rc = check_grid(grid, "wave-per-row SpMV");
+    int rc = check_grid(grid, B, "wave-per-row SpMV");
     if (rc)
       return rc;
-    dim3 g((unsigned)grid), b((unsigned)B);
+    dim3 g = grid_dim(grid, B), b((unsigned)B);
     switch (G) {
     case 1: launch_group<1>(g, b, st, ro, col, val, x, y, n, narrow); break;
     case 2: launch_group<2>(g, b, st, ro, col, val, x, y, n, narrow); break;
@@ -1054,10 +1057,10 @@ int launch_spmv(const int32_t *ro, const int32_t *col, const float *val,
   }
   if (streq(o.spmv_mapping, "block-per-row")) {
     int64_t grid = std::max<int64_t>(rows, 1);
-    int rc = check_grid(grid, "block-per-row SpMV");
+    int rc = check_grid(grid, B, "block-per-row SpMV");
     if (rc)
       return rc;
-    dim3 g((unsigned)grid), b((unsigned)B);
+    dim3 g = grid_dim(grid, B), b((unsigned)B);
     if (narrow)
       hipLaunchKernelGGL(spmv_block_per_row<true>, g, b, 0, st, ro, col, val,
                          x, y, n);
@@ -1077,15 +1080,15 @@ int launch_spmv(const int32_t *ro, const int32_t *col, const float *val,
     const int64_t chunk = o.spmv_position_chunk_size;
     int64_t workers = ceil_div(nnz, chunk);
     int64_t grid = std::max<int64_t>(ceil_div(workers, B), 1);
-    rc = check_grid(grid, "thread-per-position SpMV");
+    rc = check_grid(grid, B, "thread-per-position SpMV");
     if (rc)
       return rc;
     if (streq(o.spmv_position_reduction, "segmented"))
-      hipLaunchKernelGGL(spmv_thread_position_segmented, dim3((unsigned)grid),
+      hipLaunchKernelGGL(spmv_thread_position_segmented, grid_dim(grid, B),
                          dim3((unsigned)B), 0, st, ro, col, val, x, y, n,
                          (int32_t)nnz, (int32_t)std::min<int64_t>(chunk, nnz));
     else
-      hipLaunchKernelGGL(spmv_thread_position_atomic, dim3((unsigned)grid),
+      hipLaunchKernelGGL(spmv_thread_position_atomic, grid_dim(grid, B),
                          dim3((unsigned)B), 0, st, ro, col, val, x, y, n,
                          (int32_t)nnz, (int32_t)std::min<int64_t>(chunk, nnz));
     return launch_check("thread-per-position SpMV kernel");
@@ -1099,12 +1102,12 @@ int launch_spmv(const int32_t *ro, const int32_t *col, const float *val,
     // the kernel is compiled for at most 256 threads per workgroup
     const int64_t OB = std::min<int64_t>(B, 256);
     const int64_t grid = ceil_div(waves, OB / kWave);
-    rc = check_grid(grid, "wave-per-row-balanced SpMV");
+    rc = check_grid(grid, OB, "wave-per-row-balanced SpMV");
     if (rc)
       return rc;
     const bool vec = aligned16(col) && aligned16(val) && narrow &&
                      narrow_offsets(nnz, 1);
-    dim3 g((unsigned)grid), b((unsigned)OB);
+    dim3 g = grid_dim(grid, OB), b((unsigned)OB);
     const int32_t z = (int32_t)nnz;
     switch (P) {
     case 1: launch_row_owner<1, false>(g, b, st, ro, col, val, x, y, n, z, chunk, waves); break;
@@ -1128,7 +1131,7 @@ int launch_spmv(const int32_t *ro, const int32_t *col, const float *val,
   const int64_t P = o.spmv_positions_per_lane;
   const int64_t units = ceil_div(nnz, P);
   const int64_t grid = std::max<int64_t>(ceil_div(units, B), 1);
-  rc = check_grid(grid, "wave-per-position SpMV");
+  rc = check_grid(grid, B, "wave-per-position SpMV");
   if (rc)
     return rc;
   const int64_t waves = grid * (B / 64);
@@ -1139,7 +1142,7 @@ int launch_spmv(const int32_t *ro, const int32_t *col, const float *val,
     return SW_OK;
   const bool vec = aligned16(col) && aligned16(val) && narrow &&
                    narrow_offsets(nnz, 1);
-  dim3 g((unsigned)grid), b((unsigned)B);
+  dim3 g = grid_dim(grid, B), b((unsigned)B);
   const int32_t z = (int32_t)nnz;
   switch (P) {
   case 1: launch_wave_position<1, false>(g, b, st, ro, col, val, x, y, n, z, units, waves); break;
@@ -1170,7 +1173,7 @@ int launch_spmv_coo(const int32_t *ri, const int32_t *col, const float *val,
   if (streq(o.spmv_mapping, "wave-per-position")) {
     const int64_t P = o.spmv_positions_per_lane;
     const int64_t grid = std::max<int64_t>(ceil_div(ceil_div(nnz, P), B), 1);
-    rc = check_grid(grid, "run-segmented COO SpMV");
+    rc = check_grid(grid, B, "run-segmented COO SpMV");
     if (rc)
       return rc;
     const bool vec = aligned16(ri) && aligned16(col) && aligned16(val) &&
@@ -1194,10 +1197,10 @@ int launch_spmv_coo(const int32_t *ri, const int32_t *col, const float *val,
     return launch_check("run-segmented COO SpMV kernel");
   }
   const int64_t grid = std::max<int64_t>(ceil_div(nnz, B), 1);
-  rc = check_grid(grid, "thread-per-nonzero COO SpMV");
+  rc = check_grid(grid, B, "thread-per-nonzero COO SpMV");
   if (rc)
     return rc;
-  hipLaunchKernelGGL(coo_thread_per_nonzero, dim3((unsigned)grid),
+  hipLaunchKernelGGL(coo_thread_per_nonzero, grid_dim(grid, B),
                      dim3((unsigned)B), 0, st, ri, col, val, x, y, nnz);
   return launch_check("thread-per-nonzero COO SpMV kernel");
 }
@@ -1243,7 +1246,7 @@ extern "C" int sw_spmv_gather_floor_f32(const int32_t *column_indices,
     return sw::fail(SW_ERR_INVALID_ARGUMENT,
                     "column index, value, vector or partial pointer is null");
   const int64_t grid = sw::ceil_div(sw::ceil_div(nnz, kFloorUnit), kWave);
-  int rc = sw::check_grid(grid, "gather floor");
+  int rc = sw::check_flat_grid(grid, kWave, "gather floor");
   if (rc)
     return rc;
   const bool vec = sw::aligned16(column_indices) && sw::aligned16(values);
@@ -1298,10 +1301,10 @@ extern "C" int sw_csr_row_at_position(const int32_t *row_offsets, int64_t rows,
   if (!row_offsets || !positions || !out_rows)
     return sw::fail(SW_ERR_INVALID_ARGUMENT, "null pointer");
   int64_t grid = sw::ceil_div(count, 256);
-  int rc = sw::check_grid(grid, "row recovery");
+  int rc = sw::check_grid(grid, 256, "row recovery");
   if (rc)
     return rc;
-  hipLaunchKernelGGL(csr_row_at_position_kernel, dim3((unsigned)grid),
+  hipLaunchKernelGGL(csr_row_at_position_kernel, sw::grid_dim(grid, 256),
                      dim3(256), 0, sw::as_stream(stream), row_offsets,
                      (int32_t)rows, positions, out_rows, count);
   return sw::launch_check("row recovery kernel");
