@@ -76,6 +76,11 @@ class Bundle:
         items = evaluate_grid(k["grid"][0], n)
         block = k["block"][0]
         assert items % block == 0 and k["block"][1:] == [1, 1]
+        # the manifest's grid is 1-D, and a dispatch holds at most 2^32 - 1
+        # work-items per dimension (a larger one would be cut short)
+        if items > 0xFFFFFFFF:
+            raise ValueError(f"{name}: {items} work-items for n = {n} pass "
+                             "the 2^32 - 1 one grid dimension holds")
         args = bytearray(k["kernarg_size"])
         for a in k["args"]:
             assert a["type"] == "ptr" and a["size"] == 8
