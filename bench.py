@@ -643,8 +643,8 @@ def main():
             res1[opts] = {"us": ms * 1e3, "graph_replay_us": gms * 1e3}
         if not args.no_cpu:
             # the reference's CPU path on the same matrix, beside the GPU
-            # mappings ("correctness + CPU
-            # comparison"): the oracle's scalar restatement of
+            # mappings (configuration 1 is the CPU-comparison case): the
+            # oracle's scalar restatement of
             # benchmark/SparseBenchmarkUtils.cpp:211-229, one thread,
             # median of at least 5 passes
             import oracle
