@@ -142,3 +142,27 @@ def test_row_ops_rows_past_one_grid_dimension(many_rows):
     # every entry the same value, expf(1) within an ulp of e
     assert torch.equal(out, out[:1].expand_as(out))
     assert abs(float(out[0]) - 2.718281828459045) <= 2.4e-7
+
+
+@pytest.mark.parametrize("opts", [
+    "spmm-mapping=thread-per-output",
+    "spmm-mapping=wave-per-row-tile spmm-tile-size=4 spmm-block-size=64",
+])
+def test_bf16_spmm_at_the_nnz_limit(big, opts):
+    """The bf16 SpMM (every value buffer bf16, fp32 sums, one rounding) at
+    the nnz cap: row lengths 1023 and 1024 both round to 1024 in bf16 (8
+    significant bits), the empty last row to 0."""
+    ro, col, _, want = big
+    k = 4
+    val = torch.ones(LIMIT, dtype=torch.bfloat16, device=G.DEV)
+    rhs = torch.ones((COLS, k), dtype=torch.bfloat16, device=G.DEV)
+    G.say(f"bf16 spmm nnz={LIMIT} rows={ROWS} k={k} opts='{opts}'")
+    out = torch.full((ROWS, k), float("nan"), dtype=torch.bfloat16,
+                     device=G.DEV)
+    sw.spmm(ro, col, val, rhs, out, options=opts)
+    torch.cuda.synchronize()
+    expect = want.to(torch.bfloat16)[:, None].expand(ROWS, k)
+    assert float(expect[0, 0]) == 1024.0 and float(expect[-1, 0]) == 0.0
+    assert torch.equal(out, expect)
+    del val
+    torch.cuda.empty_cache()
