@@ -14,11 +14,14 @@
 2. Rows past one grid dimension: 2^26 + 2^20 rows put wave-per-row and
    block-per-row SpMV (64 work-items per row) and the wave row reduction and
    row-wise map past 2^32 - 1 work-items too.
+3. COO past 2^31 entries (coo_spmv has no nnz cap: each entry carries its
+   row), through the reference's kernel and the run-segmented one.
 
 Values, x and the right-hand sides are ones (the map's row values zero), so
 every product output is a row length, exact in fp32, and every mapping must
-reproduce it bit for bit; the map gives one value, exp(1), at every entry.  The first case holds about 17 GiB of device
-memory, the second about 1 GiB.
+reproduce it bit for bit; the map gives one value, exp(1), at every entry.
+Device memory: about 17 GiB for the first case (25 GiB with the bf16 SpMM),
+1 GiB for the second, 43 GiB at the peak of the third.
 """
 import pytest
 import torch
@@ -165,4 +168,31 @@ def test_bf16_spmm_at_the_nnz_limit(big, opts):
     assert float(expect[0, 0]) == 1024.0 and float(expect[-1, 0]) == 0.0
     assert torch.equal(out, expect)
     del val
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("opts", [
+    None,  # the reference's thread-per-nonzero kernel
+    "spmv-mapping=wave-per-position spmv-positions-per-lane=4 "
+    "spmv-block-size=64",
+])
+def test_coo_past_two_to_the_31_entries(dev, opts):
+    """COO entries carry their row, so coo_spmv has no nnz cap: 2^31 + 2^20
+    row-sorted entries (rows of 1024, past every 32-bit position), their
+    positions and byte offsets 64-bit in both kernels.  Values and x are
+    ones: each row sums to 1024 exactly."""
+    nnz = (1 << 31) + (1 << 20)
+    rows = nnz // 1024
+    p = torch.arange(nnz, dtype=torch.int64, device=G.DEV)
+    ri = torch.div(p, 1024, rounding_mode="floor").to(torch.int32)
+    col = p.remainder_(COLS).to(torch.int32)
+    del p
+    val = torch.ones(nnz, dtype=torch.float32, device=G.DEV)
+    x = torch.ones(COLS, dtype=torch.float32, device=G.DEV)
+    G.say(f"coo nnz={nnz} rows={rows} opts='{opts}'")
+    y = torch.full((rows,), float("nan"), device=G.DEV)
+    sw.coo_spmv(ri, col, val, x, y, options=opts)
+    torch.cuda.synchronize()
+    assert torch.equal(y, torch.full_like(y, 1024.0))
+    del ri, col, val
     torch.cuda.empty_cache()
