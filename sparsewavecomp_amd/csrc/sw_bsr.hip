@@ -532,6 +532,12 @@ int launch_bsr(const int32_t *bro, const int32_t *bcol, const T *bval,
   if (rows == 0 || k == 0)
     return SW_OK;
   const int nbr = (int)(rows / 16);
+  // The matrix-core kernels index block rows by blockIdx.x alone (y holds
+  // the column strips), so their x must stay within one grid dimension's
+  // 2^32 - 1 work-items (512-work-item workgroups: about 8.4 million block
+  // rows); past it the thread-per-output kernel below, whose launch folds,
+  // computes the product.
+  mfma_ok = mfma_ok && nbr <= sw::grid_row(512);
   if constexpr (sizeof(T) == 4) {
     // fp32 with k % 4 == 0 takes the column-interleaved kernel (measured on
     // configuration 4: 167 us against 189 us for the one-column-per-lane

@@ -16,12 +16,15 @@
    row-wise map past 2^32 - 1 work-items too.
 3. COO past 2^31 entries (coo_spmv has no nnz cap: each entry carries its
    row), through the reference's kernel and the run-segmented one.
+4. BSR past 8.4 million block rows, where the matrix-core kernels' 1-D x
+   ends and the thread-per-output kernel takes over (fp32 and bf16).
 
 Values, x and the right-hand sides are ones (the map's row values zero), so
 every product output is a row length, exact in fp32, and every mapping must
 reproduce it bit for bit; the map gives one value, exp(1), at every entry.
 Device memory: about 17 GiB for the first case (25 GiB with the bf16 SpMM),
-1 GiB for the second, 43 GiB at the peak of the third.
+1 GiB for the second, 43 GiB at the peak of the third, 13 GiB for the
+fourth.
 """
 import pytest
 import torch
@@ -195,4 +198,27 @@ def test_coo_past_two_to_the_31_entries(dev, opts):
     torch.cuda.synchronize()
     assert torch.equal(y, torch.full_like(y, 1024.0))
     del ri, col, val
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+def test_bsr_block_rows_past_the_matrix_core_grid(dev, dt):
+    """The BSR matrix-core kernels index block rows by blockIdx.x alone, so
+    past 2^32 - 1 work-items in x (about 8.4 million block rows) the BSR
+    SpMM takes its thread-per-output kernel, whose launch folds.  Here
+    2^23 + 2^16 block rows of one 16 x 16 block of ones on the diagonal,
+    times a right-hand side of ones (K = 4): every output is 16, exact in
+    fp32 and in bf16."""
+    nbr = (1 << 23) + (1 << 16)
+    rows, k = nbr * 16, 4
+    bro = torch.arange(nbr + 1, dtype=torch.int32, device=G.DEV)
+    bcol = torch.arange(nbr, dtype=torch.int32, device=G.DEV)
+    bval = torch.ones(nbr * 256, dtype=dt, device=G.DEV)
+    rhs = torch.ones((rows, k), dtype=dt, device=G.DEV)
+    out = torch.full((rows, k), float("nan"), dtype=dt, device=G.DEV)
+    G.say(f"bsr block rows={nbr} dtype={dt}")
+    sw.bsr_spmm(bro, bcol, bval, rhs, out, block_size=16)
+    torch.cuda.synchronize()
+    assert torch.equal(out, torch.full_like(out, 16.0))
+    del bval, rhs, out
     torch.cuda.empty_cache()
