@@ -21,6 +21,13 @@
  * fp32 accumulation is the more accurate choice and parity with the fp32
  * path is tolerance-based (rel-L2 <= 1e-2).
  *
+ * Sizes: CSR operands take nnz <= INT32_MAX - 65536 and rows <= INT32_MAX - 1
+ * (larger: SW_ERR_INVALID_SHAPE before any launch); COO takes any nnz.
+ * Every mapping runs at those limits: a launch of more than 2^32 - 1
+ * work-items, which one grid dimension cannot hold, is folded into a 2-D
+ * grid, and the BSR SpMM past about 8.4 million block rows computes with
+ * its thread-per-output kernel.
+ *
  * Citations are path:line into the reference (sott0n/SparseWaveComp).
  */
 #ifndef SPARSEWAVE_AMD_H
